@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""North-star benchmark: chunk_gla forward + backward, B=4 T=8192 H=16 K=V=128, bf16,
+chunk 64, h0 and dht (its headline metric).
+
+One step = chunk_gla forward (o, ht) + backward (dq, dk, dv, dg, dh0) on synthetic inputs
+already resident in HBM (numpy default_rng(seed=4), draw order
+q, k, v, g_raw, h0, do, dht; g = logsigmoid(g_raw) / 16; h0, dht ~ N(0, 0.1^2)).
+
+Prints ONE JSON line with the driver's fields plus
+  roofline     : the dominant kernel of a step (largest share of its time), timed alone on
+                 torch's current stream (the stream the C ABI launches on) with HIP events,
+                 against the HBM roofline with its algorithmic bytes per launch;
+  cpu_baseline : the numpy oracle (float32, one thread) on a bounded sample of the same
+                 workload (1 batch row, 8 of the 16 heads, full T), scaled to tokens/s of
+                 the whole workload;
+  kernels      : every kernel's average duration and achieved GB/s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "pallas-kernel_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+B, T, H, K, V, C = 4, 8192, 16, 128, 128, 64
+SEED = 4
+METRIC = "chunk_gla fwd+bwd tokens/s & % bf16 MFMA peak, B4 T8192 H16 K=V=128"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK = 2.517e15
+# algorithmic flops per token-head: fwd 4KV + 2C(K+V), bwd twice that
+FLOPS_STEP = B * T * H * (12 * K * V + 6 * C * (K + V))
+# state traffic (h/dht fp32) counted once per use
+STATE_BYTES = B * H * K * V * 4
+BF = 2  # bf16 bytes
+
+
+def _inputs(device):
+    import numpy as np
+    import torch
+
+    r = np.random.default_rng(SEED)
+    f = np.float32
+    q = r.standard_normal((B, T, H, K), dtype=f)
+    k = r.standard_normal((B, T, H, K), dtype=f)
+    v = r.standard_normal((B, T, H, V), dtype=f)
+    graw = r.standard_normal((B, T, H, K), dtype=f)
+    h0 = r.standard_normal((B, H, K, V), dtype=f) * 0.1
+    do = r.standard_normal((B, T, H, V), dtype=f)
+    dht = r.standard_normal((B, H, K, V), dtype=f) * 0.1
+    g = (-np.logaddexp(0, -graw) / 16).astype(f)
+    bf = lambda x: torch.from_numpy(x).to(device).to(torch.bfloat16)  # noqa: E731
+    fp = lambda x: torch.from_numpy(x).to(device)  # noqa: E731
+    return dict(q=bf(q), k=bf(k), v=bf(v), g=bf(g), h0=fp(h0), do=bf(do), dht=fp(dht))
+
+
+def _kernel_profile(x, reps=10):
+    """Average duration of each kernel of a step, each launched alone through the C ABI."""
+    import torch
+
+    from tops import _lib
+    from tops._lib import SeqLayout, call, ptr, stream_of
+
+    dev = x["q"].device
+    seq = SeqLayout(B, T, C, None, dev)
+    st = stream_of(dev)
+    sc = K ** -0.5
+    bf = _lib.BF16
+    h = torch.empty(seq.NC, H, K, V, dtype=torch.bfloat16, device=dev)
+    dh = torch.empty_like(h)
+    o, dq, dk, dv, dg = (torch.empty_like(x[n]) for n in ("v", "q", "k", "v", "g"))
+    ht, dh0 = torch.empty_like(x["h0"]), torch.empty_like(x["h0"])
+    q, k, v, g, h0, do, dht = (x[n] for n in ("q", "k", "v", "g", "h0", "do", "dht"))
+    lay = (B, T, H, K, V, C, *seq.args(), bf, st)
+    tok = B * T * H
+    hbytes = seq.NC * H * K * V * BF
+    kernels = {
+        "state_scan_fwd": (lambda: call("tops_gla_chunk_fwd_h", ptr(k), ptr(v), ptr(g), 0,
+                                        ptr(h0), ptr(h), ptr(ht), *lay),
+                           tok * (2 * K + V) * BF + STATE_BYTES * 2 + hbytes),
+        "chunk_fwd_o": (lambda: call("tops_gla_chunk_fwd_o", ptr(q), ptr(k), ptr(v), ptr(g), 0,
+                                     ptr(h), None, None, ptr(o), sc, *lay),
+                        tok * (3 * K + 2 * V) * BF + hbytes),
+        "state_scan_bwd": (lambda: call("tops_gla_chunk_bwd_dh", ptr(q), ptr(g), 0, ptr(do),
+                                        ptr(dht), ptr(dh), ptr(dh0), sc, *lay),
+                           tok * (2 * K + V) * BF + STATE_BYTES * 2 + hbytes),
+        "chunk_bwd_dqkg": (lambda: call("tops_gla_chunk_bwd_dqkg", ptr(q), ptr(k), ptr(v),
+                                        ptr(g), ptr(h), ptr(do), ptr(dh), ptr(dq), ptr(dk),
+                                        ptr(dg), sc, *lay),
+                           tok * (6 * K + 2 * V) * BF + 2 * hbytes),
+        "chunk_bwd_dv": (lambda: call("tops_gla_chunk_bwd_dv", ptr(q), ptr(k), ptr(g), ptr(do),
+                                      ptr(dh), ptr(dv), sc, *lay),
+                         tok * (3 * K + 2 * V) * BF + hbytes),
+    }
+    res = {}
+    cur = torch.cuda.current_stream(dev)
+    for name, (fn, nbytes) in kernels.items():
+        fn()  # warm (and produces h / dh for the kernels after it)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        for _ in range(reps):
+            fn()
+        e1.record(cur)
+        torch.cuda.synchronize(dev)
+        ms = e0.elapsed_time(e1) / reps
+        res[name] = dict(ms=round(ms, 4), bytes=int(nbytes),
+                         gbs=round(nbytes / (ms * 1e-3) / 1e9, 1))
+    return res
+
+
+def _cpu_baseline(heads=8):
+    """Float32 numpy oracle (single thread) on B=1, `heads` heads, full T; scaled to the
+    whole workload's tokens/s."""
+    import numpy as np
+
+    import oracle as orc
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    r = np.random.default_rng(SEED)
+    f = np.float32
+    q, k, v = (r.standard_normal((1, T, heads, d), dtype=f) for d in (K, K, V))
+    g = (-np.logaddexp(0, -r.standard_normal((1, T, heads, K), dtype=f)) / 16).astype(f)
+    h0 = r.standard_normal((1, heads, K, V), dtype=f) * 0.1
+    do = r.standard_normal((1, T, heads, V), dtype=f)
+    dht = r.standard_normal((1, heads, K, V), dtype=f) * 0.1
+
+    def run():
+        orc.chunk_gla(q, k, v, g, initial_state=h0, output_final_state=True, chunk_size=C,
+                      dtype=np.float32)
+        orc.chunk_gla_bwd(q, k, v, g, None, None, K ** -0.5, h0, None, None, do, dht,
+                          chunk_size=C, dtype=np.float32)
+
+    ctx = threadpool_limits(limits=1) if threadpool_limits else None
+    t0 = time.perf_counter()
+    if ctx:
+        with ctx:
+            run()
+    else:
+        run()
+    dt = time.perf_counter() - t0
+    frac = heads / (B * H)  # share of the workload's (batch, head) slices
+    tokens_per_s = B * T / (dt / frac)
+    return dict(value=round(tokens_per_s, 1), unit="tokens/s", cores=1, kind="port",
+                sample=f"numpy float32 oracle chunk_gla fwd+bwd on B=1 T={T} H={heads} "
+                       f"K=V={K} (={frac:.3f} of the workload), {dt:.1f} s, scaled",
+                affinity_cpus=len(os.sched_getaffinity(0)))
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernel-profile", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=8)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the GLA path shards over batch and "
+              "heads with no communication); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import tops.ops.gla as G
+
+    dev = torch.device("cuda:0")
+    x = _inputs(dev)
+    lq, lk, lv, lg, lh0 = (x[n].clone().requires_grad_() for n in ("q", "k", "v", "g", "h0"))
+
+    def step():
+        o, ht = G.chunk_gla(lq, lk, lv, lg, initial_state=lh0, output_final_state=True,
+                            chunk_size=C)
+        return torch.autograd.grad((o, ht), (lq, lk, lv, lg, lh0), (x["do"], x["dht"]))
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    cur = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    for _ in range(a.steps):
+        step()
+    e1.record(cur)
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / a.steps
+    tokens_s = B * T / (ms * 1e-3)
+
+    out = {
+        "metric": METRIC,
+        "value": round(tokens_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "chunk_gla fwd+bwd (BASELINE configs[3])", "B": B, "T": T,
+                   "H": H, "K": K, "V": V, "chunk_size": C, "h0": True, "dht": True,
+                   "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
+        "tflops": round(FLOPS_STEP / (ms * 1e-3) / 1e12, 2),
+        "mfma_frac": round(FLOPS_STEP / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
+    }
+    if not a.no_kernel_profile:
+        prof = _kernel_profile(x)
+        dom = max(prof, key=lambda n: prof[n]["ms"])
+        d = prof[dom]
+        out["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": d["gbs"],
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}
+        out["kernels"] = prof
+    if not a.no_cpu_baseline:
+        out["cpu_baseline"] = _cpu_baseline(a.cpu_heads)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

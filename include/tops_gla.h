@@ -1,0 +1,172 @@
+/*
+ * tops_gla.h -- C ABI of the MI355X (gfx950) Gated Linear Attention kernels.
+ *
+ * This is the drop-in boundary for the reference's GLA hot path (package `tops`,
+ * primatrix/pallas-kernel). The reference has no native boundary: its Python functions
+ * lower to `pl.pallas_call` custom calls. Each entry point below replaces one of those
+ * launch sites (cited per function) and is what an XLA typed-FFI handler or a ctypes
+ * binding calls.
+ *
+ * Conventions (all entry points):
+ *  - Tensors are device pointers (HBM), row-major, in the reference layout: q/k/g
+ *    [B, T, H, K], v/o/do [B, T, H, V], states [N, H, K, V]. No pointer is retained.
+ *  - `dtype` is the element type of q, k, v, g, o and of the q/k/v/g/do gradients:
+ *    TOPS_GLA_F32 or TOPS_GLA_BF16. Initial/final states and their gradients are float32.
+ *  - Sequences: fixed-length when `cu_seqlens == NULL` (B sequences of T tokens, N == B);
+ *    otherwise B must be 1, `cu_seqlens` is a device int32 array [N + 1] of token offsets
+ *    and `chunk_offsets` a device int32 array [N + 1] with the prefix sums of
+ *    ceil(len_i / chunk_size); `NC` is the total number of chunks (chunk_offsets[N]).
+ *    For fixed-length calls NC must equal B * ceil(T / chunk_size).
+ *  - Per-chunk state buffers ([NC, H, K, V], element type `dtype`) are caller-provided
+ *    workspaces; the library allocates nothing.
+ *  - Work is enqueued on `stream` (a hipStream_t); nothing synchronizes the device.
+ *  - Return value: TOPS_GLA_OK, or an error code with a message from
+ *    tops_gla_last_error() (thread-local). Invalid arguments never launch a kernel.
+ *  - chunk_size: 16, 32 or 64 for the MFMA kernels; any power of two for the cumsum.
+ */
+#ifndef TOPS_GLA_H_
+#define TOPS_GLA_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum tops_gla_status {
+  TOPS_GLA_OK = 0,
+  TOPS_GLA_EINVAL = 1,      /* bad shape / pointer / flag */
+  TOPS_GLA_EUNSUPPORTED = 2, /* valid for the reference, not supported by these kernels */
+  TOPS_GLA_EHIP = 3          /* HIP launch error */
+};
+
+enum tops_gla_dtype { TOPS_GLA_F32 = 0, TOPS_GLA_BF16 = 1 };
+
+/* Message describing the last error on the calling thread ("" if none). */
+const char* tops_gla_last_error(void);
+
+/* Library version string. */
+const char* tops_gla_version(void);
+
+/*
+ * Chunk-local (optionally reverse, scaled) prefix sum of gates over the last-but-one axis
+ * groups of `chunk_size` tokens, restarting at every sequence start.
+ * Replaces: chunk_cumsum_kernel launch, tops/ops/gla/chunk.py:176-189
+ *           (chunk_local_cumsum_vector, chunk.py:110-198).
+ * g/out: [B, T, H, S] (or [B, H, T, S] when head_first), element types in_dtype/out_dtype.
+ */
+int tops_gla_chunk_local_cumsum(const void* g, void* out, int64_t B, int64_t T, int64_t H,
+                                int64_t S, int chunk_size, int reverse, int has_scale,
+                                float scale, int head_first, const int32_t* cu_seqlens,
+                                const int32_t* chunk_offsets, int64_t N, int64_t NC,
+                                int in_dtype, int out_dtype, void* stream);
+
+/*
+ * Inter-chunk state scan: h[c] = state entering chunk c ([NC, H, K, V], dtype), and the
+ * final state ht [N, H, K, V] (float32). g holds raw log-gates (the chunk-local cumsum is
+ * taken in-kernel) or, with g_is_cumsum, the cumsum itself. h0/h/ht may be NULL.
+ * Replaces: chunk_fwd_h_kernel launch, tops/ops/common/chunk_h.py:252-271
+ *           (body :18-119; jnp ref tops/ops/gla/chunk.py:206-292).
+ */
+int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_cumsum,
+                         const float* h0, void* h, float* ht, int64_t B, int64_t T, int64_t H,
+                         int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                         const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                         void* stream);
+
+/*
+ * Reverse state-gradient scan: dh[c] = dL/d(state leaving chunk c) ([NC, H, K, V], dtype),
+ * dh0 [N, H, K, V] float32 (may be NULL). dht may be NULL (zero).
+ * Replaces: chunk_bwd_dh_kernel launch, tops/ops/common/chunk_h.py:681-695
+ *           (body :495-591; jnp ref chunk_bwd_dh_ref :399-492).
+ */
+int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const void* dout,
+                          const float* dht, void* dh, float* dh0, float scale, int64_t B,
+                          int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
+                          const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                          int64_t NC, int dtype, void* stream);
+
+/*
+ * Per-chunk intra matrix and output. A_out (float32, [NC * chunk_size, H, chunk_size],
+ * unmasked, scaled) and o ([B, T, H, V], dtype) are optional; with A_in the given matrix
+ * is used (causally masked) instead of recomputing it; h ([NC, H, K, V], dtype) may be NULL
+ * (no inter-chunk term).
+ * Replaces: chunk_gla_fwd_intra_gk launch, tops/ops/gla/chunk.py:416-427, and
+ *           chunk_gla_fwd_o_gk_pl launch, chunk.py:1360-1376 (bodies :350-383, :1259-1312).
+ */
+int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void* g,
+                         int g_is_cumsum, const void* h, const float* A_in, float* A_out,
+                         void* o, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
+                         int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                         const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                         void* stream);
+
+/*
+ * chunk_gla forward: state scan into h_ws ([NC, H, K, V], dtype, required: it is the
+ * residual the backward reuses) then the per-chunk output. h0/ht may be NULL.
+ * Replaces the device part of chunk_gla_fwd, tops/ops/gla/chunk.py:1145-1166.
+ */
+int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* g,
+                       const float* h0, void* o, float* ht, void* h_ws, float scale, int64_t B,
+                       int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
+                       const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                       int64_t NC, int dtype, void* stream);
+
+/*
+ * chunk_gla backward: (dq, dk, dv, dg, dh0). `h` are the forward states ([NC, H, K, V]); if
+ * NULL they are recomputed into h_ws (then required). dh_ws ([NC, H, K, V], dtype) is
+ * required. h0, dht and dh0 may be NULL.
+ * Replaces the device part of chunk_gla_bwd_with_pl, tops/ops/gla/chunk.py:1019-1064
+ * (chunk_bwd_dh_kernel + chunk_gla_bwd_fused_pl, :1482-1550).
+ */
+int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
+                       const float* h0, const void* h, const void* dout, const float* dht,
+                       void* dq, void* dk, void* dv, void* dg, float* dh0, void* h_ws,
+                       void* dh_ws, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
+                       int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                       const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                       void* stream);
+
+/*
+ * Per-chunk dq, dk, dg of the backward (intra-chunk dA computed in-kernel) from the forward
+ * states h and the state gradients dh (both [NC, H, K, V], dtype, as produced by
+ * tops_gla_chunk_fwd_h / tops_gla_chunk_bwd_dh on raw gates g).
+ * Replaces: chunk_gla_bwd_dA_ref + chunk_gla_bwd_dqk_intra_ref + chunk_gla_bwd_dqkg_ref,
+ *           tops/ops/gla/chunk.py:504-539, :603-648, :656-743 (the dq/dk/dg part of
+ *           chunk_gla_bwd_fused_kernel, :1423-1479).
+ */
+int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const void* g,
+                            const void* h, const void* dout, const void* dh, void* dq, void* dk,
+                            void* dg, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
+                            int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                            const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                            void* stream);
+
+/*
+ * Per-chunk dv = tril(A)^T do + (k e^{gamma - g~}) dh (A recomputed in-kernel).
+ * Replaces: chunk_gla_bwd_dv_ref, tops/ops/gla/chunk.py:547-595 (the dv part of
+ *           chunk_gla_bwd_fused_kernel, :1423-1479).
+ */
+int tops_gla_chunk_bwd_dv(const void* q, const void* k, const void* g, const void* dout,
+                          const void* dh, void* dv, float scale, int64_t B, int64_t T,
+                          int64_t H, int64_t K, int64_t V, int chunk_size,
+                          const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                          int64_t NC, int dtype, void* stream);
+
+/*
+ * Fused recurrent forward. gk [B, T, H, K] / gv [B, T, H, V] gates may be NULL; o is
+ * written in o_dtype (the reference returns float32); h0/ht float32, may be NULL.
+ * Replaces: _fused_recurrent_gla_fwd pallas_call, tops/ops/gla/fused_recurrent.py:344-362
+ *           (body :139-227).
+ */
+int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, const void* gk,
+                                 const void* gv, const float* h0, void* o, float* ht,
+                                 float scale, int reverse, int64_t B, int64_t T, int64_t H,
+                                 int64_t K, int64_t V, const int32_t* cu_seqlens, int64_t N,
+                                 int dtype, int o_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TOPS_GLA_H_ */

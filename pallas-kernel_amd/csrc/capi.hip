@@ -1,0 +1,450 @@
+// extern "C" entry points declared in include/tops_gla.h: argument validation, sequence
+// layout, and kernel dispatch. Nothing here allocates or synchronizes.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/tops_gla.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return TOPS_GLA_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(TOPS_GLA_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool dtype_ok(int d) { return d == TOPS_GLA_F32 || d == TOPS_GLA_BF16; }
+
+constexpr int64_t kMaxInt = 2147483647;
+
+// Validates the sequence description and fills a SeqInfo.
+int make_seq(int64_t B, int64_t T, int64_t H, int chunk, const int32_t* cu,
+             const int32_t* chunk_off, int64_t N, int64_t NC, bool need_chunk_off,
+             tops::SeqInfo* si) {
+  if (B < 0 || T < 0 || H <= 0) return fail(TOPS_GLA_EINVAL, "bad B/T/H (%lld, %lld, %lld)",
+                                            (long long)B, (long long)T, (long long)H);
+  if (chunk <= 0) return fail(TOPS_GLA_EINVAL, "chunk_size must be positive");
+  if (B * T > kMaxInt) return fail(TOPS_GLA_EUNSUPPORTED, "B*T exceeds 2^31 tokens");
+  si->C = chunk;
+  if (cu == nullptr) {
+    const int64_t nt = (T + chunk - 1) / chunk;
+    if (NC != B * nt)
+      return fail(TOPS_GLA_EINVAL, "NC (%lld) != B * ceil(T / chunk_size) (%lld)",
+                  (long long)NC, (long long)(B * nt));
+    si->N = (int)B;
+    si->T = (int)T;
+    si->NC = (int)NC;
+    si->cu = nullptr;
+    si->chunk_cu = nullptr;
+  } else {
+    if (B != 1) return fail(TOPS_GLA_EINVAL, "cu_seqlens requires B == 1 (got %lld)",
+                            (long long)B);
+    if (N <= 0) return fail(TOPS_GLA_EINVAL, "cu_seqlens needs N >= 1 sequences");
+    if (need_chunk_off && chunk_off == nullptr)
+      return fail(TOPS_GLA_EINVAL, "chunk_offsets is required with cu_seqlens");
+    if (NC < 0 || NC > kMaxInt) return fail(TOPS_GLA_EINVAL, "bad NC");
+    si->N = (int)N;
+    si->T = (int)T;
+    si->NC = (int)NC;
+    si->cu = cu;
+    si->chunk_cu = chunk_off;
+  }
+  if ((int64_t)si->NC * H > kMaxInt) return fail(TOPS_GLA_EUNSUPPORTED, "NC*H too large");
+  return TOPS_GLA_OK;
+}
+
+int check_mfma_common(int64_t K, int64_t V, int chunk, int dtype) {
+  if (!dtype_ok(dtype)) return fail(TOPS_GLA_EINVAL, "dtype must be F32 (0) or BF16 (1)");
+  if (K <= 0 || V <= 0) return fail(TOPS_GLA_EINVAL, "K and V must be positive");
+  if (chunk != 16 && chunk != 32 && chunk != 64)
+    return fail(TOPS_GLA_EUNSUPPORTED, "chunk_size %d: the MFMA kernels take 16, 32 or 64",
+                chunk);
+  // LDS of the per-chunk output kernel grows with K (all K tiles of q e^{g} stay resident)
+  const int64_t esz = dtype == TOPS_GLA_BF16 ? 2 : 4;
+  const int64_t CP = chunk < 32 ? 32 : chunk;
+  const int64_t pad = 16 / esz;
+  const int64_t KP = (K + 63) / 64 * 64;
+  const int64_t lds = chunk * (KP + pad) * esz + KP * 4 + chunk * (64 + pad) * esz +
+                      chunk * (CP + pad) * esz + 64 * (CP + pad) * esz +
+                      64 * (64 + pad) * esz + 1024 + 64;
+  if (lds > 160 * 1024)
+    return fail(TOPS_GLA_EUNSUPPORTED,
+                "K=%lld with chunk_size %d needs %lld B of LDS (> 160 KiB); use a smaller "
+                "chunk_size or bf16",
+                (long long)K, chunk, (long long)lds);
+  return TOPS_GLA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tops_gla_last_error(void) { return g_err; }
+
+const char* tops_gla_version(void) { return "tops-gla-mi355x 0.1.0 (gfx950)"; }
+
+int tops_gla_chunk_local_cumsum(const void* g, void* out, int64_t B, int64_t T, int64_t H,
+                                int64_t S, int chunk_size, int reverse, int has_scale,
+                                float scale, int head_first, const int32_t* cu_seqlens,
+                                const int32_t* chunk_offsets, int64_t N, int64_t NC,
+                                int in_dtype, int out_dtype, void* stream) {
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(TOPS_GLA_EINVAL, "bad dtype");
+  if (chunk_size <= 0 || (chunk_size & (chunk_size - 1)) != 0)
+    return fail(TOPS_GLA_EINVAL, "chunk_size must be a power of 2 (got %d)", chunk_size);
+  if (S < 0) return fail(TOPS_GLA_EINVAL, "bad S");
+  if ((g == nullptr || out == nullptr) && B * T * H * S > 0)
+    return fail(TOPS_GLA_EINVAL, "g and out must not be NULL");
+  tops::SeqInfo si;
+  int rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (NC * H > 2147483647LL || (S + 255) / 256 > 65535)
+    return fail(TOPS_GLA_EUNSUPPORTED, "grid too large");
+  tops::CumsumArgs p;
+  p.g = g;
+  p.out = out;
+  p.H = (int)H;
+  p.S = (int)S;
+  p.reverse = reverse != 0;
+  p.has_scale = has_scale != 0;
+  p.head_first = head_first != 0;
+  p.scale = scale;
+  p.T_total = T;
+  p.si = si;
+  return hip_status(tops::run_cumsum(p, in_dtype, out_dtype, (hipStream_t)stream),
+                    "chunk_local_cumsum");
+}
+
+int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_cumsum,
+                         const float* h0, void* h, float* ht, int64_t B, int64_t T, int64_t H,
+                         int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                         const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                         void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if ((k == nullptr || v == nullptr || g == nullptr) && B * T > 0)
+    return fail(TOPS_GLA_EINVAL, "k, v and g must not be NULL");
+  tops::ScanArgs p;
+  p.a = k;
+  p.b = v;
+  p.g = g;
+  p.g_is_cumsum = g_is_cumsum != 0;
+  p.s_init = h0;
+  p.s_all = h;
+  p.s_final = ht;
+  p.scale = 1.f;
+  p.H = (int)H;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.si = si;
+  return hip_status(tops::run_state_scan(p, false, dtype, (hipStream_t)stream), "chunk_fwd_h");
+}
+
+int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const void* dout,
+                          const float* dht, void* dh, float* dh0, float scale, int64_t B,
+                          int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
+                          const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                          int64_t NC, int dtype, void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if ((q == nullptr || dout == nullptr || g == nullptr) && B * T > 0)
+    return fail(TOPS_GLA_EINVAL, "q, g and do must not be NULL");
+  tops::ScanArgs p;
+  p.a = q;
+  p.b = dout;
+  p.g = g;
+  p.g_is_cumsum = g_is_cumsum != 0;
+  p.s_init = dht;
+  p.s_all = dh;
+  p.s_final = dh0;
+  p.scale = scale;
+  p.H = (int)H;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.si = si;
+  return hip_status(tops::run_state_scan(p, true, dtype, (hipStream_t)stream), "chunk_bwd_dh");
+}
+
+int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void* g,
+                         int g_is_cumsum, const void* h, const float* A_in, float* A_out,
+                         void* o, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
+                         int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                         const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                         void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (B * T > 0 && (q == nullptr || g == nullptr))
+    return fail(TOPS_GLA_EINVAL, "q and g must not be NULL");
+  if (B * T > 0 && A_in == nullptr && k == nullptr)
+    return fail(TOPS_GLA_EINVAL, "k is required unless A_in is given");
+  if (B * T > 0 && o != nullptr && v == nullptr)
+    return fail(TOPS_GLA_EINVAL, "v is required for o");
+  if (o == nullptr && A_out == nullptr) return ok();
+  tops::FwdOArgs p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.g = g;
+  p.g_is_cumsum = g_is_cumsum != 0;
+  p.h = h;
+  p.A_in = A_in;
+  p.A_out = A_in ? nullptr : A_out;
+  p.o = o;
+  p.scale = scale;
+  p.H = (int)H;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.si = si;
+  return hip_status(tops::run_chunk_fwd_o(p, dtype, (hipStream_t)stream), "chunk_fwd_o");
+}
+
+int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* g,
+                       const float* h0, void* o, float* ht, void* h_ws, float scale, int64_t B,
+                       int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
+                       const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                       int64_t NC, int dtype, void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || g == nullptr ||
+                    o == nullptr || h_ws == nullptr))
+    return fail(TOPS_GLA_EINVAL, "q, k, v, g, o and h_ws must not be NULL");
+  hipStream_t st = (hipStream_t)stream;
+  tops::ScanArgs s;
+  s.a = k;
+  s.b = v;
+  s.g = g;
+  s.g_is_cumsum = 0;
+  s.s_init = h0;
+  s.s_all = h_ws;
+  s.s_final = ht;
+  s.scale = 1.f;
+  s.H = (int)H;
+  s.K = (int)K;
+  s.V = (int)V;
+  s.si = si;
+  rc = hip_status(tops::run_state_scan(s, false, dtype, st), "chunk_fwd (state scan)");
+  if (rc) return rc;
+  tops::FwdOArgs p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.g = g;
+  p.g_is_cumsum = 0;
+  p.h = h_ws;
+  p.A_in = nullptr;
+  p.A_out = nullptr;
+  p.o = o;
+  p.scale = scale;
+  p.H = (int)H;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.si = si;
+  return hip_status(tops::run_chunk_fwd_o(p, dtype, st), "chunk_fwd (output)");
+}
+
+int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
+                       const float* h0, const void* h, const void* dout, const float* dht,
+                       void* dq, void* dk, void* dv, void* dg, float* dh0, void* h_ws,
+                       void* dh_ws, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
+                       int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                       const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                       void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || g == nullptr ||
+                    dout == nullptr || dq == nullptr || dk == nullptr || dv == nullptr ||
+                    dg == nullptr || dh_ws == nullptr))
+    return fail(TOPS_GLA_EINVAL, "q, k, v, g, do, dq, dk, dv, dg and dh_ws must not be NULL");
+  if (h == nullptr && h_ws == nullptr && B * T > 0)
+    return fail(TOPS_GLA_EINVAL, "h_ws is required when h is NULL");
+  hipStream_t st = (hipStream_t)stream;
+  if (h == nullptr) {
+    tops::ScanArgs s;
+    s.a = k;
+    s.b = v;
+    s.g = g;
+    s.g_is_cumsum = 0;
+    s.s_init = h0;
+    s.s_all = h_ws;
+    s.s_final = nullptr;
+    s.scale = 1.f;
+    s.H = (int)H;
+    s.K = (int)K;
+    s.V = (int)V;
+    s.si = si;
+    rc = hip_status(tops::run_state_scan(s, false, dtype, st), "chunk_bwd (state recompute)");
+    if (rc) return rc;
+    h = h_ws;
+  }
+  tops::ScanArgs d;
+  d.a = q;
+  d.b = dout;
+  d.g = g;
+  d.g_is_cumsum = 0;
+  d.s_init = dht;
+  d.s_all = dh_ws;
+  d.s_final = dh0;
+  d.scale = scale;
+  d.H = (int)H;
+  d.K = (int)K;
+  d.V = (int)V;
+  d.si = si;
+  rc = hip_status(tops::run_state_scan(d, true, dtype, st), "chunk_bwd (dh scan)");
+  if (rc) return rc;
+  tops::BwdArgs p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.g = g;
+  p.dout = dout;
+  p.h = h;
+  p.dh = dh_ws;
+  p.dq = dq;
+  p.dk = dk;
+  p.dv = dv;
+  p.dg = dg;
+  p.scale = scale;
+  p.H = (int)H;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.si = si;
+  return hip_status(tops::run_chunk_bwd(p, dtype, st), "chunk_bwd (gradients)");
+}
+
+int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const void* g,
+                            const void* h, const void* dout, const void* dh, void* dq, void* dk,
+                            void* dg, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
+                            int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                            const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                            void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || g == nullptr ||
+                    h == nullptr || dout == nullptr || dh == nullptr || dq == nullptr ||
+                    dk == nullptr || dg == nullptr))
+    return fail(TOPS_GLA_EINVAL, "no argument of chunk_bwd_dqkg may be NULL");
+  tops::BwdArgs p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.g = g;
+  p.dout = dout;
+  p.h = h;
+  p.dh = dh;
+  p.dq = dq;
+  p.dk = dk;
+  p.dv = nullptr;
+  p.dg = dg;
+  p.scale = scale;
+  p.H = (int)H;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.si = si;
+  return hip_status(tops::run_chunk_bwd(p, dtype, (hipStream_t)stream, 1), "chunk_bwd_dqkg");
+}
+
+int tops_gla_chunk_bwd_dv(const void* q, const void* k, const void* g, const void* dout,
+                          const void* dh, void* dv, float scale, int64_t B, int64_t T,
+                          int64_t H, int64_t K, int64_t V, int chunk_size,
+                          const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                          int64_t NC, int dtype, void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (B * T > 0 && (q == nullptr || k == nullptr || g == nullptr || dout == nullptr ||
+                    dh == nullptr || dv == nullptr))
+    return fail(TOPS_GLA_EINVAL, "no argument of chunk_bwd_dv may be NULL");
+  tops::BwdArgs p;
+  p.q = q;
+  p.k = k;
+  p.v = nullptr;
+  p.g = g;
+  p.dout = dout;
+  p.h = nullptr;
+  p.dh = dh;
+  p.dq = p.dk = p.dg = nullptr;
+  p.dv = dv;
+  p.scale = scale;
+  p.H = (int)H;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.si = si;
+  return hip_status(tops::run_chunk_bwd(p, dtype, (hipStream_t)stream, 2), "chunk_bwd_dv");
+}
+
+int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, const void* gk,
+                                 const void* gv, const float* h0, void* o, float* ht,
+                                 float scale, int reverse, int64_t B, int64_t T, int64_t H,
+                                 int64_t K, int64_t V, const int32_t* cu_seqlens, int64_t N,
+                                 int dtype, int o_dtype, void* stream) {
+  if (!dtype_ok(dtype) || !dtype_ok(o_dtype)) return fail(TOPS_GLA_EINVAL, "bad dtype");
+  if (dtype == TOPS_GLA_F32 && o_dtype != TOPS_GLA_F32)
+    return fail(TOPS_GLA_EUNSUPPORTED, "float32 inputs need a float32 output");
+  if (K <= 0 || V <= 0) return fail(TOPS_GLA_EINVAL, "K and V must be positive");
+  if (K > 256)
+    return fail(TOPS_GLA_EUNSUPPORTED, "fused_recurrent keeps K <= 256 in registers (K=%lld)",
+                (long long)K);
+  tops::SeqInfo si;
+  const int64_t NC = cu_seqlens ? 0 : B * T;  // chunk count unused; 1-token "chunks"
+  int rc = make_seq(B, T, H, 1, cu_seqlens, nullptr, N, NC, false, &si);
+  if (rc) return rc;
+  if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || o == nullptr))
+    return fail(TOPS_GLA_EINVAL, "q, k, v and o must not be NULL");
+  if ((int64_t)si.N * H * ((V + 63) / 64) > kMaxInt)
+    return fail(TOPS_GLA_EUNSUPPORTED, "grid too large");
+  tops::RecArgs p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.gk = gk;
+  p.gv = gv;
+  p.h0 = h0;
+  p.o = o;
+  p.ht = ht;
+  p.scale = scale;
+  p.H = (int)H;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.reverse = reverse != 0;
+  p.si = si;
+  return hip_status(tops::run_recurrent_fwd(p, dtype, o_dtype, (hipStream_t)stream),
+                    "fused_recurrent_fwd");
+}
+
+}  // extern "C"

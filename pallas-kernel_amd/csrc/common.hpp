@@ -1,0 +1,275 @@
+// Device-side building blocks shared by every GLA kernel (gfx950 / CDNA4 only).
+//
+// * Element types: `float` and `bf16` (bit-exact storage of bfloat16). Inputs of one call
+//   share one element type; the MFMA operand type equals it (bf16 -> 16x16x32 bf16 MFMA,
+//   float -> 8 x 16x16x4 f32 MFMA), accumulation is always fp32.
+// * MFMA operand fragments: lane l supplies row (l & 15) and the 8 contraction indices
+//   8*(l >> 4) .. +7 of a 16 x 32 slab. Both operands are read from LDS "contraction-major"
+//   (contraction index contiguous), so an output tile is `X[m][k] . Y[n][k]^T`.
+// * Accumulator layout (16x16 f32x4): acc[r] holds row 4*(l >> 4) + r, column l & 15.
+// * Sequence layout: tokens are flattened to one index tau over [B*T) (fixed length) or
+//   [T_total) (varlen, B == 1); element (tau, head, d) lives at (tau*H + head)*D + d.
+//   Chunks never cross a sequence boundary; the last chunk of a sequence may be partial.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tops {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct bf16 {
+  uint16_t u;
+};
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return __uint_as_float((uint32_t)x.u << 16); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float f);
+template <>
+__device__ __forceinline__ float from_f32<float>(float f) {
+  return f;
+}
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float f) {
+  // round to nearest even; NaN stays a (quiet) NaN
+  uint32_t u = __float_as_uint(f);
+  bf16 r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    r.u = 0x7fc0;
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);
+    r.u = (uint16_t)(u >> 16);
+  }
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T zero_elem() {
+  return from_f32<T>(0.f);
+}
+
+// exp for gate factors: correctly rounded-ish ocml expf on the fp32 path (parity bar 1e-4
+// absolute), the hardware exp2 path on the bf16 path (operands are rounded to bf16 anyway).
+template <typename T>
+__device__ __forceinline__ float gexp(float x);
+template <>
+__device__ __forceinline__ float gexp<float>(float x) {
+  return expf(x);
+}
+template <>
+__device__ __forceinline__ float gexp<bf16>(float x) {
+  return __expf(x);
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). Remap the
+// hardware block id so that consecutive logical blocks land on the same XCD.
+__device__ __forceinline__ int xcd_remap(int L, int total) {
+  if ((total & 7) != 0) return L;
+  return (L & 7) * (total >> 3) + (L >> 3);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA fragments
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Frag;
+template <>
+struct Frag<bf16> {
+  uint4 d;
+};
+template <>
+struct Frag<float> {
+  float4 a, b;
+};
+
+__device__ __forceinline__ Frag<bf16> ld_frag(const bf16* p) {
+  Frag<bf16> f;
+  f.d = *reinterpret_cast<const uint4*>(p);
+  return f;
+}
+__device__ __forceinline__ Frag<float> ld_frag(const float* p) {
+  Frag<float> f;
+  f.a = *reinterpret_cast<const float4*>(p);
+  f.b = *reinterpret_cast<const float4*>(p + 4);
+  return f;
+}
+
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<bf16>& a, const Frag<bf16>& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a.d),
+                                                 __builtin_bit_cast(bf16x8_t, b.d), acc, 0,
+                                                 0, 0);
+}
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<float>& a, const Frag<float>& b) {
+  // Contraction index 8*(l>>4)+e is fed to MFMA #e as its k = l>>4 (a consistent
+  // permutation of the 32 indices for both operands).
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.a.x, b.a.x, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.a.y, b.a.y, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.a.z, b.a.z, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.a.w, b.a.w, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.b.x, b.b.x, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.b.y, b.b.y, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.b.z, b.b.z, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.b.w, b.b.w, acc, 0, 0, 0);
+}
+
+// acc += X[0:16][0:klen] . Y[0:16][0:klen]^T, both in LDS, contraction-major, klen % 32 == 0.
+template <typename T>
+__device__ __forceinline__ void mma_tile(f32x4& acc, const T* X, int px, const T* Y, int py,
+                                         int klen, int lane) {
+  const T* xr = X + (lane & 15) * px + (lane >> 4) * 8;
+  const T* yr = Y + (lane & 15) * py + (lane >> 4) * 8;
+  for (int kk = 0; kk < klen; kk += 32) mma(acc, ld_frag(xr + kk), ld_frag(yr + kk));
+}
+
+__device__ __forceinline__ f32x4 zero4() {
+  f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  return z;
+}
+
+// LDS row pitch (elements) for a contraction-major buffer of width w: +16 bytes of padding
+// breaks the 16-way bank conflict of 16 lanes reading 16 consecutive rows.
+template <typename T>
+__host__ __device__ constexpr int pitch_of(int w) {
+  return w + (int)(16 / sizeof(T));
+}
+
+// ---------------------------------------------------------------------------
+// Sequence / chunk layout
+// ---------------------------------------------------------------------------
+struct SeqInfo {
+  int N;                // sequences
+  int T;                // tokens per sequence (fixed-length mode)
+  int C;                // chunk size
+  int NC;               // total chunks
+  const int* cu;        // [N+1] token offsets (varlen) or nullptr
+  const int* chunk_cu;  // [N+1] chunk offsets (varlen) or nullptr
+};
+
+__device__ __forceinline__ void seq_range(const SeqInfo& s, int i, int& bos, int& eos,
+                                          int& c0, int& nc) {
+  if (s.cu) {
+    bos = s.cu[i];
+    eos = s.cu[i + 1];
+    c0 = s.chunk_cu[i];
+    nc = s.chunk_cu[i + 1] - c0;
+  } else {
+    const int nt = (s.T + s.C - 1) / s.C;
+    bos = i * s.T;
+    eos = bos + s.T;
+    c0 = i * nt;
+    nc = nt;
+  }
+}
+
+// Token range of sequence i only (reads no chunk offsets; valid with chunk_cu == nullptr).
+__device__ __forceinline__ void seq_bounds(const SeqInfo& s, int i, int& bos, int& eos) {
+  if (s.cu) {
+    bos = s.cu[i];
+    eos = s.cu[i + 1];
+  } else {
+    bos = i * s.T;
+    eos = bos + s.T;
+  }
+}
+
+// Global chunk index -> (sequence, first token, valid rows).
+__device__ __forceinline__ void chunk_range(const SeqInfo& s, int c, int& seq, int& t0,
+                                            int& len) {
+  if (s.cu) {
+    int lo = 0, hi = s.N - 1;  // largest i with chunk_cu[i] <= c (skips empty sequences)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s.chunk_cu[mid] <= c) lo = mid; else hi = mid - 1;
+    }
+    seq = lo;
+    t0 = s.cu[lo] + (c - s.chunk_cu[lo]) * s.C;
+    len = min(s.C, s.cu[lo + 1] - t0);
+  } else {
+    const int nt = (s.T + s.C - 1) / s.C;
+    seq = c / nt;
+    const int n = c - seq * nt;
+    t0 = seq * s.T + n * s.C;
+    len = min(s.C, s.T - n * s.C);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Chunk-local cumsum of one 64-column gate tile, cooperative over a 256-thread block.
+// Thread t owns column (t & 63) and rows [(t >> 6) * RPS, +RPS), RPS = C / 4.
+// On return gt[] holds the inclusive cumsum of its rows, `gamma` the value at row C-1
+// (rows >= len read as 0, so this equals the last valid row), `first` the value at row 0.
+// If G_IS_CUMSUM the input already holds the cumsum and is only loaded.
+// sTot needs 4*64 floats; contains a __syncthreads().
+// ---------------------------------------------------------------------------
+template <int C, typename TIN>
+__device__ __forceinline__ void tile_cumsum(const TIN* __restrict__ g, long row_stride,
+                                            int len, int col_valid, bool g_is_cumsum,
+                                            float* sTot, float (&gt)[C / 4], float& gamma,
+                                            float& first) {
+  constexpr int RPS = C / 4;
+  const int tid = threadIdx.x;
+  const int col = tid & 63, seg = tid >> 6;
+  const int r0 = seg * RPS;
+  float run = 0.f;
+#pragma unroll
+  for (int r = 0; r < RPS; ++r) {
+    const int row = r0 + r;
+    float x = 0.f;
+    if (row < len && col_valid) x = to_f32(g[(long)row * row_stride]);
+    if (g_is_cumsum) {
+      gt[r] = x;
+    } else {
+      run += x;
+      gt[r] = run;
+    }
+  }
+  if (g_is_cumsum) {
+    // gamma = value at the last valid row; first = row 0
+    sTot[seg * 64 + col] = 0.f;
+    __syncthreads();
+    if (len > 0) {
+      const int lr = len - 1;
+      if (lr >= r0 && lr < r0 + RPS) {
+#pragma unroll
+        for (int r = 0; r < RPS; ++r)
+          if (r0 + r == lr) sTot[col] = gt[r];  // seg-local write into slot 0 of the column
+      }
+    }
+    // slot 64+col: row 0
+    if (seg == 0) sTot[64 + col] = gt[0];
+    __syncthreads();
+    gamma = sTot[col];
+    first = sTot[64 + col];
+    // rows beyond len keep their loaded 0; callers only use them multiplied by zero inputs,
+    // but keep them equal to gamma so exp() stays bounded.
+#pragma unroll
+    for (int r = 0; r < RPS; ++r)
+      if (r0 + r >= len) gt[r] = gamma;
+    __syncthreads();
+    return;
+  }
+  sTot[seg * 64 + col] = run;
+  __syncthreads();
+  float off = 0.f, tot = 0.f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const float v = sTot[s * 64 + col];
+    off += (s < seg) ? v : 0.f;
+    tot += v;
+  }
+#pragma unroll
+  for (int r = 0; r < RPS; ++r) gt[r] += off;
+  gamma = tot;
+  first = sTot[col];  // segment 0's total is not row 0; fixed below
+  __syncthreads();
+  if (seg == 0) sTot[col] = gt[0];
+  __syncthreads();
+  first = sTot[col];
+  __syncthreads();
+}
+
+}  // namespace tops

@@ -1,0 +1,79 @@
+// Internal (C++) launch interface between the C-ABI layer (capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+
+namespace tops {
+
+enum DType { DT_F32 = 0, DT_BF16 = 1 };
+
+// Inter-chunk state scan (chunk_h.hip).
+struct ScanArgs {
+  const void* a;        // forward: k ; reverse: q
+  const void* b;        // forward: v ; reverse: do
+  const void* g;        // gates (raw, or chunk-local cumsum when g_is_cumsum)
+  int g_is_cumsum;
+  const float* s_init;  // forward: h0 ; reverse: dht (nullable)
+  void* s_all;          // per-chunk states [NC, H, K, V] in the input dtype (nullable)
+  float* s_final;       // forward: ht ; reverse: dh0 (nullable)
+  float scale;          // reverse only
+  int H, K, V;
+  SeqInfo si;
+};
+hipError_t run_state_scan(const ScanArgs& p, bool reverse, int dtype, hipStream_t st);
+
+// Per-chunk intra matrix and output (chunk_fwd.hip).
+struct FwdOArgs {
+  const void *q, *k, *v, *g;
+  int g_is_cumsum;
+  const void* h;        // [NC, H, K, V] state at chunk start (nullable: no inter term)
+  const float* A_in;    // [NC*C, H, C] given intra matrix (nullable: computed)
+  float* A_out;         // [NC*C, H, C] unmasked intra matrix (nullable)
+  void* o;              // [tokens, H, V] (nullable)
+  float scale;
+  int H, K, V;
+  SeqInfo si;
+};
+hipError_t run_chunk_fwd_o(const FwdOArgs& p, int dtype, hipStream_t st);
+
+// Per-chunk gradients (chunk_bwd.hip).
+struct BwdArgs {
+  const void *q, *k, *v, *g, *dout;
+  const void* h;        // [NC, H, K, V] forward states (chunk start)
+  const void* dh;       // [NC, H, K, V] state gradients (chunk end)
+  void *dq, *dk, *dv, *dg;
+  float scale;
+  int H, K, V;
+  SeqInfo si;
+};
+// which: bit 0 = dq/dk/dg kernel, bit 1 = dv kernel
+hipError_t run_chunk_bwd(const BwdArgs& p, int dtype, hipStream_t st, int which = 3);
+
+// Chunk-local cumsum (cumsum.hip).
+struct CumsumArgs {
+  const void* g;
+  void* out;
+  int H, S;
+  int reverse, has_scale, head_first;
+  float scale;
+  long T_total;         // tokens per batch row (head_first stride)
+  SeqInfo si;
+};
+hipError_t run_cumsum(const CumsumArgs& p, int in_dtype, int out_dtype, hipStream_t st);
+
+// Fused recurrent forward (recurrent.hip).
+struct RecArgs {
+  const void *q, *k, *v, *gk, *gv;  // gk / gv nullable
+  const float* h0;                  // nullable
+  void* o;                          // [tokens, H, V] in o_dtype
+  float* ht;                        // nullable
+  float scale;
+  int H, K, V;
+  int reverse;
+  SeqInfo si;                       // C unused
+};
+hipError_t run_recurrent_fwd(const RecArgs& p, int dtype, int o_dtype, hipStream_t st);
+
+}  // namespace tops

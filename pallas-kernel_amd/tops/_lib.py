@@ -1,0 +1,176 @@
+"""ctypes binding of ``libtops_gla.so`` (C ABI: ``include/tops_gla.h``).
+
+The library is loaded after torch so that it binds to the HIP runtime torch already loaded
+(both carry SONAME ``libamdhip64.so.7``): one runtime, one set of streams in the process.
+Every entry point enqueues on torch's current stream of the tensors' device. A missing
+library or a non-ROCm tensor raises; nothing falls back to the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get(
+    "TOPS_GLA_LIB", os.path.join(os.path.dirname(_HERE), "lib", "libtops_gla.so"))
+
+F32, BF16 = 0, 1
+_DT = {torch.float32: F32, torch.bfloat16: BF16}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argtypes (order of include/tops_gla.h)
+_SIGS = {
+    "tops_gla_chunk_local_cumsum": [_P, _P, _I64, _I64, _I64, _I64, _I, _I, _I, _F, _I, _P, _P,
+                                    _I64, _I64, _I, _I, _P],
+    "tops_gla_chunk_fwd_h": [_P, _P, _P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P,
+                             _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_bwd_dh": [_P, _P, _I, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I,
+                              _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_fwd_o": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64,
+                             _I64, _I, _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I,
+                           _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64,
+                           _I64, _I64, _I64, _I64, _I, _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_bwd_dqkg": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64,
+                                _I64, _I64, _I, _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_bwd_dv": [_P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I, _P,
+                              _P, _I64, _I64, _I, _P],
+    "tops_gla_fused_recurrent_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _F, _I, _I64, _I64, _I64,
+                                     _I64, _I64, _P, _I64, _I, _I, _P],
+}
+EXPORTED = ["tops_gla_last_error", "tops_gla_version"] + list(_SIGS)
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load():
+    """Load the shared library (once) and declare every prototype."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"tops GLA: {LIB_PATH} is not built; run `python -c 'import "
+                    f"__graft_entry__ as g; g.build()'` or `make -C pallas-kernel_amd/csrc`")
+            lib = ctypes.CDLL(LIB_PATH)
+            lib.tops_gla_last_error.restype = ctypes.c_char_p
+            lib.tops_gla_last_error.argtypes = []
+            lib.tops_gla_version.restype = ctypes.c_char_p
+            lib.tops_gla_version.argtypes = []
+            for name, args in _SIGS.items():
+                fn = getattr(lib, name)
+                fn.argtypes = args
+                fn.restype = ctypes.c_int
+            _lib = lib
+    return _lib
+
+
+def call(name, *args):
+    """Invoke ``name``; map the C status to a Python exception."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.tops_gla_last_error().decode()
+        if rc == 1:
+            raise ValueError(f"{name}: {msg}")
+        if rc == 2:
+            raise NotImplementedError(f"{name}: {msg}")
+        raise RuntimeError(f"{name}: {msg}")
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def dtype_code(dt):
+    if dt not in _DT:
+        raise TypeError(f"tops GLA kernels take float32 or bfloat16, got {dt}")
+    return _DT[dt]
+
+
+def check_device(*tensors):
+    """All tensors on one ROCm device; returns it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "tops GLA runs only on a ROCm GPU (tensor on %s); there is no CPU path" % t.device)
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def stream_of(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class SeqLayout:
+    """Sequence/chunk description passed to every chunked entry point.
+
+    Fixed-length: ``N = B`` sequences of T tokens. Varlen (``cu_seqlens``, B == 1): token
+    offsets and per-sequence chunk offsets uploaded as int32 device arrays (cached).
+    """
+
+    _cache: dict = {}
+
+    def __init__(self, B, T, chunk, cu_seqlens, device):
+        self.B, self.T, self.C = int(B), int(T), int(chunk)
+        if cu_seqlens is None:
+            self.N = self.B
+            self.NC = self.B * ((self.T + self.C - 1) // self.C)
+            self.cu = self.chunk_cu = None
+            self.cu_list = None
+            return
+        cu = to_list(cu_seqlens)
+        assert self.B == 1, f"cu_seqlens requires B == 1, got B={self.B}"
+        assert len(cu) >= 2 and cu[0] == 0 and all(b >= a for a, b in zip(cu, cu[1:])), \
+            f"cu_seqlens must be non-decreasing from 0: {cu}"
+        assert cu[-1] <= self.T, f"cu_seqlens[-1]={cu[-1]} exceeds T={self.T}"
+        self.cu_list = cu
+        self.N = len(cu) - 1
+        nch = [(b - a + self.C - 1) // self.C for a, b in zip(cu, cu[1:])]
+        coff = [0]
+        for n in nch:
+            coff.append(coff[-1] + n)
+        self.NC = coff[-1]
+        key = (tuple(cu), self.C, str(device))
+        hit = SeqLayout._cache.get(key)
+        if hit is None:
+            hit = (torch.tensor(cu, dtype=torch.int32, device=device),
+                   torch.tensor(coff, dtype=torch.int32, device=device))
+            if len(SeqLayout._cache) > 64:
+                SeqLayout._cache.clear()
+            SeqLayout._cache[key] = hit
+        self.cu, self.chunk_cu = hit
+
+    def args(self):
+        """``cu_seqlens, chunk_offsets, N, NC`` as C arguments."""
+        return (ptr(self.cu), ptr(self.chunk_cu), self.N, self.NC)
+
+
+def to_list(cu):
+    if isinstance(cu, torch.Tensor):
+        return [int(x) for x in cu.detach().cpu().reshape(-1).tolist()]
+    try:
+        import numpy as np
+
+        return [int(x) for x in np.asarray(cu).reshape(-1).tolist()]
+    except Exception:  # pragma: no cover - plain sequences
+        return [int(x) for x in cu]

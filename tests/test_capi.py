@@ -1,0 +1,138 @@
+"""C-ABI boundary checks that run without a GPU.
+
+* ``libtops_gla.so`` loads and exports every function ``include/tops_gla.h`` declares, with
+  the argument count the Python binding uses.
+* Invalid arguments are rejected by the host-side validator with the documented status code
+  and message, before any HIP call (so these calls are safe on a machine without a GPU).
+* The Python API refuses CPU tensors (there is no CPU fallback).
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from tops import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tops_gla.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|const char\*)\s+(tops_gla_\w+)\s*\(([^)]*)\)\s*;", src):
+        params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+def test_header_lists_entry_points():
+    decl = _declared()
+    assert len(decl) == 11, decl
+    assert set(decl) == set(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name, nargs in _declared().items():
+        assert hasattr(lib, name), f"{name} not exported"
+        if name in _lib._SIGS:
+            assert len(_lib._SIGS[name]) == nargs, f"{name}: binding has {len(_lib._SIGS[name])}"\
+                f" args, header declares {nargs}"
+    assert lib.tops_gla_version().startswith(b"tops-gla-mi355x")
+
+
+def _rc(name, *args):
+    lib = _lib.load()
+    rc = getattr(lib, name)(*args)
+    return rc, lib.tops_gla_last_error().decode()
+
+
+NULL = None
+
+
+def test_chunk_fwd_rejects_bad_dtype():
+    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1.0,
+                  1, 64, 1, 64, 64, 64, NULL, NULL, 1, 1, 7, NULL)
+    assert rc == 1 and "dtype" in msg
+
+
+def test_chunk_fwd_rejects_unsupported_chunk():
+    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1.0,
+                  1, 64, 1, 64, 64, 48, NULL, NULL, 1, 2, 1, NULL)
+    assert rc == 2 and "chunk_size" in msg
+
+
+def test_chunk_fwd_rejects_wrong_chunk_count():
+    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1.0,
+                  2, 100, 1, 64, 64, 64, NULL, NULL, 2, 3, 1, NULL)
+    assert rc == 1 and "NC" in msg
+
+
+def test_chunk_fwd_rejects_null_buffers():
+    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1.0,
+                  1, 64, 1, 64, 64, 64, NULL, NULL, 1, 1, 1, NULL)
+    assert rc == 1 and "NULL" in msg
+
+
+def test_varlen_requires_batch_one():
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc, msg = _rc("tops_gla_chunk_fwd_h", fake, fake, fake, 0, NULL, NULL, NULL, 2, 64, 1, 64,
+                  64, 64, fake, fake, 2, 2, 1, NULL)
+    assert rc == 1 and "B == 1" in msg
+
+
+def test_lds_budget_reported():
+    rc, msg = _rc("tops_gla_chunk_fwd_o", NULL, NULL, NULL, NULL, 0, NULL, NULL, NULL, NULL,
+                  1.0, 1, 64, 1, 2048, 64, 64, NULL, NULL, 1, 1, 0, NULL)
+    assert rc == 2 and "LDS" in msg
+
+
+def test_recurrent_rejects_large_k():
+    rc, msg = _rc("tops_gla_fused_recurrent_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL,
+                  NULL, 1.0, 0, 1, 8, 1, 512, 64, NULL, 1, 1, 0, NULL)
+    assert rc == 2 and "K <= 256" in msg
+
+
+def test_cumsum_rejects_non_power_of_two():
+    rc, msg = _rc("tops_gla_chunk_local_cumsum", NULL, NULL, 1, 8, 1, 4, 12, 0, 0, 1.0, 0,
+                  NULL, NULL, 1, 1, 0, 0, NULL)
+    assert rc == 1 and "power of 2" in msg
+
+
+def test_empty_problem_is_a_no_op():
+    # zero tokens: valid, nothing launched (safe without a GPU)
+    rc, msg = _rc("tops_gla_chunk_local_cumsum", NULL, NULL, 1, 0, 1, 4, 16, 0, 0, 1.0, 0, NULL,
+                  NULL, 1, 0, 0, 0, NULL)
+    assert rc == 0 and msg == ""
+
+
+def test_python_api_refuses_cpu_tensors():
+    from tops.ops.gla import chunk_gla, fused_recurrent_gla
+
+    q = torch.randn(1, 16, 1, 8)
+    v = torch.randn(1, 16, 1, 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        chunk_gla(q, q, v, torch.zeros_like(q))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fused_recurrent_gla(q, q, v, gk=torch.zeros_like(q))
+
+
+def test_python_api_asserts_shapes_like_reference():
+    from tops.ops.gla import fused_recurrent_gla
+
+    q = torch.randn(1, 16, 2, 8)
+    with pytest.raises(AssertionError, match="Expected k shape"):
+        fused_recurrent_gla(q, q[:, :, :1], q)
+
+
+def test_seq_layout_chunk_offsets():
+    s = _lib.SeqLayout(1, 50, 16, [0, 13, 37, 50], "cpu")
+    assert (s.N, s.NC) == (3, 1 + 2 + 1)
+    assert s.chunk_cu.tolist() == [0, 1, 3, 4]
+    f = _lib.SeqLayout(3, 37, 16, None, "cpu")
+    assert (f.N, f.NC) == (3, 9) and f.cu is None

@@ -1,0 +1,316 @@
+"""GPU parity: chunked GLA (forward, backward, sub-functions) vs the numpy oracle.
+
+Inputs follow the reference's test tables (``tests/ops/gla/test_pallas_chunk_gla.py:24-126``,
+``test_pallas_chunk_bwd.py:20-80``): odd T, T=1/3, K != V, small dims, many heads, custom
+scale, h0/dht, varlen with chunk-aligned and unaligned segments, chunk sizes 16/32/64.
+Gates are ``logsigmoid(randn)`` (the reference tests' un-normalized gates) unless noted.
+Tolerances: float32 max-abs <= 1e-4; bfloat16 max-abs / max|ref| <= 2e-2 (written in
+``gla_cases``).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from gla_cases import check, make_inputs, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+torch.backends.cuda.matmul.allow_tf32 = False
+
+
+def _gla():
+    import tops.ops.gla as G
+
+    return G
+
+
+FWD_CASES = [
+    dict(B=2, T=32, H=4, K=32, V=64, seed=42),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=13, h0=True),
+    dict(B=1, T=128, H=2, K=64, V=128, seed=7),
+    dict(B=2, T=32, H=1, K=32, V=64, seed=10),
+    dict(B=2, T=32, H=4, K=16, V=128, seed=20),
+    dict(B=2, T=32, H=4, K=128, V=16, seed=21),
+    dict(B=1, T=1, H=2, K=32, V=64, seed=30),
+    dict(B=1, T=3, H=2, K=32, V=64, seed=31),
+    dict(B=2, T=37, H=4, K=16, V=32, seed=40),
+    dict(B=1, T=100, H=2, K=32, V=64, seed=42, h0=True),
+    dict(B=1, T=64, H=16, K=32, V=64, seed=60),
+    dict(B=2, T=32, H=2, K=8, V=16, seed=71, h0=True),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=200, scale=0.1),
+    dict(B=1, T=96, H=4, K=32, V=64, seed=10, cu=[0, 32, 64, 96]),
+    dict(B=1, T=48, H=4, K=32, V=64, seed=18, cu=[0, 16, 48], h0=True),
+    dict(B=1, T=50, H=2, K=16, V=32, seed=402, cu=[0, 13, 37, 50]),
+    dict(B=1, T=45, H=2, K=32, V=64, seed=404, cu=[0, 20, 45], h0=True),
+    dict(B=1, T=512, H=2, K=32, V=64, seed=304, h0=True),
+    dict(B=1, T=256, H=2, K=128, V=64, seed=351),
+    dict(B=1, T=256, H=2, K=256, V=512, seed=5, h0=True, C=64),
+    dict(B=1, T=256, H=1, K=192, V=96, seed=6, C=32),
+    # C1: fp32, B=1 T=256 H=2 K=V=64, chunk 64, g/16
+    dict(B=1, T=256, H=2, K=64, V=64, seed=1, C=64, gate_div=16.0),
+]
+
+
+def _cid(c):
+    s = f"B{c['B']}T{c['T']}H{c['H']}K{c['K']}V{c['V']}-C{c.get('C', 16)}"
+    for key in ("h0", "dht"):
+        if c.get(key):
+            s += f"-{key}"
+    if c.get("cu"):
+        s += f"-segs{len(c['cu']) - 1}"
+    if "scale" in c:
+        s += f"-s{c['scale']}"
+    return s
+
+
+def _run_fwd(cfg, dtype):
+    G = _gla()
+    cu = cfg.get("cu")
+    N = len(cu) - 1 if cu else cfg["B"]
+    q, k, v, g, s0, _, _ = make_inputs(cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"],
+                                       cfg["seed"], gate_div=cfg.get("gate_div", 1.0),
+                                       h0=cfg.get("h0", False), N=N, dtype=dtype)
+    o, ht = G.chunk_gla(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype), to_dev(g, dtype),
+                        scale=cfg.get("scale"), initial_state=to_dev(s0, "state"),
+                        output_final_state=True,
+                        cu_seqlens=None if cu is None else torch.tensor(cu),
+                        chunk_size=cfg.get("C", 16))
+    torch.cuda.synchronize()
+    on, hn = orc.naive_recurrent_gla(q, k, v, g, scale=cfg.get("scale"), initial_state=s0,
+                                     output_final_state=True, cu_seqlens=cu)
+    return to_np(o), to_np(ht), on, hn, o.dtype
+
+
+@pytest.mark.parametrize("cfg", FWD_CASES, ids=[_cid(c) for c in FWD_CASES])
+def test_chunk_gla_fwd_f32(cfg):
+    o, ht, on, hn, odt = _run_fwd(cfg, "f32")
+    assert odt == torch.float32
+    check("o", o, on, "f32")
+    check("ht", ht, hn, "f32")
+
+
+@pytest.mark.parametrize("cfg", FWD_CASES, ids=[_cid(c) for c in FWD_CASES])
+def test_chunk_gla_fwd_bf16(cfg):
+    o, ht, on, hn, odt = _run_fwd(cfg, "bf16")
+    assert odt == torch.bfloat16
+    check("o", o, on, "bf16")
+    check("ht", ht, hn, "bf16")
+
+
+def test_no_final_state_and_state_split():
+    G = _gla()
+    q, k, v, g, _, _, _ = make_inputs(1, 40, 2, 16, 32, 77)
+    d = lambda x: to_dev(x, "f32")  # noqa: E731
+    o, s = G.chunk_gla(d(q), d(k), d(v), d(g), output_final_state=False)
+    assert s is None
+    _, s_full = G.chunk_gla(d(q), d(k), d(v), d(g), output_final_state=True)
+    _, s1 = G.chunk_gla(d(q[:, :20]), d(k[:, :20]), d(v[:, :20]), d(g[:, :20]),
+                        output_final_state=True)
+    _, s2 = G.chunk_gla(d(q[:, 20:]), d(k[:, 20:]), d(v[:, 20:]), d(g[:, 20:]),
+                        initial_state=s1, output_final_state=True)
+    check("split", to_np(s2), to_np(s_full), "f32")
+
+
+BWD_CASES = [
+    dict(B=2, T=32, H=4, K=32, V=64, seed=42),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=15, h0=True, dht=True),
+    dict(B=1, T=128, H=2, K=64, V=128, seed=7, dht=True),
+    dict(B=2, T=32, H=4, K=16, V=128, seed=20, h0=True),
+    dict(B=2, T=32, H=4, K=128, V=16, seed=21),
+    dict(B=2, T=37, H=4, K=16, V=32, seed=40, dht=True),
+    dict(B=1, T=64, H=16, K=32, V=64, seed=60),
+    dict(B=2, T=32, H=2, K=8, V=16, seed=70, h0=True),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=200, scale=0.1),
+    dict(B=1, T=256, H=2, K=32, V=64, seed=303, h0=True, dht=True),
+    dict(B=2, T=64, H=4, K=32, V=64, seed=500, C=32),
+    dict(B=2, T=128, H=4, K=32, V=64, seed=502, C=64, h0=True, dht=True),
+    dict(B=1, T=48, H=4, K=32, V=64, seed=20, cu=[0, 16, 48], h0=True, dht=True),
+    dict(B=1, T=45, H=2, K=32, V=64, seed=604, cu=[0, 20, 45], h0=True, dht=True),
+    dict(B=1, T=50, H=2, K=16, V=32, seed=602, cu=[0, 13, 37, 50]),
+    dict(B=1, T=256, H=2, K=256, V=512, seed=8, C=64, h0=True, dht=True),
+    dict(B=1, T=192, H=2, K=128, V=128, seed=4, C=64, h0=True, dht=True, gate_div=16.0),
+]
+
+
+def _run_bwd(cfg, dtype):
+    G = _gla()
+    cu = cfg.get("cu")
+    N = len(cu) - 1 if cu else cfg["B"]
+    B, T, H, K, V = (cfg[x] for x in "BTHKV")
+    q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, cfg["seed"],
+                                          gate_div=cfg.get("gate_div", 1.0),
+                                          h0=cfg.get("h0", False), dht=cfg.get("dht", False),
+                                          N=N, dtype=dtype)
+    sc = cfg.get("scale")
+    tq, tk, tv, tg = (to_dev(x, dtype).requires_grad_() for x in (q, k, v, g))
+    th0 = to_dev(s0, "state")
+    if th0 is not None:
+        th0.requires_grad_()
+    o, ht = G.chunk_gla(tq, tk, tv, tg, scale=sc, initial_state=th0, output_final_state=True,
+                        cu_seqlens=None if cu is None else torch.tensor(cu),
+                        chunk_size=cfg.get("C", 16))
+    loss = (o.float() * to_dev(do, "f32")).sum()
+    if dht is not None:
+        loss = loss + (ht * to_dev(dht, "state")).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    ref = orc.chunk_gla_bwd(q, k, v, g, None, None, K ** -0.5 if sc is None else sc, s0, None,
+                            None, do, dht, cu_seqlens=cu, chunk_size=16)
+    got = [to_np(x.grad) for x in (tq, tk, tv, tg)] + [None if th0 is None else to_np(th0.grad)]
+    return got, ref
+
+
+@pytest.mark.parametrize("cfg", BWD_CASES, ids=[_cid(c) for c in BWD_CASES])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_chunk_gla_bwd(cfg, dtype):
+    got, ref = _run_bwd(cfg, dtype)
+    for name, a, b in zip(["dq", "dk", "dv", "dg", "dh0"], got, ref):
+        if a is None:
+            continue
+        # float32: the 1e-4 bar applies to values of order one; gradients summed over long
+        # chunks (dg, dh0) are compared relative to max(1, max|ref|)
+        atol = 1e-4 * max(1.0, float(np.abs(b).max())) if dtype == "f32" else None
+        check(name, a, b, dtype, atol=atol)
+
+
+# ---------------------------------------------------------------------------
+# sub-functions
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("C", [4, 16, 64])
+@pytest.mark.parametrize("reverse", [False, True])
+@pytest.mark.parametrize("varlen", [False, True])
+def test_chunk_local_cumsum(C, reverse, varlen):
+    G = _gla()
+    r = np.random.default_rng(3)
+    cu = [0, 7, 20, 70] if varlen else None
+    B = 1 if varlen else 2
+    g = r.standard_normal((B, 70, 3, 40))
+    out = G.chunk_local_cumsum(to_dev(g, "f32"), C, reverse=reverse, scale=0.5,
+                               cu_seqlens=cu)
+    ref = orc.chunk_local_cumsum(g, C, reverse=reverse, scale=0.5, cu_seqlens=cu)
+    check("cumsum", to_np(out), ref, "f32", atol=1e-5)
+    hf = G.chunk_local_cumsum(to_dev(g.transpose(0, 2, 1, 3), "f32"), C, reverse=reverse,
+                              head_first=True, cu_seqlens=cu)
+    ref2 = orc.chunk_local_cumsum(g, C, reverse=reverse, cu_seqlens=cu)
+    check("cumsum_hf", to_np(hf).transpose(0, 2, 1, 3), ref2, "f32", atol=1e-5)
+
+
+def test_fwd_subfunctions_compose():
+    """chunk_local_cumsum -> chunk_fwd_h -> intra -> o_gk reproduces the oracle's pieces."""
+    G = _gla()
+    B, T, H, K, V, C = 2, 128, 2, 64, 32, 32
+    q, k, v, g, s0, _, _ = make_inputs(B, T, H, K, V, 11, h0=True)
+    d = lambda x: to_dev(x, "f32")  # noqa: E731
+    gc = G.chunk_local_cumsum(d(g), C)
+    gc_ref = orc.chunk_local_cumsum(g, C)
+    check("g_cumsum", to_np(gc), gc_ref, "f32", atol=1e-5)
+    h, ht = G.chunk_fwd_h(d(k), d(v), gc, to_dev(s0, "state"), True, chunk_size=C)
+    h_ref, ht_ref = orc.chunk_fwd_h(k, v, gc_ref, s0, True, chunk_size=C)
+    check("h", to_np(h), h_ref, "f32")
+    check("ht", to_np(ht), ht_ref, "f32")
+    A = G.chunk_gla_fwd_intra_gk(d(q), d(k), gc, K ** -0.5, chunk_size=C)
+    A_ref = orc.chunk_gla_fwd_intra_gk(q, k, gc_ref, K ** -0.5, C)
+    check("A", to_np(A), A_ref, "f32", atol=1e-4 * max(1.0, np.abs(A_ref).max()))
+    o = G.chunk_gla_fwd_o_gk(d(q), d(v), gc, A, h, K ** -0.5, chunk_size=C)
+    o_ref = orc.chunk_gla_fwd_o_gk(q, v, gc_ref, A_ref, h_ref, K ** -0.5, C)
+    check("o", to_np(o), o_ref, "f32")
+    gcs, A2, h2, ht2, o2 = G.chunk_gla_fwd(d(q), d(k), d(v), d(g), None, None, K ** -0.5,
+                                           to_dev(s0, "state"), True, chunk_size=C)
+    check("fwd.o", to_np(o2), o_ref, "f32")
+    check("fwd.h", to_np(h2), h_ref, "f32")
+    check("fwd.ht", to_np(ht2), ht_ref, "f32")
+
+
+def test_chunk_gla_fwd_and_bwd_orchestrators_padded():
+    G = _gla()
+    B, T, H, K, V, C = 1, 45, 2, 32, 64, 16
+    cu = [0, 20, 45]
+    q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, 604, h0=True, dht=True, N=2)
+    d = lambda x: to_dev(x, "f32")  # noqa: E731
+    out = G.chunk_gla_fwd(d(q), d(k), d(v), d(g), None, None, K ** -0.5, to_dev(s0, "state"),
+                          True, cu_seqlens=cu, chunk_size=C)
+    ref = orc.chunk_gla_fwd(q, k, v, g, None, None, K ** -0.5, s0, True, cu_seqlens=cu,
+                            chunk_size=C)
+    for name, a, b in zip(["g_cumsum", "A", "h", "ht", "o"], out, ref):
+        check(name, to_np(a), b, "f32", atol=1e-4 * max(1.0, np.abs(b).max()))
+    grads = G.chunk_gla_bwd(d(q), d(k), d(v), d(g), None, None, K ** -0.5, to_dev(s0, "state"),
+                            out[2], None, d(do), to_dev(dht, "state"), cu_seqlens=cu,
+                            chunk_size=C)
+    gref = orc.chunk_gla_bwd(q, k, v, g, None, None, K ** -0.5, s0, None, None, do, dht,
+                             cu_seqlens=cu, chunk_size=C)
+    for name, a, b in zip(["dq", "dk", "dv", "dg", "dh0"], grads, gref):
+        check(name, to_np(a), b, "f32", atol=1e-4 * max(1.0, np.abs(b).max()))
+
+
+def test_g_gamma_gradient_reduced():
+    G = _gla()
+    B, T, H, K, V = 1, 48, 2, 16, 16
+    q, k, v, _, _, do, _ = make_inputs(B, T, H, K, V, 12)
+    gg = -np.abs(np.random.default_rng(1).standard_normal((H, 1))) * 0.1
+    d = lambda x: to_dev(x, "f32")  # noqa: E731
+    tgg = d(gg).requires_grad_()
+    o, _ = G.chunk_gla(d(q), d(k), d(v), g_gamma=tgg, chunk_size=16)
+    (o * d(do)).sum().backward()
+    o_ref, _ = orc.chunk_gla(q, k, v, g_gamma=gg, chunk_size=16)
+    check("o", to_np(o), o_ref, "f32")
+    _, _, _, dg_ref, _ = orc.chunk_gla_bwd(q, k, v, None, gg, None, K ** -0.5, None, None, None,
+                                           do, None, chunk_size=16)
+    check("dg_gamma", to_np(tgg.grad), dg_ref, "f32", atol=1e-4 * max(1, np.abs(dg_ref).max()))
+
+
+def test_deterministic():
+    G = _gla()
+    q, k, v, g, s0, do, _ = make_inputs(2, 200, 3, 64, 64, 9, h0=True, dtype="bf16")
+    outs = []
+    for _ in range(2):
+        tq, tk, tv, tg = (to_dev(x, "bf16").requires_grad_() for x in (q, k, v, g))
+        o, _ = G.chunk_gla(tq, tk, tv, tg, chunk_size=64)
+        (o.float() * to_dev(do, "f32")).sum().backward()
+        outs.append([o.detach().clone()] + [x.grad.clone() for x in (tq, tk, tv, tg)])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# north-star shape: per-(b, h) slices against the oracle, full-size properties
+# ---------------------------------------------------------------------------
+
+
+def test_north_star_shape_slices():
+    """C4 (B4 T8192 H16 K=V=128, bf16, chunk 64) fwd+bwd: two (b, h) slices vs the oracle,
+    plus finiteness of every output at full size."""
+    G = _gla()
+    B, T, H, K, V = 4, 8192, 16, 128, 128
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    mk = lambda *s: torch.randn(*s, generator=gen, device="cuda")  # noqa: E731
+    q, k, v = (mk(B, T, H, K).to(torch.bfloat16) for _ in range(3))
+    g = (torch.nn.functional.logsigmoid(mk(B, T, H, K)) / 16).to(torch.bfloat16)
+    h0 = mk(B, H, K, V) * 0.1
+    do = mk(B, T, H, V).to(torch.bfloat16)
+    dht = mk(B, H, K, V) * 0.1
+    tq, tk, tv, tg = (x.clone().requires_grad_() for x in (q, k, v, g))
+    th0 = h0.clone().requires_grad_()
+    o, ht = G.chunk_gla(tq, tk, tv, tg, initial_state=th0, output_final_state=True,
+                        chunk_size=64)
+    torch.autograd.backward([o, ht], [do, dht])
+    torch.cuda.synchronize()
+    for t in (o, ht, tq.grad, tk.grad, tv.grad, tg.grad, th0.grad):
+        assert torch.isfinite(t.float()).all()
+    for b, h in [(0, 0), (3, 15)]:
+        sl = lambda x: to_np(x[b:b + 1, :, h:h + 1])  # noqa: E731
+        s0 = to_np(h0[b:b + 1, h:h + 1])
+        sdt = to_np(dht[b:b + 1, h:h + 1])
+        qn, kn, vn, gn, don = (sl(x) for x in (q, k, v, g, do))
+        on, hn = orc.chunk_gla(qn, kn, vn, gn, initial_state=s0, output_final_state=True,
+                               chunk_size=64)
+        check("o", sl(o), on, "bf16")
+        check("ht", to_np(ht[b:b + 1, h:h + 1]), hn, "bf16")
+        ref = orc.chunk_gla_bwd(qn, kn, vn, gn, None, None, K ** -0.5, s0, None, None, don,
+                                sdt, chunk_size=64)
+        for name, x, r in zip(["dq", "dk", "dv", "dg"], (tq, tk, tv, tg), ref):
+            check(name, sl(x.grad), r, "bf16")
+        check("dh0", to_np(th0.grad[b:b + 1, h:h + 1]), ref[4], "bf16")

@@ -1,0 +1,132 @@
+"""GPU parity: fused_recurrent_gla and naive_recurrent_gla vs the numpy oracle.
+
+Cases mirror ``tests/ops/gla/test_pallas_fused_recurrent.py:24-174``: gate modes gk / gv /
+gk+gv / none, reverse, varlen (single-token and unaligned segments), h0, custom scale,
+long T, K != V. Output is float32 (the reference convention) for fused_recurrent_gla and the
+input dtype for naive_recurrent_gla.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from gla_cases import check, logsigmoid, round_bf16, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    dict(B=2, T=32, H=4, K=32, V=64, seed=42),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=13, h0=True),
+    dict(B=1, T=128, H=2, K=64, V=128, seed=7),
+    dict(B=2, T=32, H=4, K=16, V=128, seed=20),
+    dict(B=2, T=32, H=4, K=128, V=16, seed=21),
+    dict(B=1, T=1, H=2, K=32, V=64, seed=30),
+    dict(B=2, T=37, H=4, K=16, V=32, seed=40),
+    dict(B=2, T=32, H=2, K=8, V=16, seed=71, h0=True),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=100, gate="gv"),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=101, gate="gk+gv"),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=102, gate="none"),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=111, reverse=True, h0=True),
+    dict(B=1, T=1, H=2, K=16, V=32, seed=112, reverse=True),
+    dict(B=2, T=32, H=4, K=32, V=64, seed=200, scale=0.1),
+    dict(B=1, T=23, H=2, K=16, V=32, seed=12, cu=[0, 7, 20, 23]),
+    dict(B=1, T=48, H=4, K=32, V=64, seed=18, cu=[0, 10, 24, 48], h0=True),
+    dict(B=1, T=4, H=2, K=16, V=32, seed=20, cu=[0, 1, 2, 3, 4]),
+    dict(B=1, T=23, H=2, K=16, V=32, seed=121, cu=[0, 7, 20, 23], reverse=True),
+    dict(B=1, T=32, H=4, K=32, V=64, seed=131, gate="gk+gv", cu=[0, 16, 32]),
+    dict(B=1, T=1024, H=2, K=32, V=64, seed=302),
+    dict(B=1, T=256, H=4, K=32, V=64, seed=380, gate="gk+gv", h0=True, reverse=True,
+         scale=0.1),
+    dict(B=1, T=256, H=2, K=256, V=512, seed=2, h0=True, gate_div=16.0),
+    dict(B=1, T=64, H=2, K=200, V=70, seed=3),
+]
+
+
+def _cid(c):
+    s = f"B{c['B']}T{c['T']}H{c['H']}K{c['K']}V{c['V']}-{c.get('gate', 'gk')}"
+    for key in ("h0", "reverse"):
+        if c.get(key):
+            s += f"-{key}"
+    if c.get("cu"):
+        s += f"-segs{len(c['cu']) - 1}"
+    return s
+
+
+def _inputs(cfg, dtype):
+    r = np.random.default_rng(cfg["seed"])
+    B, T, H, K, V = (cfg[x] for x in "BTHKV")
+    gate = cfg.get("gate", "gk")
+    div = cfg.get("gate_div", 1.0)
+    q, k = r.standard_normal((2, B, T, H, K))
+    v = r.standard_normal((B, T, H, V))
+    gk = logsigmoid(r.standard_normal((B, T, H, K))) / div if "gk" in gate else None
+    gv = logsigmoid(r.standard_normal((B, T, H, V))) / div if "gv" in gate else None
+    cu = cfg.get("cu")
+    N = len(cu) - 1 if cu else B
+    s0 = r.standard_normal((N, H, K, V)) if cfg.get("h0") else None
+    if dtype == "bf16":
+        q, k, v = (round_bf16(x) for x in (q, k, v))
+        gk = None if gk is None else round_bf16(gk)
+        gv = None if gv is None else round_bf16(gv)
+    return q, k, v, gk, gv, s0, cu
+
+
+@pytest.mark.parametrize("cfg", CASES, ids=[_cid(c) for c in CASES])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_fused_recurrent(cfg, dtype):
+    import tops.ops.gla as G
+
+    q, k, v, gk, gv, s0, cu = _inputs(cfg, dtype)
+    d = lambda x: to_dev(x, dtype)  # noqa: E731
+    o, ht = G.fused_recurrent_gla(d(q), d(k), d(v), gk=d(gk), gv=d(gv), scale=cfg.get("scale"),
+                                  initial_state=to_dev(s0, "state"), output_final_state=True,
+                                  reverse=cfg.get("reverse", False),
+                                  cu_seqlens=None if cu is None else torch.tensor(cu))
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float32 and ht.dtype == torch.float32
+    on, hn = orc.fused_recurrent_gla(q, k, v, gk=gk, gv=gv, scale=cfg.get("scale"),
+                                     initial_state=s0, output_final_state=True,
+                                     reverse=cfg.get("reverse", False), cu_seqlens=cu)
+    # the recurrent kernel computes in fp32 from the (bf16-rounded) inputs: hold both dtypes
+    # to the fp32 bar, relative to the output magnitude for long accumulations
+    check("o", to_np(o), on, "f32", atol=1e-4 * max(1.0, float(np.abs(on).max())))
+    check("ht", to_np(ht), hn, "f32", atol=1e-4 * max(1.0, float(np.abs(hn).max())))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_naive_recurrent(dtype):
+    import tops.ops.gla as G
+
+    cfg = dict(B=1, T=50, H=2, K=32, V=64, seed=41, h0=True, cu=[0, 13, 50])
+    q, k, v, gk, _, s0, cu = _inputs(cfg, dtype)
+    d = lambda x: to_dev(x, dtype)  # noqa: E731
+    o, ht = G.naive_recurrent_gla(d(q), d(k), d(v), d(gk), initial_state=to_dev(s0, "state"),
+                                  output_final_state=True, cu_seqlens=cu)
+    assert o.dtype == (torch.float32 if dtype == "f32" else torch.bfloat16)
+    on, hn = orc.naive_recurrent_gla(q, k, v, gk, initial_state=s0, output_final_state=True,
+                                     cu_seqlens=cu)
+    check("o", to_np(o), on, dtype)
+    check("ht", to_np(ht), hn, "f32")
+
+
+def test_fused_recurrent_c2_shape_slices():
+    """C2 (B8 T2048 H4 K256 V512, bf16, h0, output_final_state): slices vs the oracle."""
+    import tops.ops.gla as G
+
+    B, T, H, K, V = 8, 2048, 4, 256, 512
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    mk = lambda *s: torch.randn(*s, generator=gen, device="cuda")  # noqa: E731
+    q, k = (mk(B, T, H, K).to(torch.bfloat16) for _ in range(2))
+    v = mk(B, T, H, V).to(torch.bfloat16)
+    gk = (torch.nn.functional.logsigmoid(mk(B, T, H, K)) / 16).to(torch.bfloat16)
+    h0 = mk(B, H, K, V) * 0.1
+    o, ht = G.fused_recurrent_gla(q, k, v, gk=gk, initial_state=h0, output_final_state=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all() and torch.isfinite(ht).all()
+    for b, h in [(0, 0), (7, 3)]:
+        sl = lambda x: to_np(x[b:b + 1, :256, h:h + 1])  # noqa: E731
+        on, _ = orc.fused_recurrent_gla(sl(q), sl(k), sl(v), gk=sl(gk),
+                                        initial_state=to_np(h0[b:b + 1, h:h + 1]),
+                                        output_final_state=False)
+        check("o[:256]", sl(o), on, "f32", atol=1e-4 * max(1.0, float(np.abs(on).max())))
