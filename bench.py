@@ -11,7 +11,7 @@ Prints ONE JSON line with the driver's fields plus
                  torch's current stream (the stream the C ABI launches on) with HIP events,
                  against the HBM roofline with its algorithmic bytes per launch;
   cpu_baseline : the numpy oracle (float32, one thread) on a bounded sample of the same
-                 workload (1 batch row, 8 of the 16 heads, full T), scaled to tokens/s of
+                 workload (1 batch row, all 16 heads, full T), scaled to tokens/s of
                  the whole workload;
   kernels      : every kernel's average duration and achieved GB/s.
 """
@@ -58,6 +58,19 @@ def _inputs(device):
     bf = lambda x: torch.from_numpy(x).to(device).to(torch.bfloat16)  # noqa: E731
     fp = lambda x: torch.from_numpy(x).to(device)  # noqa: E731
     return dict(q=bf(q), k=bf(k), v=bf(v), g=bf(g), h0=fp(h0), do=bf(do), dht=fp(dht))
+
+
+def _copy_calibration(device, mib=512, reps=3):
+    """Plain device copy of a known size: the HBM-counter calibration point for rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE runs (bytes read = bytes written = mib MiB per dispatch)."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize(device)
 
 
 def _kernel_profile(x, reps=10):
@@ -114,7 +127,18 @@ def _kernel_profile(x, reps=10):
     return res
 
 
-def _cpu_baseline(heads=8):
+def _measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed, copy-calibrated rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["bytes_per_launch"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def _cpu_baseline(heads=16):
     """Float32 numpy oracle (single thread) on B=1, `heads` heads, full T; scaled to the
     whole workload's tokens/s."""
     import numpy as np
@@ -162,7 +186,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-profile", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=8)
+    ap.add_argument("--cpu-heads", type=int, default=16)
+    ap.add_argument("--profile-reps", type=int, default=10)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 512 MiB device copy (counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the GLA path shards over batch and "
@@ -215,13 +242,16 @@ def main():
         "mfma_frac": round(FLOPS_STEP / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
     }
     if not a.no_kernel_profile:
-        prof = _kernel_profile(x)
+        prof = _kernel_profile(x, max(1, a.profile_reps))
         dom = max(prof, key=lambda n: prof[n]["ms"])
         d = prof[dom]
         out["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": d["gbs"],
                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}
+                           "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
+                           "traffic": _measured_traffic(dom)}
         out["kernels"] = prof
+    if a.calibrate_copy:
+        _copy_calibration(dev)
     if not a.no_cpu_baseline:
         out["cpu_baseline"] = _cpu_baseline(a.cpu_heads)
     print(json.dumps(out), flush=True)
