@@ -94,12 +94,9 @@ def _kernel_profile(x, reps=10):
     tok = B * T * H
     hbytes = seq.NC * H * K * V * BF
     kernels = {
-        "state_scan_fwd": (lambda: call("tops_gla_chunk_fwd_h", ptr(k), ptr(v), ptr(g), 0,
-                                        ptr(h0), ptr(h), ptr(ht), *lay),
-                           tok * (2 * K + V) * BF + STATE_BYTES * 2 + hbytes),
-        "chunk_fwd_o": (lambda: call("tops_gla_chunk_fwd_o", ptr(q), ptr(k), ptr(v), ptr(g), 0,
-                                     ptr(h), None, None, ptr(o), sc, *lay),
-                        tok * (3 * K + 2 * V) * BF + hbytes),
+        "chunk_fwd_fused": (lambda: call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g),
+                                         ptr(h0), ptr(o), ptr(ht), ptr(h), sc, *lay),
+                            tok * (3 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes),
         "state_scan_bwd": (lambda: call("tops_gla_chunk_bwd_dh", ptr(q), ptr(g), 0, ptr(do),
                                         ptr(dht), ptr(dh), ptr(dh0), sc, *lay),
                            tok * (2 * K + V) * BF + STATE_BYTES * 2 + hbytes),

@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <initializer_list>
+
 #include "../../include/tops_gla.h"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -31,6 +33,18 @@ int hip_status(hipError_t e, const char* what) {
 }
 
 bool dtype_ok(int d) { return d == TOPS_GLA_F32 || d == TOPS_GLA_BF16; }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// 16-byte vector access is valid when K and V rows are whole 16-byte pieces and every
+// base pointer is 16-byte aligned (NULL counts as aligned).
+int vec_ok(int dtype, int64_t K, int64_t V, std::initializer_list<const void*> ptrs) {
+  const int epp = dtype == TOPS_GLA_BF16 ? 8 : 4;
+  if (K % epp != 0 || V % epp != 0) return 0;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return 0;
+  return 1;
+}
 
 constexpr int64_t kMaxInt = 2147483647;
 
@@ -155,6 +169,7 @@ int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_c
   p.H = (int)H;
   p.K = (int)K;
   p.V = (int)V;
+  p.vec = vec_ok(dtype, K, V, {k, v, g, h});
   p.si = si;
   return hip_status(tops::run_state_scan(p, false, dtype, (hipStream_t)stream), "chunk_fwd_h");
 }
@@ -183,6 +198,7 @@ int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const v
   p.H = (int)H;
   p.K = (int)K;
   p.V = (int)V;
+  p.vec = vec_ok(dtype, K, V, {q, dout, g, dh});
   p.si = si;
   return hip_status(tops::run_state_scan(p, true, dtype, (hipStream_t)stream), "chunk_bwd_dh");
 }
@@ -237,6 +253,26 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
                     o == nullptr || h_ws == nullptr))
     return fail(TOPS_GLA_EINVAL, "q, k, v, g, o and h_ws must not be NULL");
   hipStream_t st = (hipStream_t)stream;
+  if (tops::fused_fwd_supported(dtype, chunk_size, (int)K)) {
+    tops::FusedFwdArgs f;
+    f.q = q;
+    f.k = k;
+    f.v = v;
+    f.g = g;
+    f.h0 = h0;
+    f.o = o;
+    f.h_out = h_ws;
+    f.ht = ht;
+    f.scale = scale;
+    f.H = (int)H;
+    f.K = (int)K;
+    f.V = (int)V;
+    const int epp = dtype == TOPS_GLA_BF16 ? 8 : 4;
+    f.vec_k = (K % epp == 0) && aligned16(q) && aligned16(k) && aligned16(g);
+    f.vec_v = (V % epp == 0) && aligned16(v) && aligned16(o) && aligned16(h_ws);
+    f.si = si;
+    return hip_status(tops::run_chunk_fwd_fused(f, dtype, st), "chunk_fwd (fused)");
+  }
   tops::ScanArgs s;
   s.a = k;
   s.b = v;
@@ -249,6 +285,7 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
   s.H = (int)H;
   s.K = (int)K;
   s.V = (int)V;
+  s.vec = vec_ok(dtype, K, V, {k, v, g, h_ws});
   s.si = si;
   rc = hip_status(tops::run_state_scan(s, false, dtype, st), "chunk_fwd (state scan)");
   if (rc) return rc;
@@ -302,6 +339,7 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     s.H = (int)H;
     s.K = (int)K;
     s.V = (int)V;
+    s.vec = vec_ok(dtype, K, V, {k, v, g, h_ws});
     s.si = si;
     rc = hip_status(tops::run_state_scan(s, false, dtype, st), "chunk_bwd (state recompute)");
     if (rc) return rc;
@@ -319,6 +357,7 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   d.H = (int)H;
   d.K = (int)K;
   d.V = (int)V;
+  d.vec = vec_ok(dtype, K, V, {q, dout, g, dh_ws});
   d.si = si;
   rc = hip_status(tops::run_state_scan(d, true, dtype, st), "chunk_bwd (dh scan)");
   if (rc) return rc;

@@ -8,107 +8,205 @@
 // value at the chunk's last row.
 //
 // One 256-thread block owns a 64(k) x 64(v) tile of the K x V state of one (sequence,
-// head) and walks that sequence's chunks in order (reverse order for dh). The state stays
-// in MFMA accumulators: wave w holds v rows [16w, 16w+16) x all 64 k columns as four
-// 16x16 tiles, orientation out[v][k] = sum_c X[v][c] Y[k][c] with X = b^T and Y = gated a^T,
-// so a lane's four accumulator values are four consecutive v of one k: they are stored to
-// the [.., K, V] state layout as one vector.
+// head) and walks that sequence's chunks in order (reverse order for dh):
+//  * the raw a (k or q), g and b (v or do) tiles of chunk n+1 are fetched with 16-byte loads
+//    into registers while chunk n computes, then written to LDS;
+//  * thread = two adjacent columns x C/8 rows: column cumsum, gating and the transposes
+//    (a^T gated, b^T) are written as whole runs of rows;
+//  * the state stays in MFMA accumulators: wave w holds v rows [16w, 16w+16) x all 64 k
+//    columns as four 16x16 tiles (out[v][k] = sum_c b^T[v][c] a^T[k][c]), so a lane's four
+//    values are four consecutive v of one k and go to the [.., K, V] layout as one vector.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace tops {
 
-template <typename T, int C, bool REV>
-__global__ __launch_bounds__(256) void state_scan_kernel(
-    const T* __restrict__ a,         // forward: k ; reverse: q        [tokens, H, K]
-    const T* __restrict__ b,         // forward: v ; reverse: do       [tokens, H, V]
-    const T* __restrict__ g,         // raw gates (or cumsum)          [tokens, H, K]
-    int g_is_cumsum,
-    const float* __restrict__ s_init,  // forward: h0 ; reverse: dht  [N, H, K, V] or null
-    T* __restrict__ s_all,             // per-chunk states [NC, H, K, V] or null
-    float* __restrict__ s_final,       // forward: ht ; reverse: dh0  [N, H, K, V] or null
-    float scale, int H, int K, int V, SeqInfo si) {
-  constexpr int CP = C < 32 ? 32 : C;  // contraction length (zero padded)
-  constexpr int PC = pitch_of<T>(CP);
-  constexpr int RPS = C / 4;
+template <typename T, int C, bool REV, bool VEC>
+__global__ __launch_bounds__(256) void state_scan_kernel(ScanArgs p) {
+  constexpr int CP = C < 32 ? 32 : C;     // contraction length (zero padded)
+  constexpr int PC = pitch_of<T>(CP);     // transposed operands [64][CP]
+  constexpr int PR = pitch_of<T>(64);     // raw tiles [C][64]
+  constexpr int EPP = 16 / (int)sizeof(T);
+  constexpr int PPR = 64 / EPP;           // 16-byte pieces per raw row
+  constexpr int NP = C * PPR;
+  constexpr int PPT = (NP + 255) / 256;
+  constexpr int NSEG = 8;                 // 32 column pairs x 8 row segments
+  constexpr int RPS = C / NSEG;
+  __shared__ __attribute__((aligned(16))) T sAr[C * PR];
+  __shared__ __attribute__((aligned(16))) T sGr[C * PR];
+  __shared__ __attribute__((aligned(16))) T sBr[C * PR];
   __shared__ __attribute__((aligned(16))) T sXT[64 * PC];  // gated a^T  [k][c]
   __shared__ __attribute__((aligned(16))) T sBT[64 * PC];  // b^T        [v][c]
   __shared__ float sGam[64];
-  __shared__ float sTot[4 * 64];
+  __shared__ float sTot[NSEG * 64];
 
+  const T* __restrict__ a = (const T*)p.a;
+  const T* __restrict__ b = (const T*)p.b;
+  const T* __restrict__ g = (const T*)p.g;
+  T* __restrict__ s_all = (T*)p.s_all;
+  const int H = p.H, K = p.K, V = p.V;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int KT = (K + 63) >> 6, VT = (V + 63) >> 6;
-  const int total = gridDim.x;
-  const int L = xcd_remap(blockIdx.x, total);
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int vt = L % VT;
   const int kt = (L / VT) % KT;
   const int bh = L / (VT * KT);
   const int seq = bh / H, hh = bh % H;
+  const int kbase = kt * 64, vbase = vt * 64;
 
   int bos, eos, c0, nc;
-  seq_range(si, seq, bos, eos, c0, nc);
+  seq_range(p.si, seq, bos, eos, c0, nc);
 
-  // zero the contraction padding [C, CP) once; chunk writes only touch [0, C)
-  if (CP > C) {
-    for (int i = tid; i < 64 * (CP - C); i += 256) {
-      const int r = i / (CP - C), cc = C + i % (CP - C);
-      sXT[r * PC + cc] = zero_elem<T>();
-      sBT[r * PC + cc] = zero_elem<T>();
-    }
+  for (int i = tid; i < 64 * PC; i += 256) {
+    sXT[i] = zero_elem<T>();
+    sBT[i] = zero_elem<T>();
   }
 
   // accumulator element -> (k, v)
-  const int kcol = kt * 64 + (lane & 15);  // + 16*n
-  const int vrow = vt * 64 + w * 16 + 4 * (lane >> 4);  // + r
+  const int kcol = kbase + (lane & 15);                 // + 16*n
+  const int vrow = vbase + w * 16 + 4 * (lane >> 4);    // + r
   f32x4 acc[4];
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     acc[n] = zero4();
-    if (s_init) {
-      const int kk = kcol + 16 * n;
+    const int kk = kcol + 16 * n;
+    if (p.s_init && kk < K) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int vv = vrow + r;
-        if (kk < K && vv < V)
-          acc[n][r] = s_init[(((long)seq * H + hh) * K + kk) * V + vv];
-      }
+      for (int r = 0; r < 4; ++r)
+        if (vrow + r < V) acc[n][r] = p.s_init[(((long)seq * H + hh) * K + kk) * V + vrow + r];
     }
   }
 
-  // prologue mapping: column `col` of the tile, rows [seg*RPS, +RPS)
-  const int col = tid & 63, seg = tid >> 6;
-  const int gk_col = kt * 64 + col, gv_col = vt * 64 + col;
-  const bool kvalid = gk_col < K, vvalid = gv_col < V;
-  const long rsK = (long)H * K, rsV = (long)H * V;
+  uint4 pa[PPT], pg[PPT], pb[PPT];
+  auto issue = [&](int step) {
+    const int ci = REV ? (nc - 1 - step) : step;
+    const int t0 = bos + ci * C;
+    const int len = min(C, eos - t0);
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pc = tid + 256 * j;
+      pa[j] = pg[j] = pb[j] = make_uint4(0, 0, 0, 0);
+      if (pc < NP) {
+        const int row = pc / PPR, col0 = (pc % PPR) * EPP;
+        if (row < len) {
+          const long rk = ((long)(t0 + row) * H + hh) * K + kbase;
+          const long rv = ((long)(t0 + row) * H + hh) * V + vbase;
+          pa[j] = gload16<T, VEC>(a + rk, col0, K - kbase - col0);
+          pg[j] = gload16<T, VEC>(g + rk, col0, K - kbase - col0);
+          pb[j] = gload16<T, VEC>(b + rv, col0, V - vbase - col0);
+        }
+      }
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pc = tid + 256 * j;
+      if (pc < NP) {
+        const int row = pc / PPR, col0 = (pc % PPR) * EPP;
+        *reinterpret_cast<uint4*>(sAr + row * PR + col0) = pa[j];
+        *reinterpret_cast<uint4*>(sGr + row * PR + col0) = pg[j];
+        *reinterpret_cast<uint4*>(sBr + row * PR + col0) = pb[j];
+      }
+    }
+  };
+  if (nc > 0) {
+    issue(0);
+    commit();
+    if (nc > 1) issue(1);
+  }
+  __syncthreads();
+
+  const int cp = tid & 31, seg = tid >> 5;   // columns 2cp, 2cp+1 ; rows [seg*RPS, +RPS)
+  const int c_0 = 2 * cp, c_1 = 2 * cp + 1;
+  const bool gcum = p.g_is_cumsum != 0;
 
   for (int step = 0; step < nc; ++step) {
     const int ci = REV ? (nc - 1 - step) : step;
     const int t0 = bos + ci * C;
     const int len = min(C, eos - t0);
-    const long baseK = ((long)t0 * H + hh) * K;
-    const long baseV = ((long)t0 * H + hh) * V;
 
-    float gt[RPS];
-    float gamma, first;
-    tile_cumsum<C>(g + baseK + gk_col, rsK, len, kvalid, g_is_cumsum != 0, sTot, gt, gamma,
-                   first);
-    (void)first;
+    // ---- column cumsum (or given cumsum) ----
+    float g0[RPS], g1[RPS];
+    float run0 = 0.f, run1 = 0.f;
 #pragma unroll
-    for (int r = 0; r < RPS; ++r) {
-      const int row = seg * RPS + r;
-      float x = 0.f, y = 0.f;
-      if (row < len) {
-        if (kvalid) x = to_f32(a[baseK + (long)row * rsK + gk_col]);
-        if (vvalid) y = to_f32(b[baseV + (long)row * rsV + gv_col]);
+    for (int rr = 0; rr < RPS; ++rr) {
+      float x0, x1;
+      Pair<T>::ld(sGr + (seg * RPS + rr) * PR + c_0, x0, x1);
+      if (gcum) {
+        g0[rr] = x0;
+        g1[rr] = x1;
+      } else {
+        run0 += x0;
+        run1 += x1;
+        g0[rr] = run0;
+        g1[rr] = run1;
       }
-      const float f = REV ? scale * gexp<T>(gt[r]) : gexp<T>(gamma - gt[r]);
-      sXT[col * PC + row] = from_f32<T>(x * f);
-      sBT[col * PC + row] = from_f32<T>(y);
     }
-    if (seg == 0) sGam[col] = gexp<T>(gamma);
+    if (gcum) {
+      // gamma = given value at the last valid row
+      const int lr = len - 1;
+      if (lr >= seg * RPS && lr < seg * RPS + RPS) {
+#pragma unroll
+        for (int rr = 0; rr < RPS; ++rr)
+          if (seg * RPS + rr == lr) {
+            sTot[c_0] = g0[rr];
+            sTot[c_1] = g1[rr];
+          }
+      }
+    } else {
+      sTot[seg * 64 + c_0] = run0;
+      sTot[seg * 64 + c_1] = run1;
+    }
+    __syncthreads();
+    float off0 = 0.f, off1 = 0.f, gam0 = 0.f, gam1 = 0.f;
+    if (gcum) {
+      gam0 = sTot[c_0];
+      gam1 = sTot[c_1];
+    } else {
+#pragma unroll
+      for (int s = 0; s < NSEG; ++s) {
+        const float x0 = sTot[s * 64 + c_0], x1 = sTot[s * 64 + c_1];
+        off0 += (s < seg) ? x0 : 0.f;
+        off1 += (s < seg) ? x1 : 0.f;
+        gam0 += x0;
+        gam1 += x1;
+      }
+    }
+
+    // ---- gated a^T and b^T, written as row runs ----
+    float xa0[RPS], xa1[RPS], xb0[RPS], xb1[RPS];
+#pragma unroll
+    for (int rr = 0; rr < RPS; ++rr) {
+      const int row = seg * RPS + rr;
+      float a0, a1, b0, b1;
+      Pair<T>::ld(sAr + row * PR + c_0, a0, a1);
+      Pair<T>::ld(sBr + row * PR + c_0, b0, b1);
+      float e0, e1;
+      if (REV) {
+        e0 = p.scale * gexp<T>(g0[rr] + off0);
+        e1 = p.scale * gexp<T>(g1[rr] + off1);
+      } else {
+        e0 = gexp<T>(gam0 - (g0[rr] + off0));
+        e1 = gexp<T>(gam1 - (g1[rr] + off1));
+      }
+      if (gcum && row >= len) e0 = e1 = 0.f;
+      xa0[rr] = a0 * e0;
+      xa1[rr] = a1 * e1;
+      xb0[rr] = b0;
+      xb1[rr] = b1;
+    }
+    store_run<T, RPS>(sXT + c_0 * PC + seg * RPS, xa0);
+    store_run<T, RPS>(sXT + c_1 * PC + seg * RPS, xa1);
+    store_run<T, RPS>(sBT + c_0 * PC + seg * RPS, xb0);
+    store_run<T, RPS>(sBT + c_1 * PC + seg * RPS, xb1);
+    if (seg == 0) {
+      sGam[c_0] = gexp<T>(gam0);
+      sGam[c_1] = gexp<T>(gam1);
+    }
     __syncthreads();
 
-    // store the state entering this chunk (forward) / leaving it (reverse)
+    // ---- state entering this chunk (forward) / leaving it (reverse) ----
     if (s_all) {
       const long cbase = ((long)(c0 + ci) * H + hh) * K;
 #pragma unroll
@@ -116,14 +214,10 @@ __global__ __launch_bounds__(256) void state_scan_kernel(
         const int kk = kcol + 16 * n;
         if (kk >= K) continue;
         T* dst = s_all + (cbase + kk) * V + vrow;
-        if (vrow + 3 < V && (V & 3) == 0) {
-          if (sizeof(T) == 2) {
-            uint2 pk;
-            pk.x = (uint32_t)from_f32<bf16>(acc[n][0]).u |
-                   ((uint32_t)from_f32<bf16>(acc[n][1]).u << 16);
-            pk.y = (uint32_t)from_f32<bf16>(acc[n][2]).u |
-                   ((uint32_t)from_f32<bf16>(acc[n][3]).u << 16);
-            *reinterpret_cast<uint2*>(dst) = pk;
+        if (VEC && vrow + 3 < V) {
+          if constexpr (sizeof(T) == 2) {
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(pack2_bf16(acc[n][0], acc[n][1]), pack2_bf16(acc[n][2], acc[n][3]));
           } else {
             *reinterpret_cast<float4*>(dst) =
                 make_float4(acc[n][0], acc[n][1], acc[n][2], acc[n][3]);
@@ -135,22 +229,25 @@ __global__ __launch_bounds__(256) void state_scan_kernel(
         }
       }
     }
-
+    // raw tiles are free now: stage the next chunk, fetch the one after
+    if (step + 1 < nc) {
+      commit();
+      if (step + 2 < nc) issue(step + 2);
+    }
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      const float d = sGam[n * 16 + (lane & 15)];
-      acc[n] *= d;
+      acc[n] *= sGam[n * 16 + (lane & 15)];
       mma_tile<T>(acc[n], sBT + (w * 16) * PC, PC, sXT + (n * 16) * PC, PC, CP, lane);
     }
     __syncthreads();
   }
 
-  if (s_final) {
+  if (p.s_final) {
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const int kk = kcol + 16 * n;
       if (kk >= K) continue;
-      float* dst = s_final + (((long)seq * H + hh) * K + kk) * V + vrow;
+      float* dst = p.s_final + (((long)seq * H + hh) * K + kk) * V + vrow;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         if (vrow + r < V) dst[r] = acc[n][r];
@@ -163,9 +260,12 @@ static hipError_t launch_scan(const ScanArgs& p, hipStream_t st) {
   const int KT = (p.K + 63) / 64, VT = (p.V + 63) / 64;
   const long blocks = (long)p.si.N * p.H * KT * VT;
   if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL((state_scan_kernel<T, C, REV>), dim3((unsigned)blocks), dim3(256), 0, st,
-                     (const T*)p.a, (const T*)p.b, (const T*)p.g, p.g_is_cumsum, p.s_init,
-                     (T*)p.s_all, p.s_final, p.scale, p.H, p.K, p.V, p.si);
+  if (p.vec)
+    hipLaunchKernelGGL((state_scan_kernel<T, C, REV, true>), dim3((unsigned)blocks), dim3(256),
+                       0, st, p);
+  else
+    hipLaunchKernelGGL((state_scan_kernel<T, C, REV, false>), dim3((unsigned)blocks),
+                       dim3(256), 0, st, p);
   return hipGetLastError();
 }
 

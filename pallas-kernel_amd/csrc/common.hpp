@@ -35,17 +35,21 @@ __device__ __forceinline__ float from_f32<float>(float f) {
 }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float f) {
-  // round to nearest even; NaN stays a (quiet) NaN
-  uint32_t u = __float_as_uint(f);
+  // gfx950 v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN
   bf16 r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    r.u = 0x7fc0;
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);
-    r.u = (uint16_t)(u >> 16);
-  }
+  r.u = __builtin_bit_cast(uint16_t, (__bf16)f);
   return r;
 }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bf16 in one 32-bit word (element a in the low half), one instruction.
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 template <typename T>
 __device__ __forceinline__ T zero_elem() {
@@ -135,6 +139,79 @@ __device__ __forceinline__ f32x4 zero4() {
 template <typename T>
 __host__ __device__ constexpr int pitch_of(int w) {
   return w + (int)(16 / sizeof(T));
+}
+
+// ---------------------------------------------------------------------------
+// Element pairs (two adjacent columns) and short vector runs in LDS
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Pair;
+template <>
+struct Pair<bf16> {
+  static __device__ __forceinline__ void ld(const bf16* p, float& a, float& b) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+    a = bf16_lo(w);
+    b = bf16_hi(w);
+  }
+  static __device__ __forceinline__ void st(bf16* p, float a, float b) {
+    *reinterpret_cast<uint32_t*>(p) = pack2_bf16(a, b);
+  }
+};
+template <>
+struct Pair<float> {
+  static __device__ __forceinline__ void ld(const float* p, float& a, float& b) {
+    const float2 w = *reinterpret_cast<const float2*>(p);
+    a = w.x;
+    b = w.y;
+  }
+  static __device__ __forceinline__ void st(float* p, float a, float b) {
+    *reinterpret_cast<float2*>(p) = make_float2(a, b);
+  }
+};
+
+// Store N consecutive values (N in {2, 4, 8}, dst aligned to N elements) as wide writes.
+template <typename T, int N>
+__device__ __forceinline__ void store_run(T* dst, const float (&x)[N]) {
+  if constexpr (sizeof(T) == 2) {
+    uint32_t w[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) w[i] = pack2_bf16(x[2 * i], x[2 * i + 1]);
+    if constexpr (N == 8) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else if constexpr (N == 4) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+    } else {
+      *reinterpret_cast<uint32_t*>(dst) = w[0];
+    }
+  } else {
+    if constexpr (N == 8) {
+      reinterpret_cast<float4*>(dst)[0] = make_float4(x[0], x[1], x[2], x[3]);
+      reinterpret_cast<float4*>(dst)[1] = make_float4(x[4], x[5], x[6], x[7]);
+    } else if constexpr (N == 4) {
+      *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
+    } else {
+      *reinterpret_cast<float2*>(dst) = make_float2(x[0], x[1]);
+    }
+  }
+}
+
+// 16 bytes of a global row starting at column col0, zero-filled past `nvalid` columns.
+// VEC: the row start and col0 are 16-byte aligned (only the tail check remains).
+template <typename T, bool VEC>
+__device__ __forceinline__ uint4 gload16(const T* __restrict__ row, int col0, int nvalid) {
+  constexpr int EPP = 16 / (int)sizeof(T);
+  uint4 r = make_uint4(0, 0, 0, 0);
+  if (VEC) {
+    if (nvalid >= EPP) r = *reinterpret_cast<const uint4*>(row + col0);
+    return r;
+  }
+  if (nvalid > 0) {
+    T tmp[EPP];
+#pragma unroll
+    for (int e = 0; e < EPP; ++e) tmp[e] = e < nvalid ? row[col0 + e] : zero_elem<T>();
+    __builtin_memcpy(&r, tmp, 16);
+  }
+  return r;
 }
 
 // ---------------------------------------------------------------------------

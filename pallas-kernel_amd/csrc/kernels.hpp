@@ -20,6 +20,7 @@ struct ScanArgs {
   float* s_final;       // forward: ht ; reverse: dh0 (nullable)
   float scale;          // reverse only
   int H, K, V;
+  int vec;              // 16-byte loads/stores allowed (K, V multiples of 16 B, aligned)
   SeqInfo si;
 };
 hipError_t run_state_scan(const ScanArgs& p, bool reverse, int dtype, hipStream_t st);
@@ -37,6 +38,22 @@ struct FwdOArgs {
   SeqInfo si;
 };
 hipError_t run_chunk_fwd_o(const FwdOArgs& p, int dtype, hipStream_t st);
+
+// Fused forward: state scan + output in one sequential pass (chunk_fwd_fused.hip).
+struct FusedFwdArgs {
+  const void *q, *k, *v, *g;
+  const float* h0;      // [N, H, K, V] or null
+  void* o;              // [tokens, H, V]
+  void* h_out;          // [NC, H, K, V] states entering each chunk (nullable)
+  float* ht;            // [N, H, K, V] or null
+  float scale;
+  int H, K, V;
+  int vec_k, vec_v;     // 16-byte loads/stores allowed for K- / V-rows
+  SeqInfo si;
+};
+// True when the fused forward handles (dtype, C, K); otherwise use run_state_scan+run_chunk_fwd_o.
+bool fused_fwd_supported(int dtype, int C, int K);
+hipError_t run_chunk_fwd_fused(const FusedFwdArgs& p, int dtype, hipStream_t st);
 
 // Per-chunk gradients (chunk_bwd.hip).
 struct BwdArgs {
