@@ -377,6 +377,7 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   p.H = (int)H;
   p.K = (int)K;
   p.V = (int)V;
+  p.vec = vec_ok(dtype, K, V, {q, k, v, g, dout, h, dh_ws, dq, dk, dv, dg});
   p.si = si;
   return hip_status(tops::run_chunk_bwd(p, dtype, st), "chunk_bwd (gradients)");
 }
@@ -412,6 +413,7 @@ int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const v
   p.H = (int)H;
   p.K = (int)K;
   p.V = (int)V;
+  p.vec = vec_ok(dtype, K, V, {q, k, v, g, h, dout, dh, dq, dk, dg});
   p.si = si;
   return hip_status(tops::run_chunk_bwd(p, dtype, (hipStream_t)stream, 1), "chunk_bwd_dqkg");
 }
@@ -443,6 +445,7 @@ int tops_gla_chunk_bwd_dv(const void* q, const void* k, const void* g, const voi
   p.H = (int)H;
   p.K = (int)K;
   p.V = (int)V;
+  p.vec = vec_ok(dtype, K, V, {q, k, g, dout, dh, dv});
   p.si = si;
   return hip_status(tops::run_chunk_bwd(p, dtype, (hipStream_t)stream, 2), "chunk_bwd_dv");
 }

@@ -7,62 +7,150 @@
 //   dA  = scale tril(do v^T)
 //   dq  = e^{g~-r} [ dA (k e^{r-g~}) + (scale e^{r}) do h^T ]
 //   dk  = e^{r-g~} [ dA^T (q e^{g~-r}) + e^{gamma-r} v dh^T ]
-//   dv  = tril(A)^T do + (k e^{gamma-g~}) dh,     A = scale (q e^{g~-r})(k e^{r-g~})^T
+//   dv  = tril(A)^T do + (k e^{r-g~}) (e^{gamma-r} dh),   A = scale (q e^{g~-r})(k e^{r-g~})^T
 //   dg  = revcumsum_chunk(q dq - k dk) + e^{gamma} sum_v h dh + sum_j k dk_inter
 //
-// chunk_bwd_dqkg_kernel: one 256-thread block per (chunk, head, 64-wide K tile); every
-//   quantity above except dv is local to a K tile (contractions run over V and the chunk).
-// chunk_bwd_dv_kernel:   one block per (chunk, head, 64-wide V tile); accumulates the
-//   K contraction of A^T and of kd.dh over K tiles.
+// chunk_bwd_dqkg_kernel: one 256-thread block per (chunk, head, 64-wide K tile); everything
+//   above except dv is local to a K tile (its contractions run over V and over the chunk).
+// chunk_bwd_dv_kernel:   one block per (chunk, head, 64-wide V tile), accumulating the
+//   K contractions of A and of k_d.dh over K tiles; it produces dv^T tiles so that each lane
+//   stores four consecutive values of a row.
+// Tiles are staged in LDS row-major exactly as loaded (16-byte global loads); operands that
+// are needed transposed (kg^T, qg^T, dA^T, dh^T, do^T, A^T) are read with transposed MFMA
+// fragments. Element-wise work maps a thread to two adjacent columns x C/8 rows.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace tops {
 
-// dynamic LDS layout of chunk_bwd_dqkg_kernel (bytes); `exch` aliases the T buffers
-template <typename T>
-struct DqkgLayout {
-  int qgT, kgT, do_, v, h, dh, dA, dAT, tbytes, exch_bytes, total;
-  __host__ __device__ DqkgLayout(int C) {
-    const int CP = C < 32 ? 32 : C;
-    const int a64 = ((64 * pitch_of<T>(CP) * (int)sizeof(T)) + 15) / 16 * 16;  // [64][CP]
-    const int c64 = ((C * pitch_of<T>(64) * (int)sizeof(T)) + 15) / 16 * 16;   // [C][64]
-    const int s64 = ((64 * pitch_of<T>(64) * (int)sizeof(T)) + 15) / 16 * 16;  // [64][64]
-    const int ccp = ((C * pitch_of<T>(CP) * (int)sizeof(T)) + 15) / 16 * 16;   // [C][CP]
-    qgT = 0;
-    kgT = qgT + a64;
-    do_ = kgT + a64;
-    v = do_ + c64;
-    h = v + c64;
-    dh = h + s64;
-    dA = dh + s64;
-    dAT = dA + ccp;
-    tbytes = dAT + ccp;
-    exch_bytes = 3 * C * 68 * 4;
-    total = tbytes > exch_bytes ? tbytes : exch_bytes;
+// ---------------------------------------------------------------------------
+// shared pieces
+// ---------------------------------------------------------------------------
+
+// 16-byte loads of an [R x 64] tile into registers: rows of stride `rs` elements, tile
+// columns col0..col0+63 of rows whose valid width is `width`; rows >= len and columns past
+// the width read as zero. Piece pc = tid + 256 j covers row pc / (64/EPP).
+template <typename T, int R, bool VEC, int PPT>
+__device__ __forceinline__ void tile_load(uint4 (&r)[PPT], const T* __restrict__ base, long rs,
+                                          int len, int col0, int width, int tid) {
+  constexpr int EPP = 16 / (int)sizeof(T);
+  constexpr int PPR = 64 / EPP;
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int pc = tid + 256 * j;
+    const int row = pc / PPR, c = (pc % PPR) * EPP;
+    r[j] = make_uint4(0, 0, 0, 0);
+    if (pc < R * PPR && row < len)
+      r[j] = gload16<T, VEC>(base + row * rs + col0, c, width - col0 - c);
   }
-};
+}
+
+template <typename T, int R, int PPT>
+__device__ __forceinline__ void tile_store(T* s, int pitch, const uint4 (&r)[PPT], int tid) {
+  constexpr int EPP = 16 / (int)sizeof(T);
+  constexpr int PPR = 64 / EPP;
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int pc = tid + 256 * j;
+    if (pc < R * PPR) *reinterpret_cast<uint4*>(s + (pc / PPR) * pitch + (pc % PPR) * EPP) = r[j];
+  }
+}
+
+template <typename T, int R>
+constexpr int pieces_per_thread() {
+  return (R * (64 / (16 / (int)sizeof(T))) + 255) / 256;
+}
+
+// Column-pair chunk-local cumsum of a raw gate tile in LDS (thread: columns c0, c0+1, rows
+// seg*RPS .. +RPS). On return d0/d1 hold g~ - r, gam0/1 = gamma, r0/1 = r for the two
+// columns. sTot: 8*64 floats, sFirst: 64 floats. Contains one __syncthreads().
+template <typename T, int C>
+__device__ __forceinline__ void pair_cumsum(const T* sG, int pitch, int c0, int seg,
+                                            float* sTot, float* sFirst, float (&d0)[C / 8],
+                                            float (&d1)[C / 8], float& gam0, float& gam1,
+                                            float& r0, float& r1) {
+  constexpr int NSEG = 8, RPS = C / NSEG;
+  float run0 = 0.f, run1 = 0.f;
+#pragma unroll
+  for (int rr = 0; rr < RPS; ++rr) {
+    float x0, x1;
+    Pair<T>::ld(sG + (seg * RPS + rr) * pitch + c0, x0, x1);
+    run0 += x0;
+    run1 += x1;
+    d0[rr] = run0;
+    d1[rr] = run1;
+  }
+  sTot[seg * 64 + c0] = run0;
+  sTot[seg * 64 + c0 + 1] = run1;
+  if (seg == 0) {
+    sFirst[c0] = d0[0];
+    sFirst[c0 + 1] = d1[0];
+  }
+  __syncthreads();
+  float off0 = 0.f, off1 = 0.f;
+  gam0 = gam1 = 0.f;
+#pragma unroll
+  for (int s = 0; s < NSEG; ++s) {
+    const float x0 = sTot[s * 64 + c0], x1 = sTot[s * 64 + c0 + 1];
+    off0 += (s < seg) ? x0 : 0.f;
+    off1 += (s < seg) ? x1 : 0.f;
+    gam0 += x0;
+    gam1 += x1;
+  }
+  r0 = 0.5f * (sFirst[c0] + gam0);
+  r1 = 0.5f * (sFirst[c0 + 1] + gam1);
+#pragma unroll
+  for (int rr = 0; rr < RPS; ++rr) {
+    d0[rr] += off0 - r0;
+    d1[rr] += off1 - r1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dq, dk, dg
+// ---------------------------------------------------------------------------
 
 template <typename T, int C>
+struct DqkgLayout {
+  static constexpr int CP = C < 32 ? 32 : C;   // contraction over the chunk: multiple of 32
+  static constexpr int P64 = pitch_of<T>(64), PCP = pitch_of<T>(CP);
+  static constexpr int ES = (int)sizeof(T);
+  static constexpr int TILE = ((CP * P64 * ES) + 15) / 16 * 16;   // [CP][64]
+  static constexpr int SQ = ((64 * P64 * ES) + 15) / 16 * 16;     // [64][64]
+  static constexpr int DA = ((CP * PCP * ES) + 15) / 16 * 16;     // [CP][CP]
+  // region A: raw q, k, g (prologue) then do, v | h, dh | qg, kg | dA
+  static constexpr int qr = 0, kr = TILE, gr = 2 * TILE;
+  static constexpr int do_ = 0, v = TILE;
+  static constexpr int h = 3 * TILE, dh = 3 * TILE + SQ;
+  static constexpr int qg = 3 * TILE + 2 * SQ, kg = qg + TILE;
+  static constexpr int dA = kg + TILE;
+  static constexpr int tbytes = dA + DA;
+  static constexpr int PX = 68;                      // fp32 exchange pitch
+  static constexpr int exch = 3 * C * PX * 4;        // aliases everything above
+  static constexpr int bytes = tbytes > exch ? tbytes : exch;
+};
+
+template <typename T, int C, bool VEC>
 __global__ __launch_bounds__(256) void chunk_bwd_dqkg_kernel(BwdArgs p) {
-  constexpr int CP = C < 32 ? 32 : C;
-  constexpr int RPS = C / 4;
-  constexpr int P64 = pitch_of<T>(64), PCP = pitch_of<T>(CP);
+  using Lay = DqkgLayout<T, C>;
+  constexpr int CP = Lay::CP, P64 = Lay::P64, PCP = Lay::PCP, PX = Lay::PX;
+  constexpr int PPT = pieces_per_thread<T, C>(), HPT = pieces_per_thread<T, 64>();
+  constexpr int NSEG = 8, RPS = C / NSEG;
   constexpr int NTM = C / 16, NT_A = NTM * NTM, NA = (NT_A + 3) / 4;
-  constexpr int NO = NTM;  // C x 64 tile = 4*NTM 16x16 tiles over 4 waves
-  constexpr int PX = 68;   // fp32 exchange pitch
+  constexpr int NO = NTM;   // [C x 64] output = 4*NTM 16x16 tiles over 4 waves
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
-  __shared__ float sTot[256], sAux[256];
-  __shared__ float sR[64], sEg[64], sHd[64];
-  const DqkgLayout<T> lay(C);
-  T* sQgT = reinterpret_cast<T*>(dyn + lay.qgT);
-  T* sKgT = reinterpret_cast<T*>(dyn + lay.kgT);
-  T* sDo = reinterpret_cast<T*>(dyn + lay.do_);
-  T* sV = reinterpret_cast<T*>(dyn + lay.v);
-  T* sH = reinterpret_cast<T*>(dyn + lay.h);
-  T* sDh = reinterpret_cast<T*>(dyn + lay.dh);
-  T* sdA = reinterpret_cast<T*>(dyn + lay.dA);
-  T* sdAT = reinterpret_cast<T*>(dyn + lay.dAT);
+  __shared__ float sTot[NSEG * 64], sAux[NSEG * 64];
+  __shared__ float sR[64], sEg[64], sGm[64], sHd[64];
+  T* sQr = reinterpret_cast<T*>(dyn + Lay::qr);
+  T* sKr = reinterpret_cast<T*>(dyn + Lay::kr);
+  T* sGr = reinterpret_cast<T*>(dyn + Lay::gr);
+  T* sDo = reinterpret_cast<T*>(dyn + Lay::do_);
+  T* sV = reinterpret_cast<T*>(dyn + Lay::v);
+  T* sH = reinterpret_cast<T*>(dyn + Lay::h);
+  T* sDh = reinterpret_cast<T*>(dyn + Lay::dh);
+  T* sQg = reinterpret_cast<T*>(dyn + Lay::qg);
+  T* sKg = reinterpret_cast<T*>(dyn + Lay::kg);
+  T* sdA = reinterpret_cast<T*>(dyn + Lay::dA);
   float* XQ = reinterpret_cast<float*>(dyn);
   float* XK = XQ + C * PX;
   float* XM = XK + C * PX;
@@ -86,111 +174,114 @@ __global__ __launch_bounds__(256) void chunk_bwd_dqkg_kernel(BwdArgs p) {
   (void)seq;
   const long rsK = (long)H * K, rsV = (long)H * V;
   const long baseK = ((long)t0 * H + hh) * K, baseV = ((long)t0 * H + hh) * V;
-  const int col = tid & 63, seg = tid >> 6;
-  const int gcol = kt * 64 + col;
-  const bool kvalid = gcol < K;
+  const int kb = kt * 64, klen = min(64, K - kb);
+  const T* __restrict__ hrow = hs + (((long)c * H + hh) * K + kb) * V;    // h[c][kb][0]
+  const T* __restrict__ dhrow = dhs + (((long)c * H + hh) * K + kb) * V;  // dh[c][kb][0]
 
-  if (CP > C) {
-    for (int i = tid; i < 64 * (CP - C); i += 256) {
-      const int rr = i / (CP - C), cc = C + i % (CP - C);
-      sQgT[rr * PCP + cc] = zero_elem<T>();
-      sKgT[rr * PCP + cc] = zero_elem<T>();
+  // global -> registers: q, k, g of this K tile and V tile 0 of do, v, h, dh
+  uint4 rq[PPT], rk[PPT], rg[PPT], rdo[PPT], rv[PPT], rh[HPT], rdh[HPT];
+  tile_load<T, C, VEC>(rq, q + baseK, rsK, len, kb, K, tid);
+  tile_load<T, C, VEC>(rk, k + baseK, rsK, len, kb, K, tid);
+  tile_load<T, C, VEC>(rg, g + baseK, rsK, len, kb, K, tid);
+  tile_load<T, C, VEC>(rdo, dout + baseV, rsV, len, 0, V, tid);
+  tile_load<T, C, VEC>(rv, v + baseV, rsV, len, 0, V, tid);
+  tile_load<T, 64, VEC>(rh, hrow, V, klen, 0, V, tid);
+  tile_load<T, 64, VEC>(rdh, dhrow, V, klen, 0, V, tid);
+  if (CP > C) {   // rows [C, CP) of the chunk-contraction operands stay zero
+    for (int i = tid; i < (CP - C) * P64; i += 256) {
+      sQg[C * P64 + i] = zero_elem<T>();
+      sKg[C * P64 + i] = zero_elem<T>();
     }
-    for (int i = tid; i < C * (CP - C); i += 256) {
-      const int rr = i / (CP - C), cc = C + i % (CP - C);
-      sdA[rr * PCP + cc] = zero_elem<T>();
-      sdAT[rr * PCP + cc] = zero_elem<T>();
-    }
+    for (int i = tid; i < CP * PCP; i += 256)
+      if (i >= C * PCP || i % PCP >= C) sdA[i] = zero_elem<T>();
   }
+  tile_store<T, C>(sQr, P64, rq, tid);
+  tile_store<T, C>(sKr, P64, rk, tid);
+  tile_store<T, C>(sGr, P64, rg, tid);
+  tile_store<T, 64>(sH, P64, rh, tid);
+  tile_store<T, 64>(sDh, P64, rdh, tid);
+  __syncthreads();
 
-  // ---- prologue: gates of this K tile ----
-  float gt[RPS], qreg[RPS], kreg[RPS];
-  float gamma, first;
-  tile_cumsum<C>(g + baseK + gcol, rsK, len, kvalid, false, sTot, gt, gamma, first);
-  const float r = 0.5f * (first + gamma);
+  // ---- cumsum and gating ----
+  const int cp = tid & 31, seg = tid >> 5;
+  const int c_0 = 2 * cp, c_1 = c_0 + 1;
+  float q0[RPS], q1[RPS], k0[RPS], k1[RPS], d0[RPS], d1[RPS];
+  float gam0, gam1, r0, r1;
+  pair_cumsum<T, C>(sGr, P64, c_0, seg, sTot, sAux, d0, d1, gam0, gam1, r0, r1);
 #pragma unroll
   for (int rr = 0; rr < RPS; ++rr) {
     const int row = seg * RPS + rr;
-    float qv = 0.f, kv = 0.f;
-    if (row < len && kvalid) {
-      qv = to_f32(q[baseK + (long)row * rsK + gcol]);
-      kv = to_f32(k[baseK + (long)row * rsK + gcol]);
-    }
-    qreg[rr] = qv;
-    kreg[rr] = kv;
-    const float d = gt[rr] - r;
-    sQgT[col * PCP + row] = from_f32<T>(qv * gexp<T>(d));
-    sKgT[col * PCP + row] = from_f32<T>(kv * gexp<T>(-d));
+    Pair<T>::ld(sQr + row * P64 + c_0, q0[rr], q1[rr]);
+    Pair<T>::ld(sKr + row * P64 + c_0, k0[rr], k1[rr]);
+    const float e0 = gexp<T>(d0[rr]), e1 = gexp<T>(d1[rr]);
+    Pair<T>::st(sQg + row * P64 + c_0, q0[rr] * e0, q1[rr] * e1);
+    Pair<T>::st(sKg + row * P64 + c_0, k0[rr] / e0, k1[rr] / e1);
   }
   if (seg == 0) {
-    sR[col] = p.scale * gexp<T>(r);
-    sEg[col] = gexp<T>(gamma - r);
+    sR[c_0] = p.scale * gexp<T>(r0);
+    sR[c_1] = p.scale * gexp<T>(r1);
+    sEg[c_0] = gexp<T>(gam0 - r0);
+    sEg[c_1] = gexp<T>(gam1 - r1);
+    sGm[c_0] = gexp<T>(gam0);
+    sGm[c_1] = gexp<T>(gam1);
   }
+  __syncthreads();   // raw q, k, g are dead: region A takes do, v
+  tile_store<T, C>(sDo, P64, rdo, tid);
+  tile_store<T, C>(sV, P64, rv, tid);
+  __syncthreads();
 
-  f32x4 dA[NA], dAT[NA], Mqx[NO], M2[NO];
+  f32x4 dA[NA], Mqx[NO], M2[NO];
 #pragma unroll
-  for (int j = 0; j < NA; ++j) dA[j] = dAT[j] = zero4();
+  for (int j = 0; j < NA; ++j) dA[j] = zero4();
 #pragma unroll
   for (int j = 0; j < NO; ++j) Mqx[j] = M2[j] = zero4();
   float hdp = 0.f;
-  const long hbase = ((long)c * H + hh) * K;
-
   for (int vt = 0; vt < VT; ++vt) {
-    const int vcol = vt * 64 + col;
-    const bool vvalid = vcol < V;
-#pragma unroll
-    for (int rr = 0; rr < RPS; ++rr) {
-      const int row = seg * RPS + rr;
-      float x = 0.f, y = 0.f;
-      if (row < len && vvalid) {
-        x = to_f32(dout[baseV + (long)row * rsV + vcol]);
-        y = to_f32(v[baseV + (long)row * rsV + vcol]);
-      }
-      sDo[row * P64 + col] = from_f32<T>(x);
-      sV[row * P64 + col] = from_f32<T>(y);
+    if (vt > 0) {
+      const int vb = vt * 64;
+      tile_load<T, C, VEC>(rdo, dout + baseV, rsV, len, vb, V, tid);
+      tile_load<T, C, VEC>(rv, v + baseV, rsV, len, vb, V, tid);
+      tile_load<T, 64, VEC>(rh, hrow, V, klen, vb, V, tid);
+      tile_load<T, 64, VEC>(rdh, dhrow, V, klen, vb, V, tid);
+      __syncthreads();   // readers of the previous V tile are done
+      tile_store<T, C>(sDo, P64, rdo, tid);
+      tile_store<T, C>(sV, P64, rv, tid);
+      tile_store<T, 64>(sH, P64, rh, tid);
+      tile_store<T, 64>(sDh, P64, rdh, tid);
+      __syncthreads();
     }
-#pragma unroll 4
-    for (int i = 0; i < 16; ++i) {
-      const int kk = seg * 16 + i;
-      const int gk = kt * 64 + kk;
-      T a = zero_elem<T>(), b = zero_elem<T>();
-      if (gk < K && vvalid) {
-        a = hs[(hbase + gk) * V + vcol];
-        b = dhs[(hbase + gk) * V + vcol];
-      }
-      sH[kk * P64 + col] = a;
-      sDh[kk * P64 + col] = b;
-    }
-    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < NA; ++j) {
+    for (int j = 0; j < NA; ++j) {   // dA[i][j] += do[i] . v[j]   (lower tiles)
       const int t = w + 4 * j;
       if (t < NT_A) {
         const int mi = t / NTM, ni = t % NTM;
-        mma_tile<T>(dA[j], sDo + mi * 16 * P64, P64, sV + ni * 16 * P64, P64, 64, lane);
-        mma_tile<T>(dAT[j], sV + mi * 16 * P64, P64, sDo + ni * 16 * P64, P64, 64, lane);
+        if (ni <= mi)
+          mma_tile<T>(dA[j], sDo + mi * 16 * P64, P64, sV + ni * 16 * P64, P64, 64, lane);
       }
     }
 #pragma unroll
-    for (int j = 0; j < NO; ++j) {
+    for (int j = 0; j < NO; ++j) {   // do h^T and v dh^T, [C x 64 k]
       const int t = w + 4 * j;
       const int mi = t >> 2, ni = t & 3;
       mma_tile<T>(Mqx[j], sDo + mi * 16 * P64, P64, sH + ni * 16 * P64, P64, 64, lane);
       mma_tile<T>(M2[j], sV + mi * 16 * P64, P64, sDh + ni * 16 * P64, P64, 64, lane);
     }
-    {
-      const int kk = tid >> 2, v0 = (tid & 3) * 16;
+    {   // sum_v h dh for row k = tid/4
+      const int kk = tid >> 2, vv = (tid & 3) * 16;
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        hdp += to_f32(sH[kk * P64 + v0 + i]) * to_f32(sDh[kk * P64 + v0 + i]);
+      for (int i = 0; i < 16; i += 2) {
+        float a0, a1, b0, b1;
+        Pair<T>::ld(sH + kk * P64 + vv + i, a0, a1);
+        Pair<T>::ld(sDh + kk * P64 + vv + i, b0, b1);
+        hdp += a0 * b0 + a1 * b1;
+      }
     }
-    __syncthreads();
   }
   hdp += __shfl_xor(hdp, 1);
   hdp += __shfl_xor(hdp, 2);
   if ((tid & 3) == 0) sHd[tid >> 2] = hdp;
 
-  // ---- masked dA / dA^T to LDS ----
+  // ---- dA (masked, scaled) to LDS, then the chunk contractions ----
 #pragma unroll
   for (int j = 0; j < NA; ++j) {
     const int t = w + 4 * j;
@@ -200,14 +291,11 @@ __global__ __launch_bounds__(256) void chunk_bwd_dqkg_kernel(BwdArgs p) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int ro = mi * 16 + 4 * (lane >> 4) + rr;
-        // dA[i=ro][j=cc] kept for j <= i ; dA^T[j=ro][i=cc] kept for i >= j
         sdA[ro * PCP + cc] = from_f32<T>(cc <= ro ? dA[j][rr] * p.scale : 0.f);
-        sdAT[ro * PCP + cc] = from_f32<T>(cc >= ro ? dAT[j][rr] * p.scale : 0.f);
       }
     }
   }
   __syncthreads();
-
   f32x4 Mqi[NO], Mk1[NO];
 #pragma unroll
   for (int j = 0; j < NO; ++j) {
@@ -215,10 +303,12 @@ __global__ __launch_bounds__(256) void chunk_bwd_dqkg_kernel(BwdArgs p) {
     const int mi = t >> 2, ni = t & 3;
     Mqi[j] = zero4();
     Mk1[j] = zero4();
-    mma_tile<T>(Mqi[j], sdA + mi * 16 * PCP, PCP, sKgT + ni * 16 * PCP, PCP, CP, lane);
-    mma_tile<T>(Mk1[j], sdAT + mi * 16 * PCP, PCP, sQgT + ni * 16 * PCP, PCP, CP, lane);
+    // dq_intra[i][k] = sum_j dA[i][j] kg[j][k]      (kg read transposed)
+    mma_tile2<T, false, true>(Mqi[j], sdA + mi * 16 * PCP, PCP, sKg + ni * 16, P64, CP, lane);
+    // dk_intra[j][k] = sum_i dA[i][j] qg[i][k]      (dA and qg read transposed)
+    mma_tile2<T, true, true>(Mk1[j], sdA + mi * 16, PCP, sQg + ni * 16, P64, CP, lane);
   }
-  __syncthreads();  // T buffers are dead; the exchange area aliases them
+  __syncthreads();   // every staged tile is dead; the fp32 exchange aliases them
 
 #pragma unroll
   for (int j = 0; j < NO; ++j) {
@@ -236,58 +326,115 @@ __global__ __launch_bounds__(256) void chunk_bwd_dqkg_kernel(BwdArgs p) {
   }
   __syncthreads();
 
-  // ---- column epilogue: dq, dk, dg ----
+  // ---- epilogue: dq, dk, dg ----
   T* __restrict__ dq = (T*)p.dq;
   T* __restrict__ dk = (T*)p.dk;
   T* __restrict__ dg = (T*)p.dg;
-  float dgr[RPS];
-  float run = 0.f, dki = 0.f;
+  float dgr0[RPS], dgr1[RPS];
+  float s0 = 0.f, s1 = 0.f, dki0 = 0.f, dki1 = 0.f;
+  const int gc0 = kb + c_0;
+  const bool ok0 = gc0 < K, ok1 = gc0 + 1 < K;
 #pragma unroll
   for (int rr = RPS - 1; rr >= 0; --rr) {
     const int row = seg * RPS + rr;
-    const float ep = gexp<T>(gt[rr] - r), en = gexp<T>(r - gt[rr]);
-    const float vq = ep * XQ[row * PX + col];
-    const float vk = en * XK[row * PX + col];
-    const float vm = en * XM[row * PX + col];
-    dki += kreg[rr] * vm;
-    run += qreg[rr] * vq - kreg[rr] * vk;
-    dgr[rr] = run;
-    if (row < len && kvalid) {
-      dq[baseK + (long)row * rsK + gcol] = from_f32<T>(vq);
-      dk[baseK + (long)row * rsK + gcol] = from_f32<T>(vk);
+    const float ep0 = gexp<T>(d0[rr]), ep1 = gexp<T>(d1[rr]);
+    const float2 xq = *reinterpret_cast<const float2*>(XQ + row * PX + c_0);
+    const float2 xk = *reinterpret_cast<const float2*>(XK + row * PX + c_0);
+    const float2 xm = *reinterpret_cast<const float2*>(XM + row * PX + c_0);
+    const float vq0 = ep0 * xq.x, vq1 = ep1 * xq.y;
+    const float vk0 = xk.x / ep0, vk1 = xk.y / ep1;
+    dki0 += k0[rr] * (xm.x / ep0);
+    dki1 += k1[rr] * (xm.y / ep1);
+    s0 += q0[rr] * vq0 - k0[rr] * vk0;
+    s1 += q1[rr] * vq1 - k1[rr] * vk1;
+    dgr0[rr] = s0;
+    dgr1[rr] = s1;
+    if (row < len) {
+      const long a = baseK + (long)row * rsK + gc0;
+      if (VEC && ok1) {
+        Pair<T>::st(dq + a, vq0, vq1);
+        Pair<T>::st(dk + a, vk0, vk1);
+      } else {
+        if (ok0) {
+          dq[a] = from_f32<T>(vq0);
+          dk[a] = from_f32<T>(vk0);
+        }
+        if (ok1) {
+          dq[a + 1] = from_f32<T>(vq1);
+          dk[a + 1] = from_f32<T>(vk1);
+        }
+      }
     }
   }
-  sTot[seg * 64 + col] = run;
-  sAux[seg * 64 + col] = dki;
+  sTot[seg * 64 + c_0] = s0;
+  sTot[seg * 64 + c_1] = s1;
+  sAux[seg * 64 + c_0] = dki0;
+  sAux[seg * 64 + c_1] = dki1;
   __syncthreads();
-  float off = 0.f, dks = 0.f;
+  float o0 = 0.f, o1 = 0.f, dks0 = 0.f, dks1 = 0.f;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    off += (s > seg) ? sTot[s * 64 + col] : 0.f;
-    dks += sAux[s * 64 + col];
+  for (int s = 0; s < NSEG; ++s) {
+    o0 += (s > seg) ? sTot[s * 64 + c_0] : 0.f;
+    o1 += (s > seg) ? sTot[s * 64 + c_1] : 0.f;
+    dks0 += sAux[s * 64 + c_0];
+    dks1 += sAux[s * 64 + c_1];
   }
-  const float dgk = gexp<T>(gamma) * sHd[col] + dks;
+  const float dgk0 = sGm[c_0] * sHd[c_0] + dks0, dgk1 = sGm[c_1] * sHd[c_1] + dks1;
 #pragma unroll
   for (int rr = 0; rr < RPS; ++rr) {
     const int row = seg * RPS + rr;
-    if (row < len && kvalid) dg[baseK + (long)row * rsK + gcol] = from_f32<T>(dgr[rr] + off + dgk);
+    if (row < len) {
+      const long a = baseK + (long)row * rsK + gc0;
+      const float x0 = dgr0[rr] + o0 + dgk0, x1 = dgr1[rr] + o1 + dgk1;
+      if (VEC && ok1) {
+        Pair<T>::st(dg + a, x0, x1);
+      } else {
+        if (ok0) dg[a] = from_f32<T>(x0);
+        if (ok1) dg[a + 1] = from_f32<T>(x1);
+      }
+    }
   }
 }
 
+// ---------------------------------------------------------------------------
+// dv
+// ---------------------------------------------------------------------------
+
 template <typename T, int C>
+struct DvLayout {
+  static constexpr int CP = C < 32 ? 32 : C;
+  static constexpr int P64 = pitch_of<T>(64), PCP = pitch_of<T>(CP);
+  static constexpr int ES = (int)sizeof(T);
+  static constexpr int TILE = ((CP * P64 * ES) + 15) / 16 * 16;
+  static constexpr int SQ = ((64 * P64 * ES) + 15) / 16 * 16;
+  static constexpr int AT = ((CP * PCP * ES) + 15) / 16 * 16;
+  // region R: raw q, k, g (per K tile), later A and do | qg, kg | dh' = e^{gamma-r} dh
+  static constexpr int qr = 0, kr = TILE, gr = 2 * TILE;
+  static constexpr int a = 0, do_ = AT;
+  static constexpr int R = (3 * TILE > AT + TILE) ? 3 * TILE : AT + TILE;
+  static constexpr int qg = R, kg = R + TILE, dh = R + 2 * TILE;
+  static constexpr int bytes = dh + SQ;
+};
+
+template <typename T, int C, bool VEC>
 __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
-  constexpr int CP = C < 32 ? 32 : C;
-  constexpr int RPS = C / 4;
-  constexpr int P64 = pitch_of<T>(64), PCP = pitch_of<T>(CP);
+  using Lay = DvLayout<T, C>;
+  constexpr int CP = Lay::CP, P64 = Lay::P64, PCP = Lay::PCP;
+  constexpr int EPP = 16 / (int)sizeof(T);
+  constexpr int PPT = pieces_per_thread<T, C>(), HPT = pieces_per_thread<T, 64>();
+  constexpr int NSEG = 8, RPS = C / NSEG;
   constexpr int NTM = C / 16, NT_A = NTM * NTM, NA = (NT_A + 3) / 4;
   constexpr int NO = NTM;
-  __shared__ __attribute__((aligned(16))) T sKg[C * P64];
-  __shared__ __attribute__((aligned(16))) T sQg[C * P64];
-  __shared__ __attribute__((aligned(16))) T sKd[C * P64];
-  __shared__ __attribute__((aligned(16))) T sDhT[64 * P64];
-  __shared__ __attribute__((aligned(16))) T sAT[C * PCP];
-  __shared__ __attribute__((aligned(16))) T sDoT[64 * PCP];
-  __shared__ float sTot[256];
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+  __shared__ float sTot[NSEG * 64], sFirst[64], sEg[64];
+  T* sQr = reinterpret_cast<T*>(dyn + Lay::qr);
+  T* sKr = reinterpret_cast<T*>(dyn + Lay::kr);
+  T* sGr = reinterpret_cast<T*>(dyn + Lay::gr);
+  T* sA = reinterpret_cast<T*>(dyn + Lay::a);
+  T* sDo = reinterpret_cast<T*>(dyn + Lay::do_);
+  T* sQg = reinterpret_cast<T*>(dyn + Lay::qg);
+  T* sKg = reinterpret_cast<T*>(dyn + Lay::kg);
+  T* sDh = reinterpret_cast<T*>(dyn + Lay::dh);
 
   const T* __restrict__ q = (const T*)p.q;
   const T* __restrict__ k = (const T*)p.k;
@@ -307,136 +454,171 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
   (void)seq;
   const long rsK = (long)H * K, rsV = (long)H * V;
   const long baseK = ((long)t0 * H + hh) * K, baseV = ((long)t0 * H + hh) * V;
-  const int col = tid & 63, seg = tid >> 6;
-  const int vcol = vt * 64 + col;
-  const bool vvalid = vcol < V;
+  const int vb = vt * 64;
+  const int cp = tid & 31, seg = tid >> 5;
+  const int c_0 = 2 * cp, c_1 = c_0 + 1;
 
-  if (CP > C) {
-    for (int i = tid; i < C * (CP - C); i += 256)
-      sAT[(i / (CP - C)) * PCP + C + i % (CP - C)] = zero_elem<T>();
-    for (int i = tid; i < 64 * (CP - C); i += 256)
-      sDoT[(i / (CP - C)) * PCP + C + i % (CP - C)] = zero_elem<T>();
-  }
-
-  f32x4 AT[NA], Mdv[NO];
+  // A[i][j] (lower tiles only) and dv^T[v][j], both accumulated over K tiles
+  f32x4 Aacc[NA], Dacc[NO];
 #pragma unroll
-  for (int j = 0; j < NA; ++j) AT[j] = zero4();
+  for (int j = 0; j < NA; ++j) Aacc[j] = zero4();
 #pragma unroll
-  for (int j = 0; j < NO; ++j) Mdv[j] = zero4();
-  const long hbase = ((long)c * H + hh) * K;
+  for (int j = 0; j < NO; ++j) Dacc[j] = zero4();
 
+  uint4 rq[PPT], rk[PPT], rg[PPT], rdh[HPT];
   for (int kt = 0; kt < KT; ++kt) {
-    const int gcol = kt * 64 + col;
-    const bool kvalid = gcol < K;
-    float gt[RPS];
-    float gamma, first;
-    tile_cumsum<C>(g + baseK + gcol, rsK, len, kvalid, false, sTot, gt, gamma, first);
-    const float r = 0.5f * (first + gamma);
+    const int kb = kt * 64;
+    tile_load<T, C, VEC>(rq, q + baseK, rsK, len, kb, K, tid);
+    tile_load<T, C, VEC>(rk, k + baseK, rsK, len, kb, K, tid);
+    tile_load<T, C, VEC>(rg, g + baseK, rsK, len, kb, K, tid);
+    tile_load<T, 64, VEC>(rdh, dhs + (((long)c * H + hh) * K + kb) * V, V, min(64, K - kb), vb,
+                          V, tid);
+    if (kt > 0) __syncthreads();   // readers of the previous K tile are done
+    tile_store<T, C>(sQr, P64, rq, tid);
+    tile_store<T, C>(sKr, P64, rk, tid);
+    tile_store<T, C>(sGr, P64, rg, tid);
+    __syncthreads();
+    float d0[RPS], d1[RPS], gam0, gam1, r0, r1;
+    pair_cumsum<T, C>(sGr, P64, c_0, seg, sTot, sFirst, d0, d1, gam0, gam1, r0, r1);
 #pragma unroll
     for (int rr = 0; rr < RPS; ++rr) {
       const int row = seg * RPS + rr;
-      float qv = 0.f, kv = 0.f;
-      if (row < len && kvalid) {
-        qv = to_f32(q[baseK + (long)row * rsK + gcol]);
-        kv = to_f32(k[baseK + (long)row * rsK + gcol]);
-      }
-      const float d = gt[rr] - r;
-      sQg[row * P64 + col] = from_f32<T>(qv * gexp<T>(d));
-      sKg[row * P64 + col] = from_f32<T>(kv * gexp<T>(-d));
-      sKd[row * P64 + col] = from_f32<T>(kv * gexp<T>(gamma - gt[rr]));
+      float qa, qb, ka, kb2;
+      Pair<T>::ld(sQr + row * P64 + c_0, qa, qb);
+      Pair<T>::ld(sKr + row * P64 + c_0, ka, kb2);
+      const float e0 = gexp<T>(d0[rr]), e1 = gexp<T>(d1[rr]);
+      Pair<T>::st(sQg + row * P64 + c_0, qa * e0, qb * e1);
+      Pair<T>::st(sKg + row * P64 + c_0, ka / e0, kb2 / e1);
     }
-#pragma unroll 4
-    for (int i = 0; i < 16; ++i) {
-      const int kk = seg * 16 + i;
-      const int gk = kt * 64 + kk;
-      T x = zero_elem<T>();
-      if (gk < K && vvalid) x = dhs[(hbase + gk) * V + vcol];
-      sDhT[col * P64 + kk] = x;
+    if (seg == 0) {
+      sEg[c_0] = gexp<T>(gam0 - r0);
+      sEg[c_1] = gexp<T>(gam1 - r1);
+    }
+    __syncthreads();
+    // dh' = dh scaled per K row by e^{gamma - r}, so that k_d . dh = kg . dh'
+#pragma unroll
+    for (int j = 0; j < HPT; ++j) {
+      const int pc = tid + 256 * j;
+      if (pc < 64 * (64 / EPP)) {
+        const int row = pc / (64 / EPP), c8 = (pc % (64 / EPP)) * EPP;
+        T vals[EPP];
+        __builtin_memcpy(vals, &rdh[j], 16);
+        const float f = sEg[row];
+        float x[EPP];
+#pragma unroll
+        for (int e = 0; e < EPP; ++e) x[e] = to_f32(vals[e]) * f;
+        store_run<T, EPP>(sDh + row * P64 + c8, x);
+      }
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < NA; ++j) {
+    for (int j = 0; j < NA; ++j) {   // A[i][j] += qg[i] . kg[j]
       const int t = w + 4 * j;
       if (t < NT_A) {
         const int mi = t / NTM, ni = t % NTM;
-        mma_tile<T>(AT[j], sKg + mi * 16 * P64, P64, sQg + ni * 16 * P64, P64, 64, lane);
+        if (ni <= mi)
+          mma_tile<T>(Aacc[j], sQg + mi * 16 * P64, P64, sKg + ni * 16 * P64, P64, 64, lane);
       }
     }
 #pragma unroll
-    for (int j = 0; j < NO; ++j) {
+    for (int j = 0; j < NO; ++j) {   // dv^T[v][j] += sum_k dh'[k][v] kg[j][k]
       const int t = w + 4 * j;
-      const int mi = t >> 2, ni = t & 3;
-      mma_tile<T>(Mdv[j], sKd + mi * 16 * P64, P64, sDhT + ni * 16 * P64, P64, 64, lane);
+      const int mv = t & 3, nj = t >> 2;
+      mma_tile2<T, true, false>(Dacc[j], sDh + mv * 16, P64, sKg + nj * 16 * P64, P64, 64,
+                                lane);
     }
-    __syncthreads();
   }
+  __syncthreads();   // raw and gated tiles are dead: region R takes A and do
 
+  {
+    uint4 rdo[PPT];
+    tile_load<T, C, VEC>(rdo, dout + baseV, rsV, len, vb, V, tid);
+    for (int i = tid; i < CP * PCP; i += 256) sA[i] = zero_elem<T>();
+    if (CP > C)
+      for (int i = tid; i < (CP - C) * P64; i += 256) sDo[C * P64 + i] = zero_elem<T>();
+    __syncthreads();   // zero fill before the tile writes below
+    tile_store<T, C>(sDo, P64, rdo, tid);
+  }
 #pragma unroll
   for (int j = 0; j < NA; ++j) {
     const int t = w + 4 * j;
     if (t < NT_A) {
       const int mi = t / NTM, ni = t % NTM;
-      const int cc = ni * 16 + (lane & 15);
+      if (ni <= mi) {
+        const int cc = ni * 16 + (lane & 15);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int ro = mi * 16 + 4 * (lane >> 4) + rr;  // j ; cc = i
-        sAT[ro * PCP + cc] = from_f32<T>(cc >= ro ? AT[j][rr] * p.scale : 0.f);
+        for (int rr = 0; rr < 4; ++rr) {
+          const int ro = mi * 16 + 4 * (lane >> 4) + rr;
+          sA[ro * PCP + cc] = from_f32<T>(cc <= ro ? Aacc[j][rr] * p.scale : 0.f);
+        }
       }
     }
   }
-#pragma unroll
-  for (int rr = 0; rr < RPS; ++rr) {
-    const int row = seg * RPS + rr;
-    float x = 0.f;
-    if (row < len && vvalid) x = to_f32(dout[baseV + (long)row * rsV + vcol]);
-    sDoT[col * PCP + row] = from_f32<T>(x);
-  }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < NO; ++j) {
+  for (int j = 0; j < NO; ++j) {   // dv^T[v][j] += sum_i do[i][v] A[i][j]
     const int t = w + 4 * j;
-    const int mi = t >> 2, ni = t & 3;
-    mma_tile<T>(Mdv[j], sAT + mi * 16 * PCP, PCP, sDoT + ni * 16 * PCP, PCP, CP, lane);
-    const int oc = vt * 64 + ni * 16 + (lane & 15);
-    if (oc < V) {
+    const int mv = t & 3, nj = t >> 2;
+    mma_tile2<T, true, true>(Dacc[j], sDo + mv * 16, P64, sA + nj * 16, PCP, CP, lane);
+    const int jj = nj * 16 + (lane & 15);
+    const int vv = vb + mv * 16 + 4 * (lane >> 4);
+    if (jj < len) {
+      T* dst = dv + baseV + (long)jj * rsV + vv;
+      if (VEC && vv + 3 < V) {
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2(pack2_bf16(Dacc[j][0], Dacc[j][1]), pack2_bf16(Dacc[j][2], Dacc[j][3]));
+        } else {
+          *reinterpret_cast<float4*>(dst) =
+              make_float4(Dacc[j][0], Dacc[j][1], Dacc[j][2], Dacc[j][3]);
+        }
+      } else {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int ro = mi * 16 + 4 * (lane >> 4) + rr;
-        if (ro < len) dv[baseV + (long)ro * rsV + oc] = from_f32<T>(Mdv[j][rr]);
+        for (int rr = 0; rr < 4; ++rr)
+          if (vv + rr < V) dst[rr] = from_f32<T>(Dacc[j][rr]);
       }
     }
   }
 }
 
-template <typename T, int C>
+template <typename T, int C, bool VEC>
 static hipError_t launch_bwd(const BwdArgs& p, hipStream_t st, int which) {
   const int KT = (p.K + 63) / 64, VT = (p.V + 63) / 64;
   const long nch = (long)p.si.NC * p.H;
   if (nch == 0) return hipSuccess;
   if (which & 1) {
-    const DqkgLayout<T> lay(C);
-    hipError_t e = hipFuncSetAttribute((const void*)chunk_bwd_dqkg_kernel<T, C>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lay.total);
+    using Lay = DqkgLayout<T, C>;
+    hipError_t e = hipFuncSetAttribute((const void*)chunk_bwd_dqkg_kernel<T, C, VEC>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((chunk_bwd_dqkg_kernel<T, C>), dim3((unsigned)(nch * KT)), dim3(256),
-                       lay.total, st, p);
+    hipLaunchKernelGGL((chunk_bwd_dqkg_kernel<T, C, VEC>), dim3((unsigned)(nch * KT)),
+                       dim3(256), Lay::bytes, st, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (which & 2) {
-    hipLaunchKernelGGL((chunk_bwd_dv_kernel<T, C>), dim3((unsigned)(nch * VT)), dim3(256), 0,
-                       st, p);
+    using Lay = DvLayout<T, C>;
+    hipError_t e = hipFuncSetAttribute((const void*)chunk_bwd_dv_kernel<T, C, VEC>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((chunk_bwd_dv_kernel<T, C, VEC>), dim3((unsigned)(nch * VT)), dim3(256),
+                       Lay::bytes, st, p);
     return hipGetLastError();
   }
   return hipSuccess;
 }
 
+template <typename T, int C>
+static hipError_t launch_vec(const BwdArgs& p, hipStream_t st, int which) {
+  return p.vec ? launch_bwd<T, C, true>(p, st, which) : launch_bwd<T, C, false>(p, st, which);
+}
+
 template <typename T>
 static hipError_t dispatch_bwd(const BwdArgs& p, hipStream_t st, int which) {
   switch (p.si.C) {
-    case 16: return launch_bwd<T, 16>(p, st, which);
-    case 32: return launch_bwd<T, 32>(p, st, which);
-    case 64: return launch_bwd<T, 64>(p, st, which);
+    case 16: return launch_vec<T, 16>(p, st, which);
+    case 32: return launch_vec<T, 32>(p, st, which);
+    case 64: return launch_vec<T, 64>(p, st, which);
     default: return hipErrorInvalidValue;
   }
 }

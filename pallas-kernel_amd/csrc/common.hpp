@@ -129,6 +129,51 @@ __device__ __forceinline__ void mma_tile(f32x4& acc, const T* X, int px, const T
   for (int kk = 0; kk < klen; kk += 32) mma(acc, ld_frag(xr + kk), ld_frag(yr + kk));
 }
 
+// ---------------------------------------------------------------------------
+// Transposed fragments: X[m][k] read from a ROW-MAJOR [k][m] LDS tile (pitch P elements),
+// `M` pointing at element [k0][m0]. gfx950 ds_read_b64_tr_b16: within each 16-lane group,
+// lane 4r+q supplies the address of row r, columns 4q..4q+3 of a 4 x 16 block and lane i
+// receives column i of that block (rows 0..3). Two such reads give lane l the 8 values
+// M[8*(l>>4) + 0..7][l & 15], i.e. the same fragment ld_frag returns from [m][k].
+// P*sizeof(T) must be a multiple of 8 and m0 a multiple of 4.
+// ---------------------------------------------------------------------------
+typedef short s4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ Frag<bf16> ld_frag_t(const bf16* M, int P, int lane) {
+  const int g = lane >> 4, j = lane & 15;
+  const bf16* p1 = M + (8 * g + (j >> 2)) * P + 4 * (j & 3);
+  const s4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4_t*)(p1));
+  const s4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4_t*)(p1 + 4 * P));
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  Frag<bf16> f;
+  f.d = make_uint4(ua.x, ua.y, ub.x, ub.y);
+  return f;
+}
+__device__ __forceinline__ Frag<float> ld_frag_t(const float* M, int P, int lane) {
+  const float* p = M + (8 * (lane >> 4)) * P + (lane & 15);
+  Frag<float> f;
+  f.a = make_float4(p[0], p[P], p[2 * P], p[3 * P]);
+  f.b = make_float4(p[4 * P], p[5 * P], p[6 * P], p[7 * P]);
+  return f;
+}
+
+// acc += X . Y^T over klen (multiple of 32). XT / YT: the operand is stored row-major as
+// [k][m] (resp. [k][n]) and is read with transposed fragments; the pointer then addresses
+// element [0][m0] and the pitch is the [k] row pitch.
+template <typename T, bool XT, bool YT>
+__device__ __forceinline__ void mma_tile2(f32x4& acc, const T* X, int px, const T* Y, int py,
+                                          int klen, int lane) {
+  for (int kk = 0; kk < klen; kk += 32) {
+    const Frag<T> a = XT ? ld_frag_t(X + kk * px, px, lane)
+                         : ld_frag(X + (lane & 15) * px + (lane >> 4) * 8 + kk);
+    const Frag<T> b = YT ? ld_frag_t(Y + kk * py, py, lane)
+                         : ld_frag(Y + (lane & 15) * py + (lane >> 4) * 8 + kk);
+    mma(acc, a, b);
+  }
+}
+
 __device__ __forceinline__ f32x4 zero4() {
   f32x4 z = {0.f, 0.f, 0.f, 0.f};
   return z;

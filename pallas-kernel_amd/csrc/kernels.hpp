@@ -63,6 +63,7 @@ struct BwdArgs {
   void *dq, *dk, *dv, *dg;
   float scale;
   int H, K, V;
+  int vec;              // every base pointer 16-byte aligned and K, V multiples of 16 bytes
   SeqInfo si;
 };
 // which: bit 0 = dq/dk/dg kernel, bit 1 = dv kernel
