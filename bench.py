@@ -91,14 +91,15 @@ def _kernel_profile(x, reps=10):
     ht, dh0 = torch.empty_like(x["h0"]), torch.empty_like(x["h0"])
     q, k, v, g, h0, do, dht = (x[n] for n in ("q", "k", "v", "g", "h0", "do", "dht"))
     lay = (B, T, H, K, V, C, *seq.args(), bf, st)
+    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, False, torch.bfloat16, dev)
     tok = B * T * H
     hbytes = seq.NC * H * K * V * BF
     kernels = {
-        "chunk_fwd_fused": (lambda: call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g),
-                                         ptr(h0), ptr(o), ptr(ht), ptr(h), sc, *lay),
-                            tok * (3 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes),
+        "chunk_fwd": (lambda: call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g),
+                                   ptr(h0), ptr(o), ptr(ht), ptr(h), ptr(ws), nws, sc, *lay),
+                      tok * (3 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes),
         "state_scan_bwd": (lambda: call("tops_gla_chunk_bwd_dh", ptr(q), ptr(g), 0, ptr(do),
-                                        ptr(dht), ptr(dh), ptr(dh0), sc, *lay),
+                                        ptr(dht), ptr(dh), ptr(dh0), ptr(ws), nws, sc, *lay),
                            tok * (2 * K + V) * BF + STATE_BYTES * 2 + hbytes),
         "chunk_bwd_dqkg": (lambda: call("tops_gla_chunk_bwd_dqkg", ptr(q), ptr(k), ptr(v),
                                         ptr(g), ptr(h), ptr(do), ptr(dh), ptr(dq), ptr(dk),

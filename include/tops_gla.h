@@ -64,27 +64,31 @@ int tops_gla_chunk_local_cumsum(const void* g, void* out, int64_t B, int64_t T, 
 /*
  * Inter-chunk state scan: h[c] = state entering chunk c ([NC, H, K, V], dtype), and the
  * final state ht [N, H, K, V] (float32). g holds raw log-gates (the chunk-local cumsum is
- * taken in-kernel) or, with g_is_cumsum, the cumsum itself. h0/h/ht may be NULL.
+ * taken in-kernel) or, with g_is_cumsum, the cumsum itself. h0/h/ht may be NULL; seg_ws
+ * as for tops_gla_chunk_fwd.
  * Replaces: chunk_fwd_h_kernel launch, tops/ops/common/chunk_h.py:252-271
  *           (body :18-119; jnp ref tops/ops/gla/chunk.py:206-292).
  */
 int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_cumsum,
-                         const float* h0, void* h, float* ht, int64_t B, int64_t T, int64_t H,
-                         int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                         const float* h0, void* h, float* ht, void* seg_ws,
+                         int64_t seg_ws_bytes, int64_t B, int64_t T, int64_t H, int64_t K,
+                         int64_t V, int chunk_size, const int32_t* cu_seqlens,
                          const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
                          void* stream);
 
 /*
  * Reverse state-gradient scan: dh[c] = dL/d(state leaving chunk c) ([NC, H, K, V], dtype),
- * dh0 [N, H, K, V] float32 (may be NULL). dht may be NULL (zero).
+ * dh0 [N, H, K, V] float32 (may be NULL). dht may be NULL (zero); seg_ws as for
+ * tops_gla_chunk_fwd.
  * Replaces: chunk_bwd_dh_kernel launch, tops/ops/common/chunk_h.py:681-695
  *           (body :495-591; jnp ref chunk_bwd_dh_ref :399-492).
  */
 int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const void* dout,
-                          const float* dht, void* dh, float* dh0, float scale, int64_t B,
-                          int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
-                          const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
-                          int64_t NC, int dtype, void* stream);
+                          const float* dht, void* dh, float* dh0, void* seg_ws,
+                          int64_t seg_ws_bytes, float scale, int64_t B, int64_t T, int64_t H,
+                          int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                          const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                          void* stream);
 
 /*
  * Per-chunk intra matrix and output. A_out (float32, [NC * chunk_size, H, chunk_size],
@@ -102,30 +106,42 @@ int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void
                          void* stream);
 
 /*
- * chunk_gla forward: state scan into h_ws ([NC, H, K, V], dtype, required: it is the
- * residual the backward reuses) then the per-chunk output. h0/ht may be NULL.
+ * Bytes of the optional sequence-segment workspace (`seg_ws`) of tops_gla_chunk_fwd and
+ * tops_gla_chunk_bwd for this problem (0: the call does not use one). With it the
+ * inter-chunk scans of fixed-length sequences run as parallel segments (local states,
+ * a combine, then all segments at once) instead of one chunk after another.
+ * No counterpart in the reference (its scans are sequential grid axes, chunk_h.py:252-271).
+ */
+int64_t tops_gla_chunk_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                                int chunk_size, int varlen, int dtype);
+
+/*
+ * chunk_gla forward: inter-chunk states into h_ws ([NC, H, K, V], dtype, required: it is
+ * the residual the backward reuses) and the per-chunk output. h0/ht may be NULL. seg_ws
+ * (256-byte aligned, seg_ws_bytes >= tops_gla_chunk_ws_bytes) may be NULL.
  * Replaces the device part of chunk_gla_fwd, tops/ops/gla/chunk.py:1145-1166.
  */
 int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* g,
-                       const float* h0, void* o, float* ht, void* h_ws, float scale, int64_t B,
-                       int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
-                       const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
-                       int64_t NC, int dtype, void* stream);
+                       const float* h0, void* o, float* ht, void* h_ws, void* seg_ws,
+                       int64_t seg_ws_bytes, float scale, int64_t B, int64_t T, int64_t H,
+                       int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                       const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                       void* stream);
 
 /*
  * chunk_gla backward: (dq, dk, dv, dg, dh0). `h` are the forward states ([NC, H, K, V]); if
  * NULL they are recomputed into h_ws (then required). dh_ws ([NC, H, K, V], dtype) is
- * required. h0, dht and dh0 may be NULL.
+ * required. h0, dht and dh0 may be NULL; seg_ws as for tops_gla_chunk_fwd.
  * Replaces the device part of chunk_gla_bwd_with_pl, tops/ops/gla/chunk.py:1019-1064
  * (chunk_bwd_dh_kernel + chunk_gla_bwd_fused_pl, :1482-1550).
  */
 int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
                        const float* h0, const void* h, const void* dout, const float* dht,
                        void* dq, void* dk, void* dv, void* dg, float* dh0, void* h_ws,
-                       void* dh_ws, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
-                       int64_t V, int chunk_size, const int32_t* cu_seqlens,
-                       const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
-                       void* stream);
+                       void* dh_ws, void* seg_ws, int64_t seg_ws_bytes, float scale,
+                       int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
+                       const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                       int64_t NC, int dtype, void* stream);
 
 /*
  * Per-chunk dq, dk, dg of the backward (intra-chunk dA computed in-kernel) from the forward

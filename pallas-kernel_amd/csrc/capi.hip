@@ -106,6 +106,32 @@ int check_mfma_common(int64_t K, int64_t V, int chunk, int dtype) {
   return TOPS_GLA_OK;
 }
 
+// The full-head kernels: bf16, chunk 64, K and V <= 128 (multiples of 8), raw gates, every
+// pointer 16-byte aligned (NULL counts as aligned).
+bool use_head(int dtype, int chunk, int64_t K, int64_t V, bool g_is_cumsum,
+              std::initializer_list<const void*> ptrs) {
+  if (!tops::head_supported(dtype, chunk, (int)K, (int)V, g_is_cumsum)) return false;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return false;
+  return true;
+}
+
+// Sequence segmentation of the full-head kernels when the caller's workspace holds it
+// (state part first, then the decays); otherwise NS = 1.
+void seg_setup(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void* ws,
+               int64_t ws_bytes, int& NS, int& SL, float*& st, float*& gm) {
+  tops::head_seg_plan(si.N, (int)H, si.T, si.C, si.cu != nullptr, NS, SL);
+  const long need = tops::head_seg_ws_bytes(si.N, NS, (int)H, (int)K, (int)V);
+  st = gm = nullptr;
+  if (NS <= 1 || ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 255u) != 0) {
+    NS = 1;
+    SL = 0;
+    return;
+  }
+  st = (float*)ws;
+  gm = (float*)((char*)ws + (long)si.N * NS * H * K * V * 4);
+}
+
 }  // namespace
 
 extern "C" {
@@ -113,6 +139,15 @@ extern "C" {
 const char* tops_gla_last_error(void) { return g_err; }
 
 const char* tops_gla_version(void) { return "tops-gla-mi355x 0.1.0 (gfx950)"; }
+
+int64_t tops_gla_chunk_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                                int chunk_size, int varlen, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || K > 128 || V > 128) return 0;
+  if (!tops::head_supported(dtype, chunk_size, (int)K, (int)V, false)) return 0;
+  int NS, SL;
+  tops::head_seg_plan((int)B, (int)H, (int)T, chunk_size, varlen != 0, NS, SL);
+  return tops::head_seg_ws_bytes((int)B, NS, (int)H, (int)K, (int)V);
+}
 
 int tops_gla_chunk_local_cumsum(const void* g, void* out, int64_t B, int64_t T, int64_t H,
                                 int64_t S, int chunk_size, int reverse, int has_scale,
@@ -146,8 +181,9 @@ int tops_gla_chunk_local_cumsum(const void* g, void* out, int64_t B, int64_t T, 
 }
 
 int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_cumsum,
-                         const float* h0, void* h, float* ht, int64_t B, int64_t T, int64_t H,
-                         int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                         const float* h0, void* h, float* ht, void* seg_ws,
+                         int64_t seg_ws_bytes, int64_t B, int64_t T, int64_t H, int64_t K,
+                         int64_t V, int chunk_size, const int32_t* cu_seqlens,
                          const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
                          void* stream) {
   int rc = check_mfma_common(K, V, chunk_size, dtype);
@@ -157,6 +193,22 @@ int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_c
   if (rc) return rc;
   if ((k == nullptr || v == nullptr || g == nullptr) && B * T > 0)
     return fail(TOPS_GLA_EINVAL, "k, v and g must not be NULL");
+  if (use_head(dtype, chunk_size, K, V, g_is_cumsum != 0, {k, v, g, h0, h, ht})) {
+    tops::HeadScanArgs s = {};
+    s.a = k;
+    s.b = v;
+    s.g = g;
+    s.s_init = h0;
+    s.s_all = h;
+    s.s_final = ht;
+    seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, s.NS, s.SL, s.seg_state, s.seg_gam);
+    s.scale = 1.f;
+    s.H = (int)H;
+    s.K = (int)K;
+    s.V = (int)V;
+    s.si = si;
+    return hip_status(tops::run_head_scan(s, false, (hipStream_t)stream), "chunk_fwd_h");
+  }
   tops::ScanArgs p;
   p.a = k;
   p.b = v;
@@ -175,10 +227,11 @@ int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_c
 }
 
 int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const void* dout,
-                          const float* dht, void* dh, float* dh0, float scale, int64_t B,
-                          int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
-                          const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
-                          int64_t NC, int dtype, void* stream) {
+                          const float* dht, void* dh, float* dh0, void* seg_ws,
+                          int64_t seg_ws_bytes, float scale, int64_t B, int64_t T, int64_t H,
+                          int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                          const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                          void* stream) {
   int rc = check_mfma_common(K, V, chunk_size, dtype);
   if (rc) return rc;
   tops::SeqInfo si;
@@ -186,6 +239,22 @@ int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const v
   if (rc) return rc;
   if ((q == nullptr || dout == nullptr || g == nullptr) && B * T > 0)
     return fail(TOPS_GLA_EINVAL, "q, g and do must not be NULL");
+  if (use_head(dtype, chunk_size, K, V, g_is_cumsum != 0, {q, dout, g, dht, dh, dh0})) {
+    tops::HeadScanArgs s = {};
+    s.a = q;
+    s.b = dout;
+    s.g = g;
+    s.s_init = dht;
+    s.s_all = dh;
+    s.s_final = dh0;
+    seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, s.NS, s.SL, s.seg_state, s.seg_gam);
+    s.scale = scale;
+    s.H = (int)H;
+    s.K = (int)K;
+    s.V = (int)V;
+    s.si = si;
+    return hip_status(tops::run_head_scan(s, true, (hipStream_t)stream), "chunk_bwd_dh");
+  }
   tops::ScanArgs p;
   p.a = q;
   p.b = dout;
@@ -240,10 +309,11 @@ int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void
 }
 
 int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* g,
-                       const float* h0, void* o, float* ht, void* h_ws, float scale, int64_t B,
-                       int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
-                       const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
-                       int64_t NC, int dtype, void* stream) {
+                       const float* h0, void* o, float* ht, void* h_ws, void* seg_ws,
+                       int64_t seg_ws_bytes, float scale, int64_t B, int64_t T, int64_t H,
+                       int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                       const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                       void* stream) {
   int rc = check_mfma_common(K, V, chunk_size, dtype);
   if (rc) return rc;
   tops::SeqInfo si;
@@ -253,6 +323,24 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
                     o == nullptr || h_ws == nullptr))
     return fail(TOPS_GLA_EINVAL, "q, k, v, g, o and h_ws must not be NULL");
   hipStream_t st = (hipStream_t)stream;
+  if (use_head(dtype, chunk_size, K, V, false, {q, k, v, g, h0, o, ht, h_ws})) {
+    tops::HeadFwdArgs f = {};
+    f.q = q;
+    f.k = k;
+    f.v = v;
+    f.g = g;
+    f.h0 = h0;
+    f.o = o;
+    f.h_out = h_ws;
+    f.ht = ht;
+    seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, f.NS, f.SL, f.seg_state, f.seg_gam);
+    f.scale = scale;
+    f.H = (int)H;
+    f.K = (int)K;
+    f.V = (int)V;
+    f.si = si;
+    return hip_status(tops::run_head_fwd(f, st), "chunk_fwd (full-head)");
+  }
   if (tops::fused_fwd_supported(dtype, chunk_size, (int)K)) {
     tops::FusedFwdArgs f;
     f.q = q;
@@ -310,10 +398,10 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
 int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
                        const float* h0, const void* h, const void* dout, const float* dht,
                        void* dq, void* dk, void* dv, void* dg, float* dh0, void* h_ws,
-                       void* dh_ws, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
-                       int64_t V, int chunk_size, const int32_t* cu_seqlens,
-                       const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
-                       void* stream) {
+                       void* dh_ws, void* seg_ws, int64_t seg_ws_bytes, float scale,
+                       int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
+                       const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                       int64_t NC, int dtype, void* stream) {
   int rc = check_mfma_common(K, V, chunk_size, dtype);
   if (rc) return rc;
   tops::SeqInfo si;
@@ -326,6 +414,37 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   if (h == nullptr && h_ws == nullptr && B * T > 0)
     return fail(TOPS_GLA_EINVAL, "h_ws is required when h is NULL");
   hipStream_t st = (hipStream_t)stream;
+  const bool head = use_head(dtype, chunk_size, K, V, false, {q, k, v, g, h0, h, dout, dht,
+                                                              dh0, h_ws, dh_ws});
+  int NS = 1, SL = 0;
+  float *seg_st = nullptr, *seg_gm = nullptr;
+  if (head) seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, NS, SL, seg_st, seg_gm);
+  auto head_scan = [&](bool rev, const void* a, const void* b, const float* s_init, void* s_all,
+                       float* s_final, float sc) {
+    tops::HeadScanArgs s = {};
+    s.a = a;
+    s.b = b;
+    s.g = g;
+    s.s_init = s_init;
+    s.s_all = s_all;
+    s.s_final = s_final;
+    s.seg_state = seg_st;
+    s.seg_gam = seg_gm;
+    s.NS = NS;
+    s.SL = SL;
+    s.scale = sc;
+    s.H = (int)H;
+    s.K = (int)K;
+    s.V = (int)V;
+    s.si = si;
+    return tops::run_head_scan(s, rev, st);
+  };
+  if (h == nullptr && head) {
+    rc = hip_status(head_scan(false, k, v, h0, h_ws, nullptr, 1.f),
+                    "chunk_bwd (state recompute)");
+    if (rc) return rc;
+    h = h_ws;
+  }
   if (h == nullptr) {
     tops::ScanArgs s;
     s.a = k;
@@ -345,22 +464,27 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     if (rc) return rc;
     h = h_ws;
   }
-  tops::ScanArgs d;
-  d.a = q;
-  d.b = dout;
-  d.g = g;
-  d.g_is_cumsum = 0;
-  d.s_init = dht;
-  d.s_all = dh_ws;
-  d.s_final = dh0;
-  d.scale = scale;
-  d.H = (int)H;
-  d.K = (int)K;
-  d.V = (int)V;
-  d.vec = vec_ok(dtype, K, V, {q, dout, g, dh_ws});
-  d.si = si;
-  rc = hip_status(tops::run_state_scan(d, true, dtype, st), "chunk_bwd (dh scan)");
-  if (rc) return rc;
+  if (head) {
+    rc = hip_status(head_scan(true, q, dout, dht, dh_ws, dh0, scale), "chunk_bwd (dh scan)");
+    if (rc) return rc;
+  } else {
+    tops::ScanArgs d;
+    d.a = q;
+    d.b = dout;
+    d.g = g;
+    d.g_is_cumsum = 0;
+    d.s_init = dht;
+    d.s_all = dh_ws;
+    d.s_final = dh0;
+    d.scale = scale;
+    d.H = (int)H;
+    d.K = (int)K;
+    d.V = (int)V;
+    d.vec = vec_ok(dtype, K, V, {q, dout, g, dh_ws});
+    d.si = si;
+    rc = hip_status(tops::run_state_scan(d, true, dtype, st), "chunk_bwd (dh scan)");
+    if (rc) return rc;
+  }
   tops::BwdArgs p;
   p.q = q;
   p.k = k;

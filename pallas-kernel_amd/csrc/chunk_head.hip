@@ -1,0 +1,760 @@
+// Full-head chunked-GLA kernels (bf16, chunk 64, K and V up to 128): one 512-thread block
+// (8 waves, two per SIMD) owns the whole K x V state of one (sequence, head) -- or of one
+// segment of a sequence -- and walks its chunks in order.
+//
+// Reference semantics: state scan tops/ops/common/chunk_h.py:18-119 (forward h) and
+// :399-591 (reverse dh); fused forward chunk_gla_fwd, tops/ops/gla/chunk.py:1083-1179.
+//
+// Layout of the per-chunk work (C = 64 rows):
+//  * every thread owns one 8-column group and RPT consecutive rows of the q / k / g tiles
+//    (and of the v / do tile); its 16-byte global loads land in registers in exactly that
+//    shape, so the chunk-local cumsum of g runs in registers: a local cumsum over the
+//    thread's rows, a lane-shuffle prefix over the row segments of a wave, and one LDS
+//    exchange of the eight wave totals. Gates are carried in base 2 (g * log2 e), so every
+//    gate factor is one hardware exp2;
+//  * loads are unconditional (rows and columns clamped into the tensor); invalid pieces are
+//    zeroed as raw 16-byte words when consumed;
+//  * gated tiles are written to LDS row-major with 16-byte stores; MFMA operands that are
+//    needed transposed (v^T, k_d^T, h'^T) are read with transposed fragments;
+//  * the K x V state lives in MFMA accumulators, out[v][k]: a lane's four values are four
+//    consecutive v of one k (one 8-byte store into the [.., K, V] state layout). Wave w
+//    holds v tiles of half (w & 1) and k tiles of quarter (w >> 1).
+//
+// Sequence segments: with NS > 1 the chunks of a sequence are split into NS segments of SL
+// chunks. Pass 1 (head_scan_kernel, pass 1) computes every segment's local final state
+// (from a zero state; the first segment in flow order starts from the given initial state)
+// and the segment's total log2 decay; head_combine_kernel turns them into the state
+// entering every segment; pass 3 (head_scan_kernel pass 3, or head_fwd_kernel) then walks
+// all segments in parallel from those states. State composition over a segment is exact:
+// h_out = 2^{Gamma} h_in + L with Gamma the summed (base-2) gates of the segment.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace tops {
+
+namespace {
+
+constexpr int HC = 64;    // chunk size of the full-head kernels
+constexpr int HNT = 512;  // threads per block
+constexpr int HNW = HNT / 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int KP>
+struct HMap {
+  static constexpr int NCG = KP / 8;     // 8-column groups
+  static constexpr int NRS = HNT / NCG;  // row segments
+  static constexpr int RPT = HC / NRS;   // rows per thread
+  static_assert(RPT >= 1 && NRS * RPT == HC, "thread mapping");
+};
+
+// State / output tile split over the 8 waves: v tiles by halves, k tiles by quarters.
+template <int KP, int VP>
+struct HTiles {
+  static constexpr int NTV = VP / 16 / 2;   // v tiles per wave
+  static constexpr int NTK = KP / 16 / 4;   // k tiles per wave
+};
+
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ void unpack8(const uint4& u, float (&x)[8]) {
+  x[0] = bf16_lo(u.x); x[1] = bf16_hi(u.x);
+  x[2] = bf16_lo(u.y); x[3] = bf16_hi(u.y);
+  x[4] = bf16_lo(u.z); x[5] = bf16_hi(u.z);
+  x[6] = bf16_lo(u.w); x[7] = bf16_hi(u.w);
+}
+__device__ __forceinline__ uint4 pack8(const float (&x)[8]) {
+  return make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]),
+                    pack2_bf16(x[6], x[7]));
+}
+__device__ __forceinline__ void st_f8(float* p, const float (&x)[8]) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(x[0], x[1], x[2], x[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(x[4], x[5], x[6], x[7]);
+}
+__device__ __forceinline__ void ld_f8(const float* p, float (&x)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+
+// RPT rows x 16 bytes starting at (row0, col0) of a row-major tile with row stride rs.
+// Unconditional: rows are clamped to len-1 and the column to w-8 (w % 8 == 0, w >= 8);
+// the caller masks what it consumes.
+template <int RPT>
+__device__ __forceinline__ void hload(uint4 (&r)[RPT], const bf16* __restrict__ base, long rs,
+                                      int row0, int len, int col0, int w) {
+  const int c = min(col0, w - 8);
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int row = min(row0 + j, len - 1);
+    r[j] = *reinterpret_cast<const uint4*>(base + (long)row * rs + c);
+  }
+}
+
+// Chunk range of the block's segment.
+struct Seg {
+  int seq, s, bos, eos, c0, cb, ce;
+};
+__device__ __forceinline__ Seg seg_of(const SeqInfo& si, int seq, int s, int NS, int SL) {
+  Seg r;
+  int nc;
+  seq_range(si, seq, r.bos, r.eos, r.c0, nc);
+  r.seq = seq;
+  r.s = s;
+  r.cb = NS > 1 ? min(nc, s * SL) : 0;
+  r.ce = NS > 1 ? min(nc, r.cb + SL) : nc;
+  return r;
+}
+
+// Base-2 chunk-local cumsum of an [HC x KP] gate tile held as RPT rows x 8 columns per
+// thread (raw, already masked). Out: gt = g~ log2 e, gam = its last row, first = its row 0.
+// sTot [HNW][KP], sFirst [KP]. One barrier.
+template <int KP>
+__device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP>::RPT],
+                                            float (&gt)[HMap<KP>::RPT][8], float (&gam)[8],
+                                            float (&first)[8], float* sTot, float* sFirst,
+                                            int cg, int rs, int lane, int w) {
+  using M = HMap<KP>;
+#pragma unroll
+  for (int j = 0; j < M::RPT; ++j) {
+    unpack8(graw[j], gt[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gt[j][e] = gt[j][e] * kLog2e + (j ? gt[j - 1][e] : 0.f);
+  }
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = gt[M::RPT - 1][e];
+#pragma unroll
+  for (int d = M::NCG; d < 64; d <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = __shfl_up(x[e], d);
+      if (lane >= d) x[e] += y;
+    }
+  }
+  if (lane >= 64 - M::NCG) st_f8(sTot + w * KP + cg * 8, x);   // wave total
+  if (rs == 0) st_f8(sFirst + cg * 8, gt[0]);
+  __syncthreads();
+  float off[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    off[e] = x[e] - gt[M::RPT - 1][e];   // exclusive prefix within the wave
+    gam[e] = 0.f;
+  }
+#pragma unroll
+  for (int ww = 0; ww < HNW; ++ww) {
+    float t[8];
+    ld_f8(sTot + ww * KP + cg * 8, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      gam[e] += t[e];
+      if (ww < w) off[e] += t[e];
+    }
+  }
+  ld_f8(sFirst + cg * 8, first);
+#pragma unroll
+  for (int j = 0; j < M::RPT; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gt[j][e] += off[e];
+}
+
+// A float routed through a VGPR. An accumulator initialised straight from a global load is
+// loaded into the accumulator registers, which makes the compiler drain every outstanding
+// load at the top of the chunk loop.
+__device__ __forceinline__ float via_vgpr(float x) {
+  float y;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
+  return y;
+}
+
+template <int NTV, int NTK>
+__device__ __forceinline__ void load_state(f32x4 (&acc)[NTV][NTK], const float* init, int K,
+                                           int V, int vt0, int kt0, int lane) {
+#pragma unroll
+  for (int i = 0; i < NTV; ++i)
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) {
+      acc[i][j] = zero4();
+      const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
+      if (init && kk < K && vv < V) {
+        const float4 x = *reinterpret_cast<const float4*>(init + (long)kk * V + vv);
+        acc[i][j][0] = via_vgpr(x.x);
+        acc[i][j][1] = via_vgpr(x.y);
+        acc[i][j][2] = via_vgpr(x.z);
+        acc[i][j][3] = via_vgpr(x.w);
+      }
+    }
+}
+
+template <int NTV, int NTK>
+__device__ __forceinline__ void store_state_f32(const f32x4 (&acc)[NTV][NTK], float* dst,
+                                                int K, int V, int vt0, int kt0, int lane) {
+#pragma unroll
+  for (int i = 0; i < NTV; ++i)
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) {
+      const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
+      if (kk < K && vv < V)
+        *reinterpret_cast<float4*>(dst + (long)kk * V + vv) =
+            make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+    }
+}
+
+template <int NTV, int NTK>
+__device__ __forceinline__ void store_state_bf16(const f32x4 (&acc)[NTV][NTK], bf16* dst,
+                                                 int K, int V, int vt0, int kt0, int lane) {
+#pragma unroll
+  for (int i = 0; i < NTV; ++i)
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) {
+      const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
+      if (kk < K && vv < V)
+        *reinterpret_cast<uint2*>(dst + (long)kk * V + vv) =
+            make_uint2(pack2_bf16(acc[i][j][0], acc[i][j][1]),
+                       pack2_bf16(acc[i][j][2], acc[i][j][3]));
+    }
+}
+
+// acc = acc * decay[k] + X^T Y over the chunk: X = b [c][v] (sB), Y = a [c][k] (sA), both
+// read with transposed fragments.
+template <int NTV, int NTK>
+__device__ __forceinline__ void state_update(f32x4 (&acc)[NTV][NTK], const bf16* sB, int PB,
+                                             const bf16* sA, int PA, const float* decay,
+                                             int vt0, int kt0, int lane) {
+#pragma unroll
+  for (int j = 0; j < NTK; ++j) {
+    const float d = decay[(kt0 + j) * 16 + (lane & 15)];
+#pragma unroll
+    for (int i = 0; i < NTV; ++i) acc[i][j] *= d;
+  }
+#pragma unroll
+  for (int kk = 0; kk < HC; kk += 32) {
+    Frag<bf16> x[NTV], y[NTK];
+#pragma unroll
+    for (int i = 0; i < NTV; ++i) x[i] = ld_frag_t(sB + kk * PB + (vt0 + i) * 16, PB, lane);
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) y[j] = ld_frag_t(sA + kk * PA + (kt0 + j) * 16, PA, lane);
+#pragma unroll
+    for (int i = 0; i < NTV; ++i)
+#pragma unroll
+      for (int j = 0; j < NTK; ++j) mma(acc[i][j], x[i], y[j]);
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// State scan: forward h (a = k, b = v) or reverse dh (a = q, b = do)
+// ---------------------------------------------------------------------------
+template <int KP, int VP, bool REV>
+__global__ __launch_bounds__(HNT) void head_scan_kernel(HeadScanArgs p) {
+  using MA = HMap<KP>;
+  using MB = HMap<VP>;
+  using TL = HTiles<KP, VP>;
+  constexpr int RPT = MA::RPT, VRPT = MB::RPT;
+  constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP);
+  constexpr int NTV = TL::NTV, NTK = TL::NTK;
+  __shared__ __attribute__((aligned(16))) bf16 sA[HC * PKP];
+  __shared__ __attribute__((aligned(16))) bf16 sB[HC * PVP];
+  __shared__ __attribute__((aligned(16))) float sTot[HNW * KP];
+  __shared__ __attribute__((aligned(16))) float sFirst[KP];
+  __shared__ __attribute__((aligned(16))) float sGam[KP];
+
+  const bf16* __restrict__ a = (const bf16*)p.a;
+  const bf16* __restrict__ b = (const bf16*)p.b;
+  const bf16* __restrict__ g = (const bf16*)p.g;
+  bf16* __restrict__ s_all = (bf16*)p.s_all;
+  const int H = p.H, K = p.K, V = p.V;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int hh = L % H;
+  const int nsl = p.ns_launch;
+  const int s = p.s_begin + (L / H) % nsl;
+  const Seg sg = seg_of(p.si, (L / H) / nsl, s, p.NS, p.SL);
+  const int nsteps = sg.ce - sg.cb;
+  const bool first_seg = REV ? (s == p.NS - 1) : (s == 0);
+  const bool last_seg = REV ? (s == 0) : (s == p.NS - 1);
+  const long rsK = (long)H * K, rsV = (long)H * V;
+  const long KV = (long)K * V;
+
+  const int cg = tid % MA::NCG, rs = tid / MA::NCG;    // a / g mapping
+  const int vg = tid % MB::NCG, vrs = tid / MB::NCG;   // b mapping
+  const bool colA = cg * 8 < K, colB = vg * 8 < V;
+
+  const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
+  f32x4 acc[NTV][NTK];
+  {
+    const float* init = nullptr;
+    if (first_seg)
+      init = p.s_init ? p.s_init + ((long)sg.seq * H + hh) * KV : nullptr;
+    else if (p.pass == 3)
+      init = p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV;
+    load_state<NTV, NTK>(acc, init, K, V, vt0, kt0, lane);
+  }
+
+  struct Regs {
+    uint4 a[RPT], g[RPT], b[VRPT];
+  };
+  auto issue = [&](int step, Regs& R) {
+    const int st = min(step, nsteps - 1);
+    const int ci = REV ? (sg.ce - 1 - st) : (sg.cb + st);
+    const int t0 = sg.bos + ci * HC;
+    const int len = min(HC, sg.eos - t0);
+    const long oa = (long)t0 * rsK + (long)hh * K;
+    hload<RPT>(R.a, a + oa, rsK, rs * RPT, len, cg * 8, K);
+    hload<RPT>(R.g, g + oa, rsK, rs * RPT, len, cg * 8, K);
+    hload<VRPT>(R.b, b + (long)t0 * rsV + (long)hh * V, rsV, vrs * VRPT, len, vg * 8, V);
+  };
+
+  float gsum[8];   // pass 1: total base-2 decay of the segment
+#pragma unroll
+  for (int e = 0; e < 8; ++e) gsum[e] = 0.f;
+
+  auto body = [&](int step, Regs& R) {
+    const int ci = REV ? (sg.ce - 1 - step) : (sg.cb + step);
+    const int t0 = sg.bos + ci * HC;
+    const int len = min(HC, sg.eos - t0);
+    uint4 gm[RPT];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+      gm[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
+    float gt[RPT][8], gam[8], first[8];
+    head_cumsum<KP>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+    (void)first;
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int row = rs * RPT + j;
+      float x[8];
+      unpack8(mask16(R.a[j], (colA && row < len) ? ~0u : 0u), x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        x[e] *= REV ? p.scale * exp2_hw(gt[j][e]) : exp2_hw(gam[e] - gt[j][e]);
+      *reinterpret_cast<uint4*>(sA + row * PKP + cg * 8) = pack8(x);
+    }
+#pragma unroll
+    for (int j = 0; j < VRPT; ++j) {
+      const int row = vrs * VRPT + j;
+      *reinterpret_cast<uint4*>(sB + row * PVP + vg * 8) =
+          mask16(R.b[j], (colB && row < len) ? ~0u : 0u);
+    }
+    if (rs == 0) {
+      float eg[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        eg[e] = exp2_hw(gam[e]);
+        gsum[e] += gam[e];
+      }
+      st_f8(sGam + cg * 8, eg);
+    }
+    issue(step + 2, R);
+    __syncthreads();
+    if (s_all)   // state entering the chunk (forward) / leaving it (reverse)
+      store_state_bf16<NTV, NTK>(acc, s_all + ((long)(sg.c0 + ci) * H + hh) * KV, K, V, vt0,
+                                 kt0, lane);
+    state_update<NTV, NTK>(acc, sB, PVP, sA, PKP, sGam, vt0, kt0, lane);
+  };
+
+  if (nsteps > 0) {
+    // The first chunk is peeled so that the loop is entered with the same sequence of
+    // outstanding loads and stores as its back edge.
+    Regs R0, R1;
+    issue(0, R0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(1, R1);
+    body(0, R0);
+    for (int step = 1; step < nsteps; step += 2) {
+      body(step, R1);
+      if (step + 1 < nsteps) body(step + 1, R0);
+    }
+  }
+
+  if (p.pass == 1) {
+    store_state_f32<NTV, NTK>(acc, p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV, K,
+                              V, vt0, kt0, lane);
+    if (rs == 0 && colA)
+      st_f8(p.seg_gam + ((long)(sg.seq * p.NS + s) * H + hh) * K + cg * 8, gsum);
+  } else if (last_seg && p.s_final) {
+    store_state_f32<NTV, NTK>(acc, p.s_final + ((long)sg.seq * H + hh) * KV, K, V, vt0, kt0,
+                              lane);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Segment combine: seg_state[s] <- state entering segment s (flow order), from the local
+// states L_s (pass 1) and the base-2 segment decays Gamma_s.
+//   forward: H_1 = L_0, H_{s+1} = 2^{Gamma_s} H_s + L_s
+//   reverse: D_{NS-2} = L_{NS-1}, D_{s-1} = 2^{Gamma_s} D_s + L_s
+// One thread per (sequence, head, k, v) element.
+// ---------------------------------------------------------------------------
+template <bool REV>
+__global__ __launch_bounds__(256) void head_combine_kernel(float* __restrict__ st,
+                                                           const float* __restrict__ gm, int N,
+                                                           int NS, int H, int K, int V) {
+  const long KV = (long)K * V;
+  const long total = (long)N * H * KV;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const long kv = i % KV;
+  const int hh = (int)((i / KV) % H), seq = (int)(i / (KV * H));
+  const int kk = (int)(kv / V);
+  auto at = [&](int s) -> long { return ((long)(seq * NS + s) * H + hh) * KV + kv; };
+  auto gam = [&](int s) -> float { return gm[((long)(seq * NS + s) * H + hh) * K + kk]; };
+  if (!REV) {
+    float h = st[at(0)];
+    for (int s = 1; s < NS; ++s) {
+      const float l = s < NS - 1 ? st[at(s)] : 0.f;
+      st[at(s)] = h;
+      if (s < NS - 1) h = exp2_hw(gam(s)) * h + l;
+    }
+  } else {
+    float d = st[at(NS - 1)];
+    for (int s = NS - 2; s >= 0; --s) {
+      const float l = s > 0 ? st[at(s)] : 0.f;
+      st[at(s)] = d;
+      if (s > 0) d = exp2_hw(gam(s)) * d + l;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused forward: per chunk (base-2 gates, r = (g~_first + gamma) / 2 per column)
+//   qg = q 2^{g~-r}, kg = k 2^{r-g~}, kd = kg 2^{gamma-r}, A = scale tril(qg kg^T),
+//   o = A v + qg (scale 2^r h), h <- 2^{gamma} h + kd^T v.
+// ---------------------------------------------------------------------------
+template <int KP, int VP>
+struct HFLayout {
+  static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP),
+                       PA = pitch_of<bf16>(HC);
+  static constexpr int qg = 0;
+  static constexpr int kg = qg + HC * PKP * 2;
+  static constexpr int kd = kg + HC * PKP * 2;
+  static constexpr int v = kd + HC * PKP * 2;
+  static constexpr int hk = v + HC * PVP * 2;      // h' [k][v]
+  static constexpr int a = hk + KP * PVP * 2;      // A  [i][j]
+  static constexpr int tot = a + HC * PA * 2;
+  static constexpr int first = tot + HNW * KP * 4;
+  static constexpr int gam = first + KP * 4;
+  static constexpr int rsc = gam + KP * 4;
+  static constexpr int bytes = rsc + KP * 4;
+};
+
+template <int KP, int VP>
+__global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
+  using M = HMap<KP>;
+  using MV = HMap<VP>;
+  using TL = HTiles<KP, VP>;
+  using Lay = HFLayout<KP, VP>;
+  constexpr int RPT = M::RPT, VRPT = MV::RPT;
+  constexpr int PKP = Lay::PKP, PVP = Lay::PVP, PA = Lay::PA;
+  constexpr int NTV = TL::NTV, NTK = TL::NTK;
+  static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
+  bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
+  bf16* sKd = reinterpret_cast<bf16*>(smem + Lay::kd);
+  bf16* sV = reinterpret_cast<bf16*>(smem + Lay::v);
+  bf16* sHk = reinterpret_cast<bf16*>(smem + Lay::hk);
+  bf16* sA = reinterpret_cast<bf16*>(smem + Lay::a);
+  float* sTot = reinterpret_cast<float*>(smem + Lay::tot);
+  float* sFirst = reinterpret_cast<float*>(smem + Lay::first);
+  float* sGam = reinterpret_cast<float*>(smem + Lay::gam);
+  float* sRs = reinterpret_cast<float*>(smem + Lay::rsc);
+
+  const bf16* __restrict__ q = (const bf16*)p.q;
+  const bf16* __restrict__ k = (const bf16*)p.k;
+  const bf16* __restrict__ v = (const bf16*)p.v;
+  const bf16* __restrict__ g = (const bf16*)p.g;
+  bf16* __restrict__ o = (bf16*)p.o;
+  bf16* __restrict__ hout = (bf16*)p.h_out;
+  const int H = p.H, K = p.K, V = p.V;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int hh = L % H;
+  const int s = (L / H) % p.NS;
+  const Seg sg = seg_of(p.si, (L / H) / p.NS, s, p.NS, p.SL);
+  const int nsteps = sg.ce - sg.cb;
+  const long rsK = (long)H * K, rsV = (long)H * V;
+  const long KV = (long)K * V;
+
+  const int cg = tid % M::NCG, rs = tid / M::NCG;
+  const int vg = tid % MV::NCG, vrs = tid / MV::NCG;
+  const bool colA = cg * 8 < K, colB = vg * 8 < V;
+
+  // zero A once (its upper triangle is never written)
+  for (int i = tid; i < HC * PA / 8; i += HNT)
+    reinterpret_cast<uint4*>(sA)[i] = make_uint4(0, 0, 0, 0);
+
+  const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
+  f32x4 acc[NTV][NTK];
+  {
+    const float* init = s == 0 ? (p.h0 ? p.h0 + ((long)sg.seq * H + hh) * KV : nullptr)
+                               : p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV;
+    load_state<NTV, NTK>(acc, init, K, V, vt0, kt0, lane);
+  }
+
+  struct Regs {
+    uint4 q[RPT], k[RPT], g[RPT], v[VRPT];
+  };
+  auto issue = [&](int step, Regs& R) {
+    const int st = min(step, nsteps - 1);
+    const int t0 = sg.bos + (sg.cb + st) * HC;
+    const int len = min(HC, sg.eos - t0);
+    const long oa = (long)t0 * rsK + (long)hh * K;
+    hload<RPT>(R.q, q + oa, rsK, rs * RPT, len, cg * 8, K);
+    hload<RPT>(R.k, k + oa, rsK, rs * RPT, len, cg * 8, K);
+    hload<RPT>(R.g, g + oa, rsK, rs * RPT, len, cg * 8, K);
+    hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V, rsV, vrs * VRPT, len, vg * 8, V);
+  };
+
+  auto body = [&](int step, Regs& R) {
+    const int ci = sg.cb + step;
+    const int t0 = sg.bos + ci * HC;
+    const int len = min(HC, sg.eos - t0);
+
+    // ---- (1) cumsum, gating ----
+    uint4 gmk[RPT];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+      gmk[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
+    float gt[RPT][8], gam[8], first[8];
+    head_cumsum<KP>(gmk, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+    float r[8], fkd[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      r[e] = 0.5f * (first[e] + gam[e]);
+      fkd[e] = exp2_hw(gam[e] - r[e]);
+    }
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int row = rs * RPT + j;
+      const uint32_t m = (colA && row < len) ? ~0u : 0u;
+      float xq[8], xk[8], xd[8];
+      unpack8(mask16(R.q[j], m), xq);
+      unpack8(mask16(R.k[j], m), xk);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = gt[j][e] - r[e];
+        xq[e] *= exp2_hw(d);
+        xk[e] *= exp2_hw(-d);
+        xd[e] = xk[e] * fkd[e];
+      }
+      *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pack8(xq);
+      *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pack8(xk);
+      *reinterpret_cast<uint4*>(sKd + row * PKP + cg * 8) = pack8(xd);
+    }
+#pragma unroll
+    for (int j = 0; j < VRPT; ++j) {
+      const int row = vrs * VRPT + j;
+      *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) =
+          mask16(R.v[j], (colB && row < len) ? ~0u : 0u);
+    }
+    if (rs == 0) {
+      float eg[8], er[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        eg[e] = exp2_hw(gam[e]);
+        er[e] = p.scale * exp2_hw(r[e]);
+      }
+      st_f8(sGam + cg * 8, eg);
+      st_f8(sRs + cg * 8, er);
+    }
+    issue(step + 2, R);
+    __syncthreads();
+
+    // ---- (2) A (lower tiles), h_n to HBM, h' = scale 2^r h into LDS ----
+    for (int t = w; t < 10; t += HNW) {
+      const int mi = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
+      const int ni = t - mi * (mi + 1) / 2;
+      f32x4 at = zero4();
+      mma_tile<bf16>(at, sQg + mi * 16 * PKP, PKP, sKg + ni * 16 * PKP, PKP, KP, lane);
+      const int jj = ni * 16 + (lane & 15);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int ii = mi * 16 + 4 * (lane >> 4) + rr;
+        sA[ii * PA + jj] = from_f32<bf16>(jj <= ii ? at[rr] * p.scale : 0.f);
+      }
+    }
+    if (hout)
+      store_state_bf16<NTV, NTK>(acc, hout + ((long)(sg.c0 + ci) * H + hh) * KV, K, V, vt0,
+                                 kt0, lane);
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) {
+      const int kk = (kt0 + j) * 16 + (lane & 15);
+      const float f = sRs[kk];
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) {
+        const int vv = (vt0 + i) * 16 + 4 * (lane >> 4);
+        *reinterpret_cast<uint2*>(sHk + kk * PVP + vv) =
+            make_uint2(pack2_bf16(acc[i][j][0] * f, acc[i][j][1] * f),
+                       pack2_bf16(acc[i][j][2] * f, acc[i][j][3] * f));
+      }
+    }
+    __syncthreads();
+
+    // ---- (3) o^T = v^T A^T + h'^T qg^T (wave: v tiles of half w&1, row tile w>>1) ----
+    {
+      const int it = w >> 1;
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) {
+        const int vt = vt0 + i;
+        f32x4 ot = zero4();
+        mma_tile2<bf16, true, false>(ot, sV + vt * 16, PVP, sA + it * 16 * PA, PA, HC, lane);
+        mma_tile2<bf16, true, false>(ot, sHk + vt * 16, PVP, sQg + it * 16 * PKP, PKP, KP,
+                                     lane);
+        const int row = it * 16 + (lane & 15);
+        const int vv = vt * 16 + 4 * (lane >> 4);
+        if (row < len && vv < V)
+          *reinterpret_cast<uint2*>(o + (long)(t0 + row) * rsV + (long)hh * V + vv) =
+              make_uint2(pack2_bf16(ot[0], ot[1]), pack2_bf16(ot[2], ot[3]));
+      }
+    }
+    state_update<NTV, NTK>(acc, sV, PVP, sKd, PKP, sGam, vt0, kt0, lane);
+  };
+
+  if (nsteps > 0) {
+    Regs R0, R1;
+    issue(0, R0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(1, R1);
+    body(0, R0);
+    for (int step = 1; step < nsteps; step += 2) {
+      body(step, R1);
+      if (step + 1 < nsteps) body(step + 1, R0);
+    }
+  }
+
+  if (s == p.NS - 1 && p.ht)
+    store_state_f32<NTV, NTK>(acc, p.ht + ((long)sg.seq * H + hh) * KV, K, V, vt0, kt0, lane);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+bool head_supported(int dtype, int C, int K, int V, bool g_is_cumsum) {
+  return dtype == DT_BF16 && C == HC && K >= 8 && V >= 8 && K <= 128 && V <= 128 &&
+         K % 8 == 0 && V % 8 == 0 && !g_is_cumsum;
+}
+
+void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL) {
+  NS = 1;
+  SL = 0;
+  if (varlen || N <= 0 || H <= 0) return;
+  const int nt = (T + C - 1) / C;
+  const long want = (512 + (long)N * H - 1) / ((long)N * H);   // about two blocks per CU
+  long ns = want < nt / 8 ? want : nt / 8;                     // segments of >= 8 chunks
+  if (ns <= 1) return;
+  SL = (int)((nt + ns - 1) / ns);
+  NS = (nt + SL - 1) / SL;
+  if (NS <= 1) {
+    NS = 1;
+    SL = 0;
+  }
+}
+
+long head_seg_ws_bytes(int N, int NS, int H, int K, int V) {
+  if (NS <= 1) return 0;
+  const long st = (long)N * NS * H * K * V * 4;
+  const long gm = (long)N * NS * H * K * 4;
+  return st + (gm + 255) / 256 * 256;
+}
+
+template <int KP, int VP, bool REV>
+static hipError_t launch_head_scan(const HeadScanArgs& p, hipStream_t st, long blocks) {
+  hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV>), dim3((unsigned)blocks), dim3(HNT), 0, st,
+                     p);
+  return hipGetLastError();
+}
+
+template <bool REV>
+static hipError_t head_scan_kp(const HeadScanArgs& p, hipStream_t st, long blocks) {
+  const bool k64 = p.K <= 64, v64 = p.V <= 64;
+  if (k64 && v64) return launch_head_scan<64, 64, REV>(p, st, blocks);
+  if (k64) return launch_head_scan<64, 128, REV>(p, st, blocks);
+  if (v64) return launch_head_scan<128, 64, REV>(p, st, blocks);
+  return launch_head_scan<128, 128, REV>(p, st, blocks);
+}
+
+static hipError_t head_scan_launch(HeadScanArgs p, bool reverse, hipStream_t st, int pass,
+                                   int s_begin, int ns_launch) {
+  p.pass = pass;
+  p.s_begin = s_begin;
+  p.ns_launch = ns_launch;
+  if (pass == 1) {   // local states only
+    p.s_all = nullptr;
+    p.s_final = nullptr;
+  }
+  const long blocks = (long)p.si.N * ns_launch * p.H;
+  if (blocks == 0) return hipSuccess;
+  return reverse ? head_scan_kp<true>(p, st, blocks) : head_scan_kp<false>(p, st, blocks);
+}
+
+static hipError_t head_combine(const HeadScanArgs& p, bool reverse, hipStream_t st) {
+  const long total = (long)p.si.N * p.H * p.K * p.V;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  if (reverse)
+    hipLaunchKernelGGL((head_combine_kernel<true>), dim3(blocks), dim3(256), 0, st,
+                       p.seg_state, p.seg_gam, p.si.N, p.NS, p.H, p.K, p.V);
+  else
+    hipLaunchKernelGGL((head_combine_kernel<false>), dim3(blocks), dim3(256), 0, st,
+                       p.seg_state, p.seg_gam, p.si.N, p.NS, p.H, p.K, p.V);
+  return hipGetLastError();
+}
+
+// Segment passes 1 and 2 (no-op when NS == 1).
+static hipError_t head_prepare_segments(const HeadScanArgs& p, bool reverse, hipStream_t st) {
+  if (p.NS <= 1) return hipSuccess;
+  // pass 1 skips the last segment in flow order (its local state is never needed)
+  hipError_t e = head_scan_launch(p, reverse, st, 1, reverse ? 1 : 0, p.NS - 1);
+  if (e != hipSuccess) return e;
+  return head_combine(p, reverse, st);
+}
+
+hipError_t run_head_scan(const HeadScanArgs& p0, bool reverse, hipStream_t st) {
+  HeadScanArgs p = p0;
+  hipError_t e = head_prepare_segments(p, reverse, st);
+  if (e != hipSuccess) return e;
+  return head_scan_launch(p, reverse, st, 3, 0, p.NS);
+}
+
+template <int KP, int VP>
+static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
+  using Lay = HFLayout<KP, VP>;
+  const long blocks = (long)p.si.N * p.NS * p.H;
+  if (blocks == 0) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((head_fwd_kernel<KP, VP>), dim3((unsigned)blocks), dim3(HNT), Lay::bytes,
+                     st, p);
+  return hipGetLastError();
+}
+
+hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
+  if (p.NS > 1) {
+    HeadScanArgs s;
+    s.a = p.k;
+    s.b = p.v;
+    s.g = p.g;
+    s.s_init = p.h0;
+    s.s_all = nullptr;
+    s.s_final = nullptr;
+    s.seg_state = p.seg_state;
+    s.seg_gam = p.seg_gam;
+    s.NS = p.NS;
+    s.SL = p.SL;
+    s.scale = 1.f;
+    s.H = p.H;
+    s.K = p.K;
+    s.V = p.V;
+    s.si = p.si;
+    hipError_t e = head_prepare_segments(s, false, st);
+    if (e != hipSuccess) return e;
+  }
+  const bool k64 = p.K <= 64, v64 = p.V <= 64;
+  if (k64 && v64) return launch_head_fwd<64, 64>(p, st);
+  if (k64) return launch_head_fwd<64, 128>(p, st);
+  if (v64) return launch_head_fwd<128, 64>(p, st);
+  return launch_head_fwd<128, 128>(p, st);
+}
+
+}  // namespace tops

@@ -240,6 +240,11 @@ __device__ __forceinline__ void store_run(T* dst, const float (&x)[N]) {
   }
 }
 
+// x & m per 32-bit word (m = all ones or zero): a branch-free "valid ? x : 0".
+__device__ __forceinline__ uint4 mask16(uint4 x, uint32_t m) {
+  return make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
+}
+
 // 16 bytes of a global row starting at column col0, zero-filled past `nvalid` columns.
 // VEC: the row start and col0 are 16-byte aligned (only the tail check remains).
 template <typename T, bool VEC>

@@ -94,4 +94,41 @@ struct RecArgs {
 };
 hipError_t run_recurrent_fwd(const RecArgs& p, int dtype, int o_dtype, hipStream_t st);
 
+// Full-head kernels (chunk_head.hip): bf16, chunk 64, K and V <= 128 (multiples of 8,
+// 16-byte aligned rows), raw gates. Optional sequence segments (fixed-length sequences):
+// seg_state [N, NS, H, K, V] f32 and seg_gam [N, NS, H, K] f32 workspaces.
+bool head_supported(int dtype, int C, int K, int V, bool g_is_cumsum);
+void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL);
+long head_seg_ws_bytes(int N, int NS, int H, int K, int V);
+
+struct HeadScanArgs {
+  const void *a, *b, *g;  // forward: k, v ; reverse: q, do
+  const float* s_init;    // forward: h0 ; reverse: dht (nullable)
+  void* s_all;            // per-chunk states [NC, H, K, V] bf16 (nullable)
+  float* s_final;         // forward: ht ; reverse: dh0 (nullable)
+  float* seg_state;       // NS > 1 only
+  float* seg_gam;
+  int NS, SL;
+  int pass, s_begin, ns_launch;   // set by the launcher
+  float scale;            // reverse only
+  int H, K, V;
+  SeqInfo si;
+};
+hipError_t run_head_scan(const HeadScanArgs& p, bool reverse, hipStream_t st);
+
+struct HeadFwdArgs {
+  const void *q, *k, *v, *g;
+  const float* h0;        // nullable
+  void* o;
+  void* h_out;            // [NC, H, K, V] bf16 (nullable)
+  float* ht;              // nullable
+  float* seg_state;       // NS > 1 only
+  float* seg_gam;
+  int NS, SL;
+  float scale;
+  int H, K, V;
+  SeqInfo si;
+};
+hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st);
+
 }  // namespace tops

@@ -30,16 +30,17 @@ _F = ctypes.c_float
 _SIGS = {
     "tops_gla_chunk_local_cumsum": [_P, _P, _I64, _I64, _I64, _I64, _I, _I, _I, _F, _I, _P, _P,
                                     _I64, _I64, _I, _I, _P],
-    "tops_gla_chunk_fwd_h": [_P, _P, _P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P,
-                             _P, _I64, _I64, _I, _P],
-    "tops_gla_chunk_bwd_dh": [_P, _P, _I, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I,
-                              _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_fwd_h": [_P, _P, _P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                             _I, _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_bwd_dh": [_P, _P, _I, _P, _P, _P, _P, _P, _I64, _F, _I64, _I64, _I64, _I64,
+                              _I64, _I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_chunk_fwd_o": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64,
                              _I64, _I, _P, _P, _I64, _I64, _I, _P],
-    "tops_gla_chunk_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I,
-                           _P, _P, _I64, _I64, _I, _P],
-    "tops_gla_chunk_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64,
-                           _I64, _I64, _I64, _I64, _I, _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_ws_bytes": [_I64, _I64, _I64, _I64, _I64, _I, _I, _I],
+    "tops_gla_chunk_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _F, _I64, _I64, _I64, _I64,
+                           _I64, _I, _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                           _F, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_chunk_bwd_dqkg": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64,
                                 _I64, _I64, _I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_chunk_bwd_dv": [_P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I, _P,
@@ -47,6 +48,9 @@ _SIGS = {
     "tops_gla_fused_recurrent_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _F, _I, _I64, _I64, _I64,
                                      _I64, _I64, _P, _I64, _I, _I, _P],
 }
+# entry points that do not return a status code
+_RESTYPE = {"tops_gla_chunk_ws_bytes": ctypes.c_int64}
+
 EXPORTED = ["tops_gla_last_error", "tops_gla_version"] + list(_SIGS)
 
 _lib = None
@@ -72,7 +76,7 @@ def load():
             for name, args in _SIGS.items():
                 fn = getattr(lib, name)
                 fn.argtypes = args
-                fn.restype = ctypes.c_int
+                fn.restype = _RESTYPE.get(name, ctypes.c_int)
             _lib = lib
     return _lib
 
@@ -88,6 +92,15 @@ def call(name, *args):
         if rc == 2:
             raise NotImplementedError(f"{name}: {msg}")
         raise RuntimeError(f"{name}: {msg}")
+
+
+def seg_workspace(B, T, H, K, V, chunk, varlen, dtype, device):
+    """Sequence-segment workspace of tops_gla_chunk_fwd / _bwd: (tensor or None, bytes)."""
+    n = int(load().tops_gla_chunk_ws_bytes(B, T, H, K, V, chunk, int(bool(varlen)),
+                                           dtype_code(dtype)))
+    if n <= 0:
+        return None, 0
+    return torch.empty(n, dtype=torch.uint8, device=device), n
 
 
 def ptr(t):

@@ -114,8 +114,10 @@ class _ChunkGLAFunction(torch.autograd.Function):
         ht = (torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev)
               if output_final_state else None)
         h_ws = torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev)
+        ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list is not None, q.dtype, dev)
         call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(o), ptr(ht),
-             ptr(h_ws), scale, B, T, H, K, V, chunk, *seq.args(), dt, stream_of(dev))
+             ptr(h_ws), ptr(ws), nws, scale, B, T, H, K, V, chunk, *seq.args(), dt,
+             stream_of(dev))
         ctx.save_for_backward(q, k, v, g, h0, h_ws)
         ctx.meta = (scale, cu_list, chunk)
         if ht is None:
@@ -136,9 +138,11 @@ class _ChunkGLAFunction(torch.autograd.Function):
         need_dh0 = h0 is not None and ctx.needs_input_grad[4]
         dh0 = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if need_dh0 else None
         dh_ws = torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev)
+        ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list is not None, q.dtype, dev)
         call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(h_ws), ptr(do),
-             ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None, ptr(dh_ws), scale, B,
-             T, H, K, V, chunk, *seq.args(), dtype_code(q.dtype), stream_of(dev))
+             ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None, ptr(dh_ws), ptr(ws),
+             nws, scale, B, T, H, K, V, chunk, *seq.args(), dtype_code(q.dtype),
+             stream_of(dev))
         return dq, dk, dv, dg, dh0, None, None, None, None
 
 
@@ -249,7 +253,8 @@ def chunk_fwd_h(k, v, gk=None, h0=None, output_final_state=False, cu_seqlens_cpu
     h = torch.empty(B, seq.NC // B, H, K, V, dtype=cdt, device=dev)
     ht = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev)
     call("tops_gla_chunk_fwd_h", ptr(kk), ptr(vv), ptr(gg), 1, ptr(_c(h0, torch.float32)),
-         ptr(h), ptr(ht), B, T, H, K, V, C, *seq.args(), dtype_code(cdt), stream_of(dev))
+         ptr(h), ptr(ht), None, 0, B, T, H, K, V, C, *seq.args(), dtype_code(cdt),
+         stream_of(dev))
     if not output_final_state:
         ht.zero_()
     return h.to(k.dtype), ht
@@ -373,9 +378,11 @@ def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_fi
     h = torch.empty(B, seq.NC // B, H, K, V, dtype=cdt, device=dev)
     ht = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if output_final_state \
         else None
+    ws, nws = (None, 0) if g_is_cumsum else _lib.seg_workspace(B, Tp, H, K, V, C,
+                                                                cu_list is not None, cdt, dev)
     call("tops_gla_chunk_fwd_h", ptr(kp), ptr(vp), ptr(g_in), g_is_cumsum,
-         ptr(_c(initial_state, torch.float32)), ptr(h), ptr(ht), B, Tp, H, K, V, C, *seq.args(),
-         dt, st)
+         ptr(_c(initial_state, torch.float32)), ptr(h), ptr(ht), ptr(ws), nws, B, Tp, H, K, V,
+         C, *seq.args(), dt, st)
     A = torch.empty(B, Tp, H, C, dtype=torch.float32, device=dev)
     o = torch.empty(B, Tp, H, V, dtype=cdt, device=dev)
     call("tops_gla_chunk_fwd_o", ptr(qp), ptr(kp), ptr(vp), ptr(g_in), g_is_cumsum, ptr(h),
@@ -417,10 +424,11 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
     dh0 = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if want_dh0 else None
     h_ws = None if h is not None else torch.empty(seq.NC, H, K, V, dtype=cdt, device=dev)
     dh_ws = torch.empty(seq.NC, H, K, V, dtype=cdt, device=dev)
+    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list is not None, cdt, dev)
     call("tops_gla_chunk_bwd", ptr(qq), ptr(kk), ptr(vv), ptr(gg),
          ptr(_c(initial_state, torch.float32)), ptr(h), ptr(dd), ptr(_c(dht, torch.float32)),
-         ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), ptr(h_ws), ptr(dh_ws), float(scale), B,
-         T, H, K, V, C, *seq.args(), dtype_code(cdt), stream_of(dev))
+         ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), ptr(h_ws), ptr(dh_ws), ptr(ws), nws,
+         float(scale), B, T, H, K, V, C, *seq.args(), dtype_code(cdt), stream_of(dev))
     dq, dk, dv, dg = dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype)
     if g_orig is None and g_gamma is not None:
         gg_shape = tuple(g_gamma.shape)

@@ -24,7 +24,7 @@ def _declared():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     out = {}
-    for m in re.finditer(r"\b(?:int|const char\*)\s+(tops_gla_\w+)\s*\(([^)]*)\)\s*;", src):
+    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(tops_gla_\w+)\s*\(([^)]*)\)\s*;", src):
         params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
         out[m.group(1)] = len(params)
     return out
@@ -32,7 +32,7 @@ def _declared():
 
 def test_header_lists_entry_points():
     decl = _declared()
-    assert len(decl) == 11, decl
+    assert len(decl) == 12, decl
     assert set(decl) == set(_lib.EXPORTED)
 
 
@@ -56,32 +56,33 @@ NULL = None
 
 
 def test_chunk_fwd_rejects_bad_dtype():
-    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1.0,
-                  1, 64, 1, 64, 64, 64, NULL, NULL, 1, 1, 7, NULL)
+    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL,
+                  0, 1.0, 1, 64, 1, 64, 64, 64, NULL, NULL, 1, 1, 7, NULL)
     assert rc == 1 and "dtype" in msg
 
 
 def test_chunk_fwd_rejects_unsupported_chunk():
-    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1.0,
-                  1, 64, 1, 64, 64, 48, NULL, NULL, 1, 2, 1, NULL)
+    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL,
+                  0, 1.0, 1, 64, 1, 64, 64, 48, NULL, NULL, 1, 2, 1, NULL)
     assert rc == 2 and "chunk_size" in msg
 
 
 def test_chunk_fwd_rejects_wrong_chunk_count():
-    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1.0,
-                  2, 100, 1, 64, 64, 64, NULL, NULL, 2, 3, 1, NULL)
+    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL,
+                  0, 1.0, 2, 100, 1, 64, 64, 64, NULL, NULL, 2, 3, 1, NULL)
     assert rc == 1 and "NC" in msg
 
 
 def test_chunk_fwd_rejects_null_buffers():
-    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1.0,
-                  1, 64, 1, 64, 64, 64, NULL, NULL, 1, 1, 1, NULL)
+    rc, msg = _rc("tops_gla_chunk_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL,
+                  0, 1.0, 1, 64, 1, 64, 64, 64, NULL, NULL, 1, 1, 1, NULL)
     assert rc == 1 and "NULL" in msg
 
 
 def test_varlen_requires_batch_one():
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    rc, msg = _rc("tops_gla_chunk_fwd_h", fake, fake, fake, 0, NULL, NULL, NULL, 2, 64, 1, 64,
+    rc, msg = _rc("tops_gla_chunk_fwd_h", fake, fake, fake, 0, NULL, NULL, NULL, NULL, 0, 2, 64,
+                  1, 64,
                   64, 64, fake, fake, 2, 2, 1, NULL)
     assert rc == 1 and "B == 1" in msg
 
@@ -136,3 +137,18 @@ def test_seq_layout_chunk_offsets():
     assert s.chunk_cu.tolist() == [0, 1, 3, 4]
     f = _lib.SeqLayout(3, 37, 16, None, "cpu")
     assert (f.N, f.NC) == (3, 9) and f.cu is None
+
+
+def test_segment_workspace_query():
+    """Host-only: the segment workspace covers [N, NS, H, K, V] f32 states + decays."""
+    lib = _lib.load()
+    q = lib.tops_gla_chunk_ws_bytes
+    # B4 T8192 H16 K=V=128 chunk 64 bf16: 128 chunks per sequence, 8 segments of 16
+    st = 4 * 8 * 16 * 128 * 128 * 4
+    gm = 4 * 8 * 16 * 128 * 4
+    assert q(4, 8192, 16, 128, 128, 64, 0, 1) == st + (gm + 255) // 256 * 256
+    assert q(4, 8192, 16, 128, 128, 64, 1, 1) == 0      # varlen: unsegmented
+    assert q(4, 8192, 16, 128, 128, 64, 0, 0) == 0      # float32: other kernels
+    assert q(4, 8192, 16, 128, 128, 32, 0, 1) == 0      # chunk 32: other kernels
+    assert q(1, 256, 2, 64, 64, 64, 0, 1) == 0          # 4 chunks: too short to split
+    assert q(4, 8192, 16, 256, 128, 64, 0, 1) == 0      # K > 128

@@ -50,6 +50,11 @@ FWD_CASES = [
     dict(B=1, T=256, H=1, K=192, V=96, seed=6, C=32),
     # C1: fp32, B=1 T=256 H=2 K=V=64, chunk 64, g/16
     dict(B=1, T=256, H=2, K=64, V=64, seed=1, C=64, gate_div=16.0),
+    # long bf16 chunk-64 sequences: the full-head kernels split them into segments
+    # (2048 tokens -> 4 segments of 8 chunks; 2000 -> partial last chunk; 1536 -> 3 segments)
+    dict(B=2, T=2048, H=2, K=128, V=128, seed=801, C=64, h0=True, gate_div=16.0),
+    dict(B=1, T=2000, H=3, K=64, V=128, seed=802, C=64, h0=True),
+    dict(B=2, T=1536, H=1, K=96, V=40, seed=803, C=64, h0=True, gate_div=4.0),
 ]
 
 
@@ -131,6 +136,9 @@ BWD_CASES = [
     dict(B=1, T=50, H=2, K=16, V=32, seed=602, cu=[0, 13, 37, 50]),
     dict(B=1, T=256, H=2, K=256, V=512, seed=8, C=64, h0=True, dht=True),
     dict(B=1, T=192, H=2, K=128, V=128, seed=4, C=64, h0=True, dht=True, gate_div=16.0),
+    dict(B=2, T=2048, H=2, K=128, V=128, seed=811, C=64, h0=True, dht=True, gate_div=16.0),
+    dict(B=1, T=2000, H=3, K=64, V=128, seed=812, C=64, h0=True, dht=True),
+    dict(B=2, T=1536, H=1, K=96, V=40, seed=813, C=64, dht=True, gate_div=4.0),
 ]
 
 
@@ -314,3 +322,38 @@ def test_north_star_shape_slices():
         for name, x, r in zip(["dq", "dk", "dv", "dg"], (tq, tk, tv, tg), ref):
             check(name, sl(x.grad), r, "bf16")
         check("dh0", to_np(th0.grad[b:b + 1, h:h + 1]), ref[4], "bf16")
+
+
+def test_segmented_scans_match_sequential():
+    """The segment-parallel scans (local states, combine, all segments at once) give the
+    sequential scan's results: tops_gla_chunk_fwd / _bwd with and without the workspace."""
+    from tops import _lib
+    from tops._lib import SeqLayout, call, ptr, stream_of
+
+    B, T, H, K, V, C = 2, 4096, 4, 128, 128, 64
+    q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, 821, gate_div=16.0, h0=True, dht=True,
+                                          dtype="bf16")
+    d = lambda x: to_dev(x, "bf16")  # noqa: E731
+    q, k, v, g, do = (d(x) for x in (q, k, v, g, do))
+    h0, dht = to_dev(s0, "state"), to_dev(dht, "state")
+    dev = q.device
+    seq = SeqLayout(B, T, C, None, dev)
+    st = stream_of(dev)
+    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, False, torch.bfloat16, dev)
+    assert nws > 0, "this shape is expected to use sequence segments"
+    outs = []
+    for w, n in ((None, 0), (ws, nws)):
+        o, h = torch.empty_like(v), torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev)
+        ht = torch.empty_like(h0)
+        call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(o), ptr(ht),
+             ptr(h), ptr(w), n, K ** -0.5, B, T, H, K, V, C, *seq.args(), _lib.BF16, st)
+        dq, dk, dv, dg = (torch.empty_like(x) for x in (q, k, v, g))
+        dh0, dh = torch.empty_like(h0), torch.empty_like(h)
+        call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(h), ptr(do),
+             ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None, ptr(dh), ptr(w), n,
+             K ** -0.5, B, T, H, K, V, C, *seq.args(), _lib.BF16, st)
+        torch.cuda.synchronize()
+        outs.append([o, ht, h, dq, dk, dv, dg, dh0, dh])
+    names = ["o", "ht", "h", "dq", "dk", "dv", "dg", "dh0", "dh"]
+    for name, a, b in zip(names, *outs):
+        check(name, to_np(b), to_np(a).astype(np.float64), "bf16")
