@@ -95,19 +95,16 @@ def _kernel_profile(x, reps=10):
     tok = B * T * H
     hbytes = seq.NC * H * K * V * BF
     kernels = {
+        # forward: segment local states + combine + fused state scan / output
         "chunk_fwd": (lambda: call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g),
                                    ptr(h0), ptr(o), ptr(ht), ptr(h), ptr(ws), nws, sc, *lay),
                       tok * (3 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes),
-        "state_scan_bwd": (lambda: call("tops_gla_chunk_bwd_dh", ptr(q), ptr(g), 0, ptr(do),
-                                        ptr(dht), ptr(dh), ptr(dh0), ptr(ws), nws, sc, *lay),
-                           tok * (2 * K + V) * BF + STATE_BYTES * 2 + hbytes),
-        "chunk_bwd_dqkg": (lambda: call("tops_gla_chunk_bwd_dqkg", ptr(q), ptr(k), ptr(v),
-                                        ptr(g), ptr(h), ptr(do), ptr(dh), ptr(dq), ptr(dk),
-                                        ptr(dg), sc, *lay),
-                           tok * (6 * K + 2 * V) * BF + 2 * hbytes),
-        "chunk_bwd_dv": (lambda: call("tops_gla_chunk_bwd_dv", ptr(q), ptr(k), ptr(g), ptr(do),
-                                      ptr(dh), ptr(dv), sc, *lay),
-                         tok * (3 * K + 2 * V) * BF + hbytes),
+        # backward: segment local dh + combine + fused reverse scan / gradients
+        "chunk_bwd": (lambda: call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g),
+                                   ptr(h0), ptr(h), ptr(do), ptr(dht), ptr(dq), ptr(dk),
+                                   ptr(dv), ptr(dg), ptr(dh0), None, ptr(dh), ptr(ws), nws,
+                                   sc, *lay),
+                      tok * (6 * K + 3 * V) * BF + STATE_BYTES * 2 + hbytes),
     }
     res = {}
     cur = torch.cuda.current_stream(dev)

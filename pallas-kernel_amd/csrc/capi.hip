@@ -465,8 +465,30 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     h = h_ws;
   }
   if (head) {
-    rc = hip_status(head_scan(true, q, dout, dht, dh_ws, dh0, scale), "chunk_bwd (dh scan)");
-    if (rc) return rc;
+    // fused: reverse dh scan and per-chunk gradients in one pass (dh_ws is not needed)
+    tops::HeadBwdArgs b = {};
+    b.q = q;
+    b.k = k;
+    b.v = v;
+    b.g = g;
+    b.dout = dout;
+    b.h = h;
+    b.dht = dht;
+    b.dq = dq;
+    b.dk = dk;
+    b.dv = dv;
+    b.dg = dg;
+    b.dh0 = dh0;
+    b.seg_state = seg_st;
+    b.seg_gam = seg_gm;
+    b.NS = NS;
+    b.SL = SL;
+    b.scale = scale;
+    b.H = (int)H;
+    b.K = (int)K;
+    b.V = (int)V;
+    b.si = si;
+    return hip_status(tops::run_head_bwd(b, st), "chunk_bwd (full-head)");
   } else {
     tops::ScanArgs d;
     d.a = q;

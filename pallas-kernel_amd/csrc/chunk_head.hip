@@ -39,10 +39,10 @@ constexpr int HNT = 512;  // threads per block
 constexpr int HNW = HNT / 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int KP>
+template <int KP, int NT = HNT>
 struct HMap {
   static constexpr int NCG = KP / 8;     // 8-column groups
-  static constexpr int NRS = HNT / NCG;  // row segments
+  static constexpr int NRS = NT / NCG;   // row segments
   static constexpr int RPT = HC / NRS;   // rows per thread
   static_assert(RPT >= 1 && NRS * RPT == HC, "thread mapping");
 };
@@ -77,17 +77,30 @@ __device__ __forceinline__ void ld_f8(const float* p, float (&x)[8]) {
   x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
 
-// RPT rows x 16 bytes starting at (row0, col0) of a row-major tile with row stride rs.
-// Unconditional: rows are clamped to len-1 and the column to w-8 (w % 8 == 0, w >= 8);
-// the caller masks what it consumes.
+// Global accesses are a uniform base pointer (scalar registers) plus a 32-bit per-lane
+// byte offset, which the compiler emits as the scalar-base form of the global loads and
+// stores: one VGPR per address instead of a 64-bit pair.
+__device__ __forceinline__ uint4 ld16(const void* base, uint32_t off) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + off);
+}
+__device__ __forceinline__ void st16(void* base, uint32_t off, const uint4& x) {
+  *reinterpret_cast<uint4*>(reinterpret_cast<char*>(base) + off) = x;
+}
+__device__ __forceinline__ void st8(void* base, uint32_t off, const uint2& x) {
+  *reinterpret_cast<uint2*>(reinterpret_cast<char*>(base) + off) = x;
+}
+
+// RPT rows x 16 bytes starting at (row0, col0) of a row-major bf16 tile at `base` with
+// row stride rs elements. Unconditional: rows are clamped to len-1 and the column to w-8
+// (w % 8 == 0, w >= 8); the caller masks what it consumes.
 template <int RPT>
-__device__ __forceinline__ void hload(uint4 (&r)[RPT], const bf16* __restrict__ base, long rs,
+__device__ __forceinline__ void hload(uint4 (&r)[RPT], const bf16* __restrict__ base, uint32_t rs,
                                       int row0, int len, int col0, int w) {
-  const int c = min(col0, w - 8);
+  const uint32_t c = (uint32_t)min(col0, w - 8);
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
-    const int row = min(row0 + j, len - 1);
-    r[j] = *reinterpret_cast<const uint4*>(base + (long)row * rs + c);
+    const uint32_t row = (uint32_t)min(row0 + j, len - 1);
+    r[j] = ld16(base, (row * rs + c) * 2u);
   }
 }
 
@@ -108,13 +121,13 @@ __device__ __forceinline__ Seg seg_of(const SeqInfo& si, int seq, int s, int NS,
 
 // Base-2 chunk-local cumsum of an [HC x KP] gate tile held as RPT rows x 8 columns per
 // thread (raw, already masked). Out: gt = g~ log2 e, gam = its last row, first = its row 0.
-// sTot [HNW][KP], sFirst [KP]. One barrier.
-template <int KP>
-__device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP>::RPT],
-                                            float (&gt)[HMap<KP>::RPT][8], float (&gam)[8],
+// sTot [NT/64][KP], sFirst [KP]. One barrier.
+template <int KP, int NT = HNT>
+__device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP, NT>::RPT],
+                                            float (&gt)[HMap<KP, NT>::RPT][8], float (&gam)[8],
                                             float (&first)[8], float* sTot, float* sFirst,
                                             int cg, int rs, int lane, int w) {
-  using M = HMap<KP>;
+  using M = HMap<KP, NT>;
 #pragma unroll
   for (int j = 0; j < M::RPT; ++j) {
     unpack8(graw[j], gt[j]);
@@ -142,7 +155,7 @@ __device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP>::RPT],
     gam[e] = 0.f;
   }
 #pragma unroll
-  for (int ww = 0; ww < HNW; ++ww) {
+  for (int ww = 0; ww < NT / 64; ++ww) {
     float t[8];
     ld_f8(sTot + ww * KP + cg * 8, t);
 #pragma unroll
@@ -177,7 +190,8 @@ __device__ __forceinline__ void load_state(f32x4 (&acc)[NTV][NTK], const float* 
       acc[i][j] = zero4();
       const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
       if (init && kk < K && vv < V) {
-        const float4 x = *reinterpret_cast<const float4*>(init + (long)kk * V + vv);
+        const float4 x = *reinterpret_cast<const float4*>(
+            reinterpret_cast<const char*>(init) + (uint32_t)(kk * V + vv) * 4u);
         acc[i][j][0] = via_vgpr(x.x);
         acc[i][j][1] = via_vgpr(x.y);
         acc[i][j][2] = via_vgpr(x.z);
@@ -195,7 +209,7 @@ __device__ __forceinline__ void store_state_f32(const f32x4 (&acc)[NTV][NTK], fl
     for (int j = 0; j < NTK; ++j) {
       const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
       if (kk < K && vv < V)
-        *reinterpret_cast<float4*>(dst + (long)kk * V + vv) =
+        *reinterpret_cast<float4*>(reinterpret_cast<char*>(dst) + (uint32_t)(kk * V + vv) * 4u) =
             make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
     }
 }
@@ -209,9 +223,9 @@ __device__ __forceinline__ void store_state_bf16(const f32x4 (&acc)[NTV][NTK], b
     for (int j = 0; j < NTK; ++j) {
       const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
       if (kk < K && vv < V)
-        *reinterpret_cast<uint2*>(dst + (long)kk * V + vv) =
+        st8(dst, (uint32_t)(kk * V + vv) * 2u,
             make_uint2(pack2_bf16(acc[i][j][0], acc[i][j][1]),
-                       pack2_bf16(acc[i][j][2], acc[i][j][3]));
+                       pack2_bf16(acc[i][j][2], acc[i][j][3])));
     }
 }
 
@@ -301,9 +315,9 @@ __global__ __launch_bounds__(HNT) void head_scan_kernel(HeadScanArgs p) {
     const int t0 = sg.bos + ci * HC;
     const int len = min(HC, sg.eos - t0);
     const long oa = (long)t0 * rsK + (long)hh * K;
-    hload<RPT>(R.a, a + oa, rsK, rs * RPT, len, cg * 8, K);
-    hload<RPT>(R.g, g + oa, rsK, rs * RPT, len, cg * 8, K);
-    hload<VRPT>(R.b, b + (long)t0 * rsV + (long)hh * V, rsV, vrs * VRPT, len, vg * 8, V);
+    hload<RPT>(R.a, a + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    hload<VRPT>(R.b, b + (long)t0 * rsV + (long)hh * V, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
   };
 
   float gsum[8];   // pass 1: total base-2 decay of the segment
@@ -500,10 +514,10 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     const int t0 = sg.bos + (sg.cb + st) * HC;
     const int len = min(HC, sg.eos - t0);
     const long oa = (long)t0 * rsK + (long)hh * K;
-    hload<RPT>(R.q, q + oa, rsK, rs * RPT, len, cg * 8, K);
-    hload<RPT>(R.k, k + oa, rsK, rs * RPT, len, cg * 8, K);
-    hload<RPT>(R.g, g + oa, rsK, rs * RPT, len, cg * 8, K);
-    hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V, rsV, vrs * VRPT, len, vg * 8, V);
+    hload<RPT>(R.q, q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    hload<RPT>(R.k, k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
   };
 
   auto body = [&](int step, Regs& R) {
@@ -604,8 +618,8 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
         const int row = it * 16 + (lane & 15);
         const int vv = vt * 16 + 4 * (lane >> 4);
         if (row < len && vv < V)
-          *reinterpret_cast<uint2*>(o + (long)(t0 + row) * rsV + (long)hh * V + vv) =
-              make_uint2(pack2_bf16(ot[0], ot[1]), pack2_bf16(ot[2], ot[3]));
+          st8(o + (long)t0 * rsV + (long)hh * V, ((uint32_t)row * (uint32_t)rsV + vv) * 2u,
+              make_uint2(pack2_bf16(ot[0], ot[1]), pack2_bf16(ot[2], ot[3])));
       }
     }
     state_update<NTV, NTK>(acc, sV, PVP, sKd, PKP, sGam, vt0, kt0, lane);
@@ -625,6 +639,459 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 
   if (s == p.NS - 1 && p.ht)
     store_state_f32<NTV, NTK>(acc, p.ht + ((long)sg.seq * H + hh) * KV, K, V, vt0, kt0, lane);
+}
+
+
+// ---------------------------------------------------------------------------
+// Fused backward: one block per (sequence, segment, head) walks the segment's chunks in
+// reverse with the state gradient dh (state leaving the chunk) in MFMA accumulators.
+// Reference: chunk_gla_bwd_with_pl, tops/ops/gla/chunk.py:1019-1064 (dh scan
+// chunk_h.py:495-591, fused gradients chunk.py:1423-1479). Per chunk, base-2 gates,
+// r = (g~_first + gamma) / 2 per column, fr = scale 2^r, fe = 2^{gamma-r}:
+//   qg = q 2^{g~-r}, kg = k 2^{r-g~}, kd = k 2^{gamma-g~}
+//   A = scale tril(qg kg^T), dA = scale tril(do v^T)
+//   dv = A^T do + kd dh
+//   dq = 2^{g~-r} [dA kg + fr do h^T]
+//   dk = 2^{r-g~} [dA^T qg + fe v dh^T]
+//   dg = revcumsum_rows(q dq - k dk) + 2^gamma sum_v h dh + sum_v dh (kd^T v)
+//   dh <- 2^gamma dh + (scale q 2^{g~})^T do
+// (the last dg term is sum_rows k dk_inter, reduced from the dh accumulators.)
+// h (state entering the chunk) comes from the forward's per-chunk states; its MFMA
+// fragments are read straight from HBM (16 bytes per lane).
+// Waves: dq/dk own KTW k tiles x RT row tiles, dv^T VTW v tiles x JT row tiles, dh as in
+// the scans. A chunk's inputs are fetched when the chunk starts: this kernel has no
+// registers left to hold the next chunk in flight, and spilling them costs far more than
+// the exposed load latency (the block's 8 waves and the other blocks keep HBM busy).
+// ---------------------------------------------------------------------------
+template <int KP, int VP, int NW>
+struct HBLayout {
+  static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP),
+                       PA = pitch_of<bf16>(HC);
+  static constexpr int PX = KP + 4;                // fp32 exchange pitch
+  // small fp32 arrays first: the exchange aliases the tiles only
+  static constexpr int tot = 0;                    // [NW][KP] cumsum wave totals
+  static constexpr int suf = tot + NW * KP * 4;    // [NW][KP] dg suffix wave totals
+  static constexpr int first = suf + NW * KP * 4;
+  static constexpr int eg = first + KP * 4;        // 2^gamma
+  static constexpr int fr = eg + KP * 4;           // scale 2^r
+  static constexpr int fe = fr + KP * 4;           // 2^{gamma-r}
+  static constexpr int hd = fe + KP * 4;           // sum_v h dh
+  static constexpr int dkc = hd + KP * 4;          // [2][KP] sum_v dh (kd^T v), per v half
+  static constexpr int qg = dkc + 2 * KP * 4;
+  static constexpr int kg = qg + HC * PKP * 2;
+  static constexpr int kd = kg + HC * PKP * 2;
+  static constexpr int v = kd + HC * PKP * 2;
+  static constexpr int dout = v + HC * PVP * 2;
+  static constexpr int dh = dout + HC * PVP * 2;   // dh [k][v] bf16
+  static constexpr int a = dh + KP * PVP * 2;
+  static constexpr int da = a + HC * PA * 2;
+  static constexpr int end_tiles = da + HC * PA * 2;
+  // exchange [HC][PX] x 2 from kd on (qg, kg stay intact for the epilogue); it may reach
+  // A / dA, which are therefore rewritten in full (zero upper tiles) every chunk
+  static constexpr int xq = kd;
+  static constexpr int xk = xq + HC * PX * 4;
+  static constexpr int end_x = xk + HC * PX * 4;
+  static constexpr int bytes = end_tiles > end_x ? end_tiles : end_x;
+};
+
+template <int KP, int VP, int NT>
+__global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
+  constexpr int NW = NT / 64;
+  using M = HMap<KP, NT>;
+  using MV = HMap<VP, NT>;
+  using Lay = HBLayout<KP, VP, NW>;
+  constexpr int RPT = M::RPT, VRPT = MV::RPT;
+  constexpr int PKP = Lay::PKP, PVP = Lay::PVP, PA = Lay::PA, PX = Lay::PX;
+  constexpr int NKT = KP / 16, NVT = VP / 16;
+  // dh tiles per wave: v by halves (w & 1), k split over the NW / 2 wave pairs
+  constexpr int NTV = VP / 32, NTK = NKT / (NW / 2);
+  // dq / dk: KTW k tiles x RT row tiles per wave; dv^T: VTW v tiles x JT row tiles
+  constexpr int KTW = NKT > NW ? NKT / NW : 1, NKG = NKT / KTW, RT = 4 * NKG / NW;
+  constexpr int VTW = NVT > NW ? NVT / NW : 1, NVG = NVT / VTW, JT = 4 * NVG / NW;
+  static_assert(NTK >= 1 && RT >= 1 && JT >= 1, "tile split");
+  constexpr int NHF = VP / 32;                      // h fragments per lane
+  static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* sTot = reinterpret_cast<float*>(smem + Lay::tot);
+  float* sSuf = reinterpret_cast<float*>(smem + Lay::suf);
+  float* sFirst = reinterpret_cast<float*>(smem + Lay::first);
+  float* sEg = reinterpret_cast<float*>(smem + Lay::eg);
+  float* sFr = reinterpret_cast<float*>(smem + Lay::fr);
+  float* sFe = reinterpret_cast<float*>(smem + Lay::fe);
+  float* sHd = reinterpret_cast<float*>(smem + Lay::hd);
+  float* sDkc = reinterpret_cast<float*>(smem + Lay::dkc);
+  bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
+  bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
+  bf16* sKd = reinterpret_cast<bf16*>(smem + Lay::kd);
+  bf16* sV = reinterpret_cast<bf16*>(smem + Lay::v);
+  bf16* sDo = reinterpret_cast<bf16*>(smem + Lay::dout);
+  bf16* sDh = reinterpret_cast<bf16*>(smem + Lay::dh);
+  bf16* sA = reinterpret_cast<bf16*>(smem + Lay::a);
+  bf16* sdA = reinterpret_cast<bf16*>(smem + Lay::da);
+  float* XQ = reinterpret_cast<float*>(smem + Lay::xq);
+  float* XK = reinterpret_cast<float*>(smem + Lay::xk);
+
+  const bf16* __restrict__ q = (const bf16*)p.q;
+  const bf16* __restrict__ k = (const bf16*)p.k;
+  const bf16* __restrict__ v = (const bf16*)p.v;
+  const bf16* __restrict__ g = (const bf16*)p.g;
+  const bf16* __restrict__ dout = (const bf16*)p.dout;
+  const bf16* __restrict__ hs = (const bf16*)p.h;
+  bf16* __restrict__ dq = (bf16*)p.dq;
+  bf16* __restrict__ dk = (bf16*)p.dk;
+  bf16* __restrict__ dv = (bf16*)p.dv;
+  bf16* __restrict__ dg = (bf16*)p.dg;
+  const int H = p.H, K = p.K, V = p.V;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int hh = L % H;
+  const int s = (L / H) % p.NS;
+  const Seg sg = seg_of(p.si, (L / H) / p.NS, s, p.NS, p.SL);
+  const int nsteps = sg.ce - sg.cb;
+  const long rsK = (long)H * K, rsV = (long)H * V;
+  const long KV = (long)K * V;
+
+  const int cg = tid % M::NCG, rs = tid / M::NCG;
+  const int vg = tid % MV::NCG, vrs = tid / MV::NCG;
+  const bool colA = cg * 8 < K, colB = vg * 8 < V;
+  const int kq0 = (w % NKG) * KTW, rt0 = (w / NKG) * RT;   // dq / dk tiles
+  const int vd0 = (w % NVG) * VTW, jt0 = (w / NVG) * JT;   // dv^T tiles
+
+  const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
+  f32x4 acc[NTV][NTK];   // dh[v][k]
+  {
+    const float* init = s == p.NS - 1
+                            ? (p.dht ? p.dht + ((long)sg.seq * H + hh) * KV : nullptr)
+                            : p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV;
+    load_state<NTV, NTK>(acc, init, K, V, vt0, kt0, lane);
+  }
+
+  uint4 Rq[RPT], Rk[RPT], Rg[RPT], Rv[VRPT], Rd[VRPT], Rh[KTW][NHF];
+  auto chunk_of = [&](int step, int& t0, int& len, int& ci) {
+    ci = sg.ce - 1 - min(step, nsteps - 1);
+    t0 = sg.bos + ci * HC;
+    len = min(HC, sg.eos - t0);
+  };
+  auto issue_main = [&](int step) {
+    int t0, len, ci;
+    chunk_of(step, t0, len, ci);
+    const long oa = (long)t0 * rsK + (long)hh * K, ov = (long)t0 * rsV + (long)hh * V;
+    hload<RPT>(Rq, q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    hload<RPT>(Rk, k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    hload<RPT>(Rg, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    hload<VRPT>(Rv, v + ov, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
+    hload<VRPT>(Rd, dout + ov, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
+  };
+  auto issue_h = [&](int step) {
+    int t0, len, ci;
+    chunk_of(step, t0, len, ci);
+    const bf16* hc = hs + ((long)(sg.c0 + ci) * H + hh) * KV;
+#pragma unroll
+    for (int t = 0; t < KTW; ++t) {
+      const uint32_t hrow = (uint32_t)min((kq0 + t) * 16 + (lane & 15), K - 1) * (uint32_t)V;
+#pragma unroll
+      for (int f = 0; f < NHF; ++f)
+        Rh[t][f] = ld16(hc, (hrow + (uint32_t)min(f * 32 + 8 * (lane >> 4), V - 8)) * 2u);
+    }
+  };
+
+
+  for (int step = 0; step < nsteps; ++step) {
+    int t0, len, ci;
+    chunk_of(step, t0, len, ci);
+    issue_main(step);
+    issue_h(step);
+
+    // ---- (1) dh to LDS, cumsum, gating ----
+#pragma unroll
+    for (int j = 0; j < NTK; ++j)
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) {
+        const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
+        *reinterpret_cast<uint2*>(sDh + kk * PVP + vv) =
+            make_uint2(pack2_bf16(acc[i][j][0], acc[i][j][1]),
+                       pack2_bf16(acc[i][j][2], acc[i][j][3]));
+      }
+    float dd[RPT][8];   // g~ - r (base 2)
+    {
+      uint4 gmk[RPT], qm[RPT], km[RPT];
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const uint32_t m = (colA && rs * RPT + j < len) ? ~0u : 0u;
+        gmk[j] = mask16(Rg[j], m);
+        qm[j] = mask16(Rq[j], m);
+        km[j] = mask16(Rk[j], m);
+      }
+      float gam[8], first[8];
+      head_cumsum<KP, NT>(gmk, dd, gam, first, sTot, sFirst, cg, rs, lane, w);
+      float r[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = 0.5f * (first[e] + gam[e]);
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const int row = rs * RPT + j;
+        float xq[8], xk[8], xd[8];
+        unpack8(qm[j], xq);
+        unpack8(km[j], xk);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xd[e] = xk[e] * exp2_hw(gam[e] - dd[j][e]);
+          dd[j][e] -= r[e];
+          xq[e] *= exp2_hw(dd[j][e]);
+          xk[e] *= exp2_hw(-dd[j][e]);
+        }
+        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pack8(xq);
+        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pack8(xk);
+        *reinterpret_cast<uint4*>(sKd + row * PKP + cg * 8) = pack8(xd);
+      }
+#pragma unroll
+      for (int j = 0; j < VRPT; ++j) {
+        const int row = vrs * VRPT + j;
+        const uint32_t m = (colB && row < len) ? ~0u : 0u;
+        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) = mask16(Rv[j], m);
+        *reinterpret_cast<uint4*>(sDo + row * PVP + vg * 8) = mask16(Rd[j], m);
+      }
+      if (rs == 0) {
+        float a8[8], b8[8], c8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          a8[e] = exp2_hw(gam[e]);
+          b8[e] = p.scale * exp2_hw(r[e]);
+          c8[e] = exp2_hw(gam[e] - r[e]);
+        }
+        st_f8(sEg + cg * 8, a8);
+        st_f8(sFr + cg * 8, b8);
+        st_f8(sFe + cg * 8, c8);
+      }
+    }
+    __syncthreads();
+
+    // ---- (2) A, dA (all 16 tiles each: the upper ones as zeros); products that need no
+    //      A / dA ----
+    for (int t = w; t < 32; t += NW) {
+      const int mi = (t >> 2) & 3, ni = t & 3;
+      f32x4 at = zero4();
+      if (ni <= mi) {
+        if (t < 16)
+          mma_tile<bf16>(at, sQg + mi * 16 * PKP, PKP, sKg + ni * 16 * PKP, PKP, KP, lane);
+        else
+          mma_tile<bf16>(at, sDo + mi * 16 * PVP, PVP, sV + ni * 16 * PVP, PVP, VP, lane);
+      }
+      bf16* dst = t < 16 ? sA : sdA;
+      const int jj = ni * 16 + (lane & 15);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int ii = mi * 16 + 4 * (lane >> 4) + rr;
+        dst[ii * PA + jj] = from_f32<bf16>(jj <= ii ? at[rr] * p.scale : 0.f);
+      }
+    }
+    // dq pre: fr do h^T (h fragments from HBM); dk pre: fe v dh^T
+    f32x4 aq[KTW][RT], ak[KTW][RT];
+    float hdp[KTW];
+#pragma unroll
+    for (int t = 0; t < KTW; ++t) {
+      const int hk = (kq0 + t) * 16 + (lane & 15);
+      hdp[t] = 0.f;
+#pragma unroll
+      for (int i = 0; i < RT; ++i) aq[t][i] = ak[t][i] = zero4();
+#pragma unroll
+      for (int f = 0; f < NHF; ++f) {
+        Frag<bf16> yh;
+        yh.d = mask16(Rh[t][f], (hk < K && f * 32 + 8 * (lane >> 4) < V) ? ~0u : 0u);
+        const Frag<bf16> ydh = ld_frag(sDh + hk * PVP + f * 32 + 8 * (lane >> 4));
+        {
+          float a8[8], b8[8];
+          unpack8(yh.d, a8);
+          unpack8(ydh.d, b8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) hdp[t] += a8[e] * b8[e];
+        }
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          const int ro = (rt0 + i) * 16 + (lane & 15);
+          mma(aq[t][i], ld_frag(sDo + ro * PVP + f * 32 + 8 * (lane >> 4)), yh);
+          mma(ak[t][i], ld_frag(sV + ro * PVP + f * 32 + 8 * (lane >> 4)), ydh);
+        }
+      }
+      hdp[t] += __shfl_xor(hdp[t], 16);
+      hdp[t] += __shfl_xor(hdp[t], 32);
+      const float fr = sFr[hk], fe = sFe[hk];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) {
+        aq[t][i] *= fr;
+        ak[t][i] *= fe;
+      }
+    }
+
+    // sum_v dh (kd^T v) per k, from the dh accumulators (before their update)
+    float dkc[NTK];
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) {
+      dkc[j] = 0.f;
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) {
+        f32x4 u = zero4();
+        mma_tile2<bf16, true, true>(u, sV + (vt0 + i) * 16, PVP, sKd + (kt0 + j) * 16, PKP, HC,
+                                    lane);
+        dkc[j] += acc[i][j][0] * u[0] + acc[i][j][1] * u[1] + acc[i][j][2] * u[2] +
+                  acc[i][j][3] * u[3];
+      }
+      dkc[j] += __shfl_xor(dkc[j], 16);
+      dkc[j] += __shfl_xor(dkc[j], 32);
+    }
+    __syncthreads();
+
+    // ---- (3) products with A / dA; dv out; dh update ----
+#pragma unroll
+    for (int t = 0; t < KTW; ++t)
+#pragma unroll
+      for (int i = 0; i < RT; ++i) {
+        const int ro = (rt0 + i) * 16, kq = kq0 + t;
+        // dq += dA kg (kg read transposed); dk += dA^T qg (both read transposed)
+        mma_tile2<bf16, false, true>(aq[t][i], sdA + ro * PA, PA, sKg + kq * 16, PKP, HC, lane);
+        mma_tile2<bf16, true, true>(ak[t][i], sdA + ro, PA, sQg + kq * 16, PKP, HC, lane);
+      }
+#pragma unroll
+    for (int u = 0; u < VTW; ++u)
+#pragma unroll
+      for (int i = 0; i < JT; ++i) {
+        const int jt = jt0 + i, vd = vd0 + u;
+        // dv^T = dh^T kd^T (dh read transposed) + do^T A (both read transposed)
+        f32x4 avt = zero4();
+        mma_tile2<bf16, true, false>(avt, sDh + vd * 16, PVP, sKd + jt * 16 * PKP, PKP, KP,
+                                     lane);
+        mma_tile2<bf16, true, true>(avt, sDo + vd * 16, PVP, sA + jt * 16, PA, HC, lane);
+        const int jj = jt * 16 + (lane & 15);
+        const int vv = vd * 16 + 4 * (lane >> 4);
+        if (jj < len && vv < V)
+          st8(dv + (long)t0 * rsV + (long)hh * V, ((uint32_t)jj * (uint32_t)rsV + vv) * 2u,
+              make_uint2(pack2_bf16(avt[0], avt[1]), pack2_bf16(avt[2], avt[3])));
+      }
+    // dh <- 2^gamma dh + (scale q 2^{g~})^T do = fr * (dh fe / scale + qg^T do)
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) {
+      const float d = sFe[(kt0 + j) * 16 + (lane & 15)] / p.scale;
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) acc[i][j] *= d;
+    }
+#pragma unroll
+    for (int kk = 0; kk < HC; kk += 32) {
+      Frag<bf16> x[NTV], y[NTK];
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) x[i] = ld_frag_t(sDo + kk * PVP + (vt0 + i) * 16, PVP, lane);
+#pragma unroll
+      for (int j = 0; j < NTK; ++j) y[j] = ld_frag_t(sQg + kk * PKP + (kt0 + j) * 16, PKP, lane);
+#pragma unroll
+      for (int i = 0; i < NTV; ++i)
+#pragma unroll
+        for (int j = 0; j < NTK; ++j) mma(acc[i][j], x[i], y[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) {
+      const float f = sFr[(kt0 + j) * 16 + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) acc[i][j] *= f;
+    }
+    __syncthreads();   // every tile read is done: the exchange aliases them
+
+    // ---- (4) exchange dq / dk pre-factors ----
+#pragma unroll
+    for (int t = 0; t < KTW; ++t) {
+      const int hk = (kq0 + t) * 16 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < RT; ++i) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int ro = (rt0 + i) * 16 + 4 * (lane >> 4) + rr;
+          XQ[ro * PX + hk] = aq[t][i][rr];
+          XK[ro * PX + hk] = ak[t][i][rr];
+        }
+      }
+      if (w < NKG && lane < 16) sHd[hk] = hdp[t];
+    }
+    if (lane < 16) {
+#pragma unroll
+      for (int j = 0; j < NTK; ++j) sDkc[(w & 1) * KP + (kt0 + j) * 16 + lane] = dkc[j];
+    }
+    __syncthreads();
+
+    // ---- (5) epilogue: dq, dk, dg rows ----
+    float pr[RPT][8];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int row = rs * RPT + j;
+      // q dq - k dk = qg xq - kg xk (xq, xk before their gate factors)
+      float xq[8], xk[8], q8[8], k8[8];
+      ld_f8(XQ + row * PX + cg * 8, xq);
+      ld_f8(XK + row * PX + cg * 8, xk);
+      unpack8(*reinterpret_cast<const uint4*>(sQg + row * PKP + cg * 8), q8);
+      unpack8(*reinterpret_cast<const uint4*>(sKg + row * PKP + cg * 8), k8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pr[j][e] = q8[e] * xq[e] - k8[e] * xk[e];
+        xq[e] *= exp2_hw(dd[j][e]);
+        xk[e] *= exp2_hw(-dd[j][e]);
+      }
+      if (row < len && colA) {
+        const long b0 = (long)t0 * rsK + (long)hh * K;
+        const uint32_t a = ((uint32_t)row * (uint32_t)rsK + cg * 8) * 2u;
+        st16(dq + b0, a, pack8(xq));
+        st16(dk + b0, a, pack8(xk));
+      }
+    }
+    // reverse cumsum over rows: in-thread, then across the wave's row segments
+#pragma unroll
+    for (int j = RPT - 2; j >= 0; --j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pr[j][e] += pr[j + 1][e];
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = pr[0][e];
+#pragma unroll
+    for (int d = M::NCG; d < 64; d <<= 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = __shfl_down(x[e], d);
+        if (lane + d < 64) x[e] += y;
+      }
+    }
+    if (lane < M::NCG) st_f8(sSuf + w * KP + cg * 8, x);
+    __syncthreads();
+    {
+      float off[8], t8[8], u8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) off[e] = x[e] - pr[0][e];   // later segments of the wave
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) {
+        ld_f8(sSuf + ww * KP + cg * 8, t8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (ww > w) off[e] += t8[e];
+      }
+      ld_f8(sEg + cg * 8, t8);
+      ld_f8(sHd + cg * 8, u8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) off[e] += t8[e] * u8[e];
+      ld_f8(sDkc + cg * 8, t8);
+      ld_f8(sDkc + KP + cg * 8, u8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) off[e] += t8[e] + u8[e];
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const int row = rs * RPT + j;
+        if (row < len && colA) {
+          float o8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o8[e] = pr[j][e] + off[e];
+          st16(dg + (long)t0 * rsK + (long)hh * K, ((uint32_t)row * (uint32_t)rsK + cg * 8) * 2u,
+               pack8(o8));
+        }
+      }
+    }
+  }
+
+  if (s == 0 && p.dh0)
+    store_state_f32<NTV, NTK>(acc, p.dh0 + ((long)sg.seq * H + hh) * KV, K, V, vt0, kt0, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -755,6 +1222,47 @@ hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   if (k64) return launch_head_fwd<64, 128>(p, st);
   if (v64) return launch_head_fwd<128, 64>(p, st);
   return launch_head_fwd<128, 128>(p, st);
+}
+
+// K = V = 128 runs with 16 waves (4 per SIMD, 128 registers each), smaller heads with 8.
+template <int KP, int VP>
+static hipError_t launch_head_bwd(const HeadBwdArgs& p, hipStream_t st) {
+  constexpr int NT = HNT;
+  using Lay = HBLayout<KP, VP, NT / 64>;
+  const long blocks = (long)p.si.N * p.NS * p.H;
+  if (blocks == 0) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute((const void*)head_bwd_kernel<KP, VP, NT>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((head_bwd_kernel<KP, VP, NT>), dim3((unsigned)blocks), dim3(NT), Lay::bytes,
+                     st, p);
+  return hipGetLastError();
+}
+
+hipError_t run_head_bwd(const HeadBwdArgs& p, hipStream_t st) {
+  if (p.NS > 1) {
+    HeadScanArgs s = {};
+    s.a = p.q;
+    s.b = p.dout;
+    s.g = p.g;
+    s.s_init = p.dht;
+    s.seg_state = p.seg_state;
+    s.seg_gam = p.seg_gam;
+    s.NS = p.NS;
+    s.SL = p.SL;
+    s.scale = p.scale;
+    s.H = p.H;
+    s.K = p.K;
+    s.V = p.V;
+    s.si = p.si;
+    hipError_t e = head_prepare_segments(s, true, st);
+    if (e != hipSuccess) return e;
+  }
+  const bool k64 = p.K <= 64, v64 = p.V <= 64;
+  if (k64 && v64) return launch_head_bwd<64, 64>(p, st);
+  if (k64) return launch_head_bwd<64, 128>(p, st);
+  if (v64) return launch_head_bwd<128, 64>(p, st);
+  return launch_head_bwd<128, 128>(p, st);
 }
 
 }  // namespace tops

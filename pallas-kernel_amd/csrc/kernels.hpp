@@ -131,4 +131,19 @@ struct HeadFwdArgs {
 };
 hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st);
 
+struct HeadBwdArgs {
+  const void *q, *k, *v, *g, *dout;
+  const void* h;          // [NC, H, K, V] bf16 forward states (chunk start)
+  const float* dht;       // nullable
+  void *dq, *dk, *dv, *dg;
+  float* dh0;             // nullable
+  float* seg_state;       // NS > 1 only
+  float* seg_gam;
+  int NS, SL;
+  float scale;
+  int H, K, V;
+  SeqInfo si;
+};
+hipError_t run_head_bwd(const HeadBwdArgs& p, hipStream_t st);
+
 }  // namespace tops
