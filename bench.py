@@ -7,13 +7,17 @@ already resident in HBM (numpy default_rng(seed=4), draw 
 q, k, v, g_raw, h0, do, dht; g = logsigmoid(g_raw) / 16; h0, dht ~ N(0, 0.1^2)).
 
 Prints ONE JSON line with the driver's fields plus
-  roofline     : the dominant kernel of a step (largest share of its time), timed alone on
-                 torch's current stream (the stream the C ABI launches on) with HIP events,
-                 against the HBM roofline with its algorithmic bytes per launch;
+  roofline     : the dominant kernel of a step (largest share of its time), timed with
+                 HIP events the library records on the launch stream (torch's current
+                 stream) right around that kernel, against the HBM roofline with its
+                 algorithmic bytes per launch, and the copy-calibrated rocprofv3
+                 FETCH_SIZE + WRITE_SIZE bytes per launch (profiles/hbm_traffic.json);
   cpu_baseline : the numpy oracle (float32, one thread) on a bounded sample of the same
                  workload (1 batch row, all 16 heads, full T), scaled to tokens/s of
                  the whole workload;
-  kernels      : every kernel's average duration and achieved GB/s.
+  kernels      : the fused forward / backward kernels: average duration, achieved GB/s;
+  stages       : the chunk_fwd / chunk_bwd entry points (segment local states + combine
+                 + fused kernel) and the part before the fused kernel.
 """
 
 from __future__ import annotations
@@ -74,12 +78,18 @@ def _copy_calibration(device, mib=512, reps=3):
 
 
 def _kernel_profile(x, reps=10):
-    """Average duration of each kernel of a step, each launched alone through the C ABI."""
+    """Per-launch duration of the step's dominant kernels, each launched through the C ABI.
+
+    kernels: the fused full-head forward / backward kernels, timed with the library's HIP
+    events recorded on the launch stream right around each kernel (tops_gla_kernel_ms);
+    stages: the whole entry points (segment local states + combine + fused kernel), timed
+    with torch events on the same stream."""
     import torch
 
     from tops import _lib
     from tops._lib import SeqLayout, call, ptr, stream_of
 
+    lib = _lib.load()
     dev = x["q"].device
     seq = SeqLayout(B, T, C, None, dev)
     st = stream_of(dev)
@@ -94,32 +104,40 @@ def _kernel_profile(x, reps=10):
     ws, nws = _lib.seg_workspace(B, T, H, K, V, C, False, torch.bfloat16, dev)
     tok = B * T * H
     hbytes = seq.NC * H * K * V * BF
-    kernels = {
-        # forward: segment local states + combine + fused state scan / output
-        "chunk_fwd": (lambda: call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g),
-                                   ptr(h0), ptr(o), ptr(ht), ptr(h), ptr(ws), nws, sc, *lay),
-                      tok * (3 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes),
-        # backward: segment local dh + combine + fused reverse scan / gradients
-        "chunk_bwd": (lambda: call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g),
-                                   ptr(h0), ptr(h), ptr(do), ptr(dht), ptr(dq), ptr(dk),
-                                   ptr(dv), ptr(dg), ptr(dh0), None, ptr(dh), ptr(ws), nws,
-                                   sc, *lay),
-                      tok * (6 * K + 3 * V) * BF + STATE_BYTES * 2 + hbytes),
-    }
-    res = {}
+    # (entry point, kernel name, timing slot, algorithmic bytes of the kernel per launch)
+    runs = [
+        ("chunk_fwd",
+         lambda: call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(o),
+                      ptr(ht), ptr(h), ptr(ws), nws, sc, *lay),
+         "head_fwd_kernel", 0, tok * (3 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes),
+        ("chunk_bwd",
+         lambda: call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(h),
+                      ptr(do), ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None,
+                      ptr(dh), ptr(ws), nws, sc, *lay),
+         "head_bwd_kernel", 1, tok * (6 * K + 3 * V) * BF + STATE_BYTES * 2 + hbytes),
+    ]
+    kernels, stages = {}, {}
     cur = torch.cuda.current_stream(dev)
-    for name, (fn, nbytes) in kernels.items():
-        fn()  # warm (and produces h / dh for the kernels after it)
+    for entry, fn, kname, slot, nbytes in runs:
+        fn()  # warm (the forward also produces the states the backward reads)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(cur)
         for _ in range(reps):
             fn()
         e1.record(cur)
         torch.cuda.synchronize(dev)
-        ms = e0.elapsed_time(e1) / reps
-        res[name] = dict(ms=round(ms, 4), bytes=int(nbytes),
-                         gbs=round(nbytes / (ms * 1e-3) / 1e9, 1))
-    return res
+        ems = e0.elapsed_time(e1) / reps
+        call("tops_gla_kernel_timing", 1)
+        kms = 0.0
+        for _ in range(reps):
+            fn()
+            kms += float(lib.tops_gla_kernel_ms(slot))
+        call("tops_gla_kernel_timing", 0)
+        kms /= reps
+        kernels[kname] = dict(ms=round(kms, 4), bytes=int(nbytes),
+                              gbs=round(nbytes / (kms * 1e-3) / 1e9, 1))
+        stages[entry] = dict(ms=round(ems, 4), segment_prep_ms=round(ems - kms, 4))
+    return kernels, stages
 
 
 def _measured_traffic(kernel):
@@ -237,7 +255,7 @@ def main():
         "mfma_frac": round(FLOPS_STEP / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
     }
     if not a.no_kernel_profile:
-        prof = _kernel_profile(x, max(1, a.profile_reps))
+        prof, stages = _kernel_profile(x, max(1, a.profile_reps))
         dom = max(prof, key=lambda n: prof[n]["ms"])
         d = prof[dom]
         out["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": d["gbs"],
@@ -245,6 +263,7 @@ def main():
                            "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
                            "traffic": _measured_traffic(dom)}
         out["kernels"] = prof
+        out["stages"] = stages
     if a.calibrate_copy:
         _copy_calibration(dev)
     if not a.no_cpu_baseline:

@@ -181,6 +181,16 @@ int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, co
                                  int64_t K, int64_t V, const int32_t* cu_seqlens, int64_t N,
                                  int dtype, int o_dtype, void* stream);
 
+/*
+ * Measurement hook (no counterpart in the reference): with timing enabled, HIP events are
+ * recorded on the launch stream around the fused full-head forward (which = 0) and
+ * backward (which = 1) kernels of tops_gla_chunk_fwd / tops_gla_chunk_bwd.
+ * tops_gla_kernel_ms waits for the last such launch and returns its duration in ms (-1 if
+ * there is none). Process-wide state, for profiling runs only.
+ */
+int tops_gla_kernel_timing(int enable);
+float tops_gla_kernel_ms(int which);
+
 #ifdef __cplusplus
 }
 #endif

@@ -134,7 +134,46 @@ void seg_setup(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void* w
 
 }  // namespace
 
+namespace tops {
+
+// Measurement hook state (process-wide; for profiling runs, not for concurrent callers).
+static bool g_kt_on = false;
+static bool g_kt_made = false;
+static bool g_kt_done[KT_COUNT] = {};
+static hipEvent_t g_kt_ev[KT_COUNT][2];
+
+void ktimer_mark(int which, bool stop, hipStream_t st) {
+  if (!g_kt_on) return;
+  if (hipEventRecord(g_kt_ev[which][stop ? 1 : 0], st) == hipSuccess && stop)
+    g_kt_done[which] = true;
+}
+
+}  // namespace tops
+
 extern "C" {
+
+int tops_gla_kernel_timing(int enable) {
+  if (enable && !tops::g_kt_made) {
+    for (int i = 0; i < tops::KT_COUNT; ++i)
+      for (int j = 0; j < 2; ++j)
+        if (hipEventCreate(&tops::g_kt_ev[i][j]) != hipSuccess)
+          return fail(TOPS_GLA_EHIP, "hipEventCreate failed");
+    tops::g_kt_made = true;
+  }
+  tops::g_kt_on = enable != 0;
+  for (int i = 0; i < tops::KT_COUNT; ++i) tops::g_kt_done[i] = false;
+  return ok();
+}
+
+float tops_gla_kernel_ms(int which) {
+  if (which < 0 || which >= tops::KT_COUNT || !tops::g_kt_done[which]) return -1.f;
+  float ms = -1.f;
+  if (hipEventSynchronize(tops::g_kt_ev[which][1]) != hipSuccess) return -1.f;
+  if (hipEventElapsedTime(&ms, tops::g_kt_ev[which][0], tops::g_kt_ev[which][1]) != hipSuccess)
+    return -1.f;
+  return ms;
+}
+
 
 const char* tops_gla_last_error(void) { return g_err; }
 

@@ -53,6 +53,13 @@ struct HTiles {
   static constexpr int NTV = VP / 16 / 2;   // v tiles per wave
   static constexpr int NTK = KP / 16 / 4;   // k tiles per wave
 };
+// The same split for NW waves: v tiles by halves (w & 1), k tiles over the NW / 2 pairs.
+template <int KP, int VP, int NW>
+struct HTilesN {
+  static constexpr int NTV = VP / 16 / 2;
+  static constexpr int NTK = KP / 16 / (NW / 2);
+  static_assert(NTK >= 1, "tile split");
+};
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -148,22 +155,24 @@ __device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP, NT>::RP
   if (lane >= 64 - M::NCG) st_f8(sTot + w * KP + cg * 8, x);   // wave total
   if (rs == 0) st_f8(sFirst + cg * 8, gt[0]);
   __syncthreads();
-  float off[8];
+  // earlier waves' totals (w is wave-uniform: plain loops, no per-lane selects)
+  float off[8], t[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    off[e] = x[e] - gt[M::RPT - 1][e];   // exclusive prefix within the wave
-    gam[e] = 0.f;
-  }
-#pragma unroll
-  for (int ww = 0; ww < NT / 64; ++ww) {
-    float t[8];
+  for (int e = 0; e < 8; ++e) off[e] = 0.f;
+  for (int ww = 0; ww < w; ++ww) {
     ld_f8(sTot + ww * KP + cg * 8, t);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      gam[e] += t[e];
-      if (ww < w) off[e] += t[e];
-    }
+    for (int e = 0; e < 8; ++e) off[e] += t[e];
   }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) gam[e] = off[e];
+  for (int ww = w; ww < NT / 64; ++ww) {
+    ld_f8(sTot + ww * KP + cg * 8, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gam[e] += t[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) off[e] += x[e] - gt[M::RPT - 1][e];   // + earlier segments
   ld_f8(sFirst + cg * 8, first);
 #pragma unroll
   for (int j = 0; j < M::RPT; ++j)
@@ -260,17 +269,17 @@ __device__ __forceinline__ void state_update(f32x4 (&acc)[NTV][NTK], const bf16*
 // ---------------------------------------------------------------------------
 // State scan: forward h (a = k, b = v) or reverse dh (a = q, b = do)
 // ---------------------------------------------------------------------------
-template <int KP, int VP, bool REV>
-__global__ __launch_bounds__(HNT) void head_scan_kernel(HeadScanArgs p) {
-  using MA = HMap<KP>;
-  using MB = HMap<VP>;
-  using TL = HTiles<KP, VP>;
+template <int KP, int VP, bool REV, int NT>
+__global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
+  using MA = HMap<KP, NT>;
+  using MB = HMap<VP, NT>;
+  using TL = HTilesN<KP, VP, NT / 64>;
   constexpr int RPT = MA::RPT, VRPT = MB::RPT;
   constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP);
   constexpr int NTV = TL::NTV, NTK = TL::NTK;
   __shared__ __attribute__((aligned(16))) bf16 sA[HC * PKP];
   __shared__ __attribute__((aligned(16))) bf16 sB[HC * PVP];
-  __shared__ __attribute__((aligned(16))) float sTot[HNW * KP];
+  __shared__ __attribute__((aligned(16))) float sTot[(NT / 64) * KP];
   __shared__ __attribute__((aligned(16))) float sFirst[KP];
   __shared__ __attribute__((aligned(16))) float sGam[KP];
 
@@ -279,7 +288,8 @@ __global__ __launch_bounds__(HNT) void head_scan_kernel(HeadScanArgs p) {
   const bf16* __restrict__ g = (const bf16*)p.g;
   bf16* __restrict__ s_all = (bf16*)p.s_all;
   const int H = p.H, K = p.K, V = p.V;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, scalar
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int hh = L % H;
   const int nsl = p.ns_launch;
@@ -333,7 +343,7 @@ __global__ __launch_bounds__(HNT) void head_scan_kernel(HeadScanArgs p) {
     for (int j = 0; j < RPT; ++j)
       gm[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
     float gt[RPT][8], gam[8], first[8];
-    head_cumsum<KP>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+    head_cumsum<KP, NT>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
     (void)first;
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
@@ -481,7 +491,8 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   bf16* __restrict__ o = (bf16*)p.o;
   bf16* __restrict__ hout = (bf16*)p.h_out;
   const int H = p.H, K = p.K, V = p.V;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, scalar
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int hh = L % H;
   const int s = (L / H) % p.NS;
@@ -742,7 +753,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   bf16* __restrict__ dv = (bf16*)p.dv;
   bf16* __restrict__ dg = (bf16*)p.dg;
   const int H = p.H, K = p.K, V = p.V;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, scalar
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int hh = L % H;
   const int s = (L / H) % p.NS;
@@ -1061,12 +1073,10 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       float off[8], t8[8], u8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) off[e] = x[e] - pr[0][e];   // later segments of the wave
-#pragma unroll
-      for (int ww = 0; ww < NW; ++ww) {
+      for (int ww = w + 1; ww < NW; ++ww) {   // later waves (w is wave-uniform)
         ld_f8(sSuf + ww * KP + cg * 8, t8);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (ww > w) off[e] += t8[e];
+        for (int e = 0; e < 8; ++e) off[e] += t8[e];
       }
       ld_f8(sEg + cg * 8, t8);
       ld_f8(sHd + cg * 8, u8);
@@ -1127,8 +1137,9 @@ long head_seg_ws_bytes(int N, int NS, int H, int K, int V) {
 
 template <int KP, int VP, bool REV>
 static hipError_t launch_head_scan(const HeadScanArgs& p, hipStream_t st, long blocks) {
-  hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV>), dim3((unsigned)blocks), dim3(HNT), 0, st,
-                     p);
+  constexpr int NT = HNT;
+  hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV, NT>), dim3((unsigned)blocks), dim3(NT), 0,
+                     st, p);
   return hipGetLastError();
 }
 
@@ -1191,14 +1202,16 @@ static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   hipError_t e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
   if (e != hipSuccess) return e;
+  ktimer_mark(KT_HEAD_FWD, false, st);
   hipLaunchKernelGGL((head_fwd_kernel<KP, VP>), dim3((unsigned)blocks), dim3(HNT), Lay::bytes,
                      st, p);
+  ktimer_mark(KT_HEAD_FWD, true, st);
   return hipGetLastError();
 }
 
 hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   if (p.NS > 1) {
-    HeadScanArgs s;
+    HeadScanArgs s = {};
     s.a = p.k;
     s.b = p.v;
     s.g = p.g;
@@ -1234,8 +1247,10 @@ static hipError_t launch_head_bwd(const HeadBwdArgs& p, hipStream_t st) {
   hipError_t e = hipFuncSetAttribute((const void*)head_bwd_kernel<KP, VP, NT>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
   if (e != hipSuccess) return e;
+  ktimer_mark(KT_HEAD_BWD, false, st);
   hipLaunchKernelGGL((head_bwd_kernel<KP, VP, NT>), dim3((unsigned)blocks), dim3(NT), Lay::bytes,
                      st, p);
+  ktimer_mark(KT_HEAD_BWD, true, st);
   return hipGetLastError();
 }
 

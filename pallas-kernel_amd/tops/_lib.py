@@ -48,8 +48,11 @@ _SIGS = {
     "tops_gla_fused_recurrent_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _F, _I, _I64, _I64, _I64,
                                      _I64, _I64, _P, _I64, _I, _I, _P],
 }
+_SIGS["tops_gla_kernel_timing"] = [_I]
+_SIGS["tops_gla_kernel_ms"] = [_I]
+
 # entry points that do not return a status code
-_RESTYPE = {"tops_gla_chunk_ws_bytes": ctypes.c_int64}
+_RESTYPE = {"tops_gla_chunk_ws_bytes": ctypes.c_int64, "tops_gla_kernel_ms": ctypes.c_float}
 
 EXPORTED = ["tops_gla_last_error", "tops_gla_version"] + list(_SIGS)
 

@@ -24,7 +24,7 @@ def _declared():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     out = {}
-    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(tops_gla_\w+)\s*\(([^)]*)\)\s*;", src):
+    for m in re.finditer(r"\b(?:int|int64_t|float|const char\*)\s+(tops_gla_\w+)\s*\(([^)]*)\)\s*;", src):
         params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
         out[m.group(1)] = len(params)
     return out
@@ -32,7 +32,7 @@ def _declared():
 
 def test_header_lists_entry_points():
     decl = _declared()
-    assert len(decl) == 12, decl
+    assert len(decl) == 14, decl
     assert set(decl) == set(_lib.EXPORTED)
 
 
