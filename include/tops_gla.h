@@ -171,7 +171,7 @@ int tops_gla_chunk_bwd_dv(const void* q, const void* k, const void* g, const voi
 
 /*
  * Fused recurrent forward. gk [B, T, H, K] / gv [B, T, H, V] gates may be NULL; o is
- * written in o_dtype (the reference returns float32); h0/ht float32, may be NULL.
+ * written in o_dtype (the reference returns float32); h0/ht float32, may be NULL. K <= 512.
  * Replaces: _fused_recurrent_gla_fwd pallas_call, tops/ops/gla/fused_recurrent.py:344-362
  *           (body :139-227).
  */
@@ -180,6 +180,25 @@ int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, co
                                  float scale, int reverse, int64_t B, int64_t T, int64_t H,
                                  int64_t K, int64_t V, const int32_t* cu_seqlens, int64_t N,
                                  int dtype, int o_dtype, void* stream);
+
+/*
+ * Fused recurrent backward: dq, dk, dv [B, T, H, K|V] float32 (the reference's output
+ * dtype), dgk / dgv float32 for the gates that are given (NULL otherwise), dh0 [N, H, K, V]
+ * float32 (NULL: not computed). o is the forward output in float32, required with gv.
+ * h0 / dht float32, may be NULL. ht_ws: caller workspace of N*H*K*V floats that receives the
+ * recomputed final state; required when dht and a gate are given, else may be NULL.
+ * K and V up to 512.
+ * Replaces: _fused_recurrent_gla_bwd pallas_call + _compute_gate_grads,
+ *           tops/ops/gla/fused_recurrent.py:776-795 and :798-876 (body :495-624, entry
+ *           :879-956).
+ */
+int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v, const void* gk,
+                                 const void* gv, const float* o, const void* dout,
+                                 const float* dht, const float* h0, float* dq, float* dk,
+                                 float* dv, float* dgk, float* dgv, float* dh0, float* ht_ws,
+                                 float scale, int reverse, int64_t B, int64_t T, int64_t H,
+                                 int64_t K, int64_t V, const int32_t* cu_seqlens, int64_t N,
+                                 int dtype, void* stream);
 
 /*
  * Measurement hook (no counterpart in the reference): with timing enabled, HIP events are

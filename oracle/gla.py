@@ -184,7 +184,7 @@ def fused_recurrent_gla_bwd(q, k, v, gk=None, gv=None, o=None, do=None, dht=None
         h = np.zeros((H, K, V), dtype)
         if h0 is not None:
             h = h + h0[i]
-        gated, states = {}, {}
+        gated = {}
         for t in ts:
             hg = h
             if gk is not None:
@@ -193,7 +193,6 @@ def fused_recurrent_gla_bwd(q, k, v, gk=None, gv=None, o=None, do=None, dht=None
                 hg = hg * np.exp(gv[b, t])[:, None, :]
             gated[t] = hg
             h = hg + k[b, t][:, :, None] * v[b, t][:, None, :]
-            states[t] = h
             dq[b, t] = scale * np.einsum("hkv,hv->hk", h, do[b, t])
         dh = np.zeros((H, K, V), dtype)
         if dht is not None:

@@ -644,8 +644,8 @@ int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, co
   if (dtype == TOPS_GLA_F32 && o_dtype != TOPS_GLA_F32)
     return fail(TOPS_GLA_EUNSUPPORTED, "float32 inputs need a float32 output");
   if (K <= 0 || V <= 0) return fail(TOPS_GLA_EINVAL, "K and V must be positive");
-  if (K > 256)
-    return fail(TOPS_GLA_EUNSUPPORTED, "fused_recurrent keeps K <= 256 in registers (K=%lld)",
+  if (K > 512)
+    return fail(TOPS_GLA_EUNSUPPORTED, "fused_recurrent keeps K <= 512 in registers (K=%lld)",
                 (long long)K);
   tops::SeqInfo si;
   const int64_t NC = cu_seqlens ? 0 : B * T;  // chunk count unused; 1-token "chunks"
@@ -653,7 +653,7 @@ int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, co
   if (rc) return rc;
   if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || o == nullptr))
     return fail(TOPS_GLA_EINVAL, "q, k, v and o must not be NULL");
-  if ((int64_t)si.N * H * ((V + 63) / 64) > kMaxInt)
+  if ((int64_t)si.N * H * ((V + 31) / 32) > kMaxInt)
     return fail(TOPS_GLA_EUNSUPPORTED, "grid too large");
   tops::RecArgs p;
   p.q = q;
@@ -672,6 +672,64 @@ int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, co
   p.si = si;
   return hip_status(tops::run_recurrent_fwd(p, dtype, o_dtype, (hipStream_t)stream),
                     "fused_recurrent_fwd");
+}
+
+int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v, const void* gk,
+                                 const void* gv, const float* o, const void* dout,
+                                 const float* dht, const float* h0, float* dq, float* dk,
+                                 float* dv, float* dgk, float* dgv, float* dh0, float* ht_ws,
+                                 float scale, int reverse, int64_t B, int64_t T, int64_t H,
+                                 int64_t K, int64_t V, const int32_t* cu_seqlens, int64_t N,
+                                 int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(TOPS_GLA_EINVAL, "bad dtype");
+  if (K <= 0 || V <= 0) return fail(TOPS_GLA_EINVAL, "K and V must be positive");
+  if (!tops::recurrent_supported((int)std::min<int64_t>(K, 1 << 20),
+                                 (int)std::min<int64_t>(V, 1 << 20)))
+    return fail(TOPS_GLA_EUNSUPPORTED,
+                "fused_recurrent backward keeps K, V <= 512 in registers (K=%lld, V=%lld)",
+                (long long)K, (long long)V);
+  tops::SeqInfo si;
+  const int64_t NC = cu_seqlens ? 0 : B * T;
+  int rc = make_seq(B, T, H, 1, cu_seqlens, nullptr, N, NC, false, &si);
+  if (rc) return rc;
+  if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || dout == nullptr ||
+                    dq == nullptr || dk == nullptr || dv == nullptr))
+    return fail(TOPS_GLA_EINVAL, "q, k, v, dout, dq, dk and dv must not be NULL");
+  if ((gk == nullptr) != (dgk == nullptr))
+    return fail(TOPS_GLA_EINVAL, "dgk must be given exactly when gk is");
+  if ((gv == nullptr) != (dgv == nullptr))
+    return fail(TOPS_GLA_EINVAL, "dgv must be given exactly when gv is");
+  if (gv != nullptr && B * T > 0 && o == nullptr)
+    return fail(TOPS_GLA_EINVAL, "o (forward output) is required when gv is used");
+  if (dht != nullptr && (gk != nullptr || gv != nullptr) && ht_ws == nullptr)
+    return fail(TOPS_GLA_EINVAL, "ht_ws is required when dht and a gate are given");
+  if ((int64_t)si.N * H * ((std::max(K, V) + 31) / 32) > kMaxInt)
+    return fail(TOPS_GLA_EUNSUPPORTED, "grid too large");
+  tops::RecBwdArgs p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.gk = gk;
+  p.gv = gv;
+  p.dout = dout;
+  p.o = o;
+  p.h0 = h0;
+  p.dht = dht;
+  p.dq = dq;
+  p.dk = dk;
+  p.dv = dv;
+  p.dgk = dgk;
+  p.dgv = dgv;
+  p.dh0 = dh0;
+  p.ht_ws = ht_ws;
+  p.scale = scale;
+  p.H = (int)H;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.reverse = reverse != 0;
+  p.si = si;
+  return hip_status(tops::run_recurrent_bwd(p, dtype, (hipStream_t)stream),
+                    "fused_recurrent_bwd");
 }
 
 }  // extern "C"

@@ -94,6 +94,43 @@ struct RecArgs {
 };
 hipError_t run_recurrent_fwd(const RecArgs& p, int dtype, int o_dtype, hipStream_t st);
 
+// Fused recurrent forward / backward (recurrent.hip). One element-wise state scan:
+//   S <- S (.) (e^{ga[r]} e^{gb[c]}) + (sa a[r]) b[c],  out[c] = so sum_r o[r] S[r][c]
+struct RecScanArgs {
+  const void *a, *ga, *o;  // row side [tokens, H, R]; ga nullable (raw log gate)
+  const void *b, *gb;      // column side [tokens, H, C]; gb nullable
+  const float* s0;         // initial state [N, H, ...] f32, nullable
+  float* sN;               // final state, nullable
+  int s_trans;             // states stored [C][R] (1) or [R][C] (0)
+  int final_gate;          // apply the last step's gate before storing sN
+  void* out;               // [tokens, H, C], out dtype (f32 in the backward)
+  float sa, so;
+  int R, C, H;
+  int dir;    // 0: bos -> eos, 1: eos - 1 -> bos
+  int shift;  // the gate of a step is applied at the next processed step
+  // gate-gradient epilogue (dg nullable): dg = running sum of gx gxf - gy out
+  // (+ sum_r s0 (.) hfin when hfin is given)
+  const void* gx;
+  const float* gxf;
+  const void* gy;
+  const float* hfin;
+  float* dg;
+  SeqInfo si;  // C unused
+};
+struct RecBwdArgs {
+  const void *q, *k, *v, *gk, *gv, *dout;  // gk / gv nullable
+  const float* o;                          // forward output f32 (needed with gv)
+  const float *h0, *dht;                   // nullable
+  float *dq, *dk, *dv, *dgk, *dgv, *dh0;   // dgk / dgv / dh0 nullable
+  float* ht_ws;                            // [N, H, K, V] f32, needed with dht and a gate
+  float scale;
+  int H, K, V;
+  int reverse;
+  SeqInfo si;
+};
+bool recurrent_supported(int K, int V);  // state rows K (forward) and V, K (backward)
+hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st);
+
 // Full-head kernels (chunk_head.hip): bf16, chunk 64, K and V <= 128 (multiples of 8,
 // 16-byte aligned rows), raw gates. Optional sequence segments (fixed-length sequences):
 // seg_state [N, NS, H, K, V] f32 and seg_gam [N, NS, H, K] f32 workspaces.

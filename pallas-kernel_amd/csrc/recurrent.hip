@@ -1,174 +1,607 @@
-// Fused recurrent GLA forward: per-token state update, no MFMA.
-// Reference: _fused_recurrent_gla_fwd_kernel, tops/ops/gla/fused_recurrent.py:139-227
-// (launcher :235-371, jnp ref :17-132):
-//   h <- h * e^{gk_t}[:, None] * e^{gv_t}[None, :] + k_t v_t^T ;  o_t = (scale q_t) . h
-// processed forward or in reverse within each sequence.
+// Fused recurrent GLA, forward and backward, on one element-wise scan kernel (fp32 VALU,
+// no MFMA: the state update is a rank-1 outer product per token).
+// Reference: tops/ops/gla/fused_recurrent.py — forward _fused_recurrent_gla_fwd_kernel
+// :139-227 (launcher :235-371, jnp ref :17-132); backward _fused_recurrent_gla_bwd_kernel
+// :495-624 (launcher :626-795), gate gradients _compute_gate_grads :798-876, entry :879-956.
 //
-// One 256-thread block per (sequence, head, 64-wide V tile). Lane l owns value column
-// vt*64 + l; wave w owns key rows [w*KPT, (w+1)*KPT), so a thread carries KPT fp32 state
-// values in registers. q (pre-scaled), k, e^{gk}, v, e^{gv} of TB consecutive tokens are
-// staged in LDS (the q/k/gk reads are wave-uniform broadcasts); each wave writes its partial
-// o_t to LDS and the four partials are summed once per staged block.
+// The scan, over an [R x C] fp32 state per (sequence, head), processed forward or backward
+// in time:
+//   S <- S (.) (e^{ga[r]} e^{gb[c]}) + (sa a[r]) b[c],   out[c] = so sum_r o[r] S[r][c]
+//   forward : S = h    [K x V], a = k, b = v, o = q (so = scale); out = o, final state ht
+//   bwd 1 dq: S = h^T  [V x K], a = v, b = k, o = do (so = scale), forward's direction
+//   bwd 2 dk: S = dh^T [V x K], a = do (sa = scale), b = q, o = v, opposite direction
+//   bwd 3 dv: S = dh   [K x V], a = q (sa = scale), b = do, o = k, opposite direction
+// Each output reduces over the state's rows, which never leave the block, so no output
+// needs a reduction across blocks. In the backward scans the gate of a step is applied when
+// the next step is processed (dh_{t-1} = G_t (.) dh_t); scan 3 applies the last one before
+// storing dh0. The gate gradients follow from the reference's identity (:798-876)
+//   dgk_t = sum_{s at or after t in scan order} (q_s dq_s - k_s dk_s) + sum_v dht (.) h_T
+//   dgv_t = sum_{s ...} (o_s do_s - v_s dv_s)                          + sum_k dht (.) h_T
+// and scans 2 and 3 visit the steps in exactly that order, so they accumulate the sums as
+// they emit dk and dv (the epilogue below); h_T is the final state of scan 1.
+//
+// Block = (sequence, head, tile of CB columns), 512 threads (8 waves). A thread holds an
+// RPT x 4 sub-tile of the state: lane l = rgl * NCG + cg owns columns cg*4 .. cg*4+3 and
+// row group rgl of its wave (RGW = 64 / NCG row groups per wave). Per step a thread reads
+// its rows' a, gate, o and its columns' b, gate from LDS (staged TB steps at a time, the
+// next stage's global loads in flight while the current one computes), updates 4 * RPT
+// state values and folds its 4 partial outputs across the wave's row groups with
+// v_permlane32_swap / v_permlane16_swap (and a DPP row rotate for 32-column tiles): the
+// lane ends with one column's sum, and the 8 waves' sums meet in LDS.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace tops {
 
-constexpr int REC_TB = 16;
+namespace {
 
-template <typename T, typename TO, int KPT>
-__global__ __launch_bounds__(256) void recurrent_fwd_kernel(RecArgs p) {
-  constexpr int KP = 4 * KPT;
-  constexpr int TB = REC_TB;
-  __shared__ __attribute__((aligned(16))) float sQ[TB * KP];
-  __shared__ __attribute__((aligned(16))) float sK[TB * KP];
-  __shared__ __attribute__((aligned(16))) float sG[TB * KP];
-  __shared__ float sV[TB * 64];
-  __shared__ float sGV[TB * 64];
-  __shared__ float sO[4 * TB * 64];
+constexpr int RNT = 512;  // threads per block
+constexpr int RNW = RNT / 64;
 
-  const T* __restrict__ q = (const T*)p.q;
-  const T* __restrict__ k = (const T*)p.k;
-  const T* __restrict__ v = (const T*)p.v;
-  const T* __restrict__ gk = (const T*)p.gk;
-  const T* __restrict__ gv = (const T*)p.gv;
-  TO* __restrict__ o = (TO*)p.o;
+template <int NCG, int RPT>
+struct RecCfg {
+  static constexpr int CB = NCG * 4;                 // columns per block
+  static constexpr int RGW = 64 / NCG;               // row groups per wave
+  static constexpr int NRG = RNW * RGW;              // row groups per block
+  static constexpr int RP = NRG * RPT;               // rows covered
+  static constexpr int TB = 16;                      // steps per stage
+};
 
-  const int H = p.H, K = p.K, V = p.V;
-  const int VT = (V + 63) >> 6;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int vt = L % VT;
-  const int bh = L / VT;
-  const int seq = bh / H, hh = bh % H;
-  int bos, eos;
-  seq_bounds(p.si, seq, bos, eos);  // varlen here carries no chunk offsets
-  const int Tq = eos - bos;
-  const int vcol = vt * 64 + lane;
-  const bool vvalid = vcol < V;
-  const int k0 = w * KPT;
+__device__ __forceinline__ long st_off(int r, int c, int R, int C, bool trans) {
+  return trans ? (long)c * R + r : (long)r * C + c;
+}
 
-  const long sbase = (((long)seq * H + hh) * K + k0) * V + vcol;  // state element (k0, vcol)
-  const int kn = min(KPT, K - k0);                                  // valid rows of this wave
-  float hr[KPT];
+__device__ __forceinline__ float ror8(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf,
+                                                    false));
+}
+
+// Sum of x[0..3] (columns cg*4 + j of this lane) over the wave's row groups. Lane l ends
+// with the sum for column (l & (NCG - 1)) * 4 + (l >> 4); for NCG = 8, lanes with bit 3
+// set hold a duplicate.
+template <int NCG>
+__device__ __forceinline__ float wave_colsum(float (&x)[4]) {
+  if (NCG == 8) {
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) hr[j] = 0.f;
-  if (p.h0 && vvalid) {
-    const float* src = p.h0 + sbase;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j)
-      if (j < kn) hr[j] = src[(long)j * V];
+    for (int j = 0; j < 4; ++j) x[j] += ror8(x[j]);
   }
-  const bool has_gk = gk != nullptr, has_gv = gv != nullptr;
+  const auto p0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[0]),
+                                                   __float_as_uint(x[2]), false, false);
+  const auto p1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[1]),
+                                                   __float_as_uint(x[3]), false, false);
+  const float u0 = __uint_as_float(p0[0]) + __uint_as_float(p0[1]);
+  const float u1 = __uint_as_float(p1[0]) + __uint_as_float(p1[1]);
+  const auto p2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(u0), __float_as_uint(u1),
+                                                   false, false);
+  return __uint_as_float(p2[0]) + __uint_as_float(p2[1]);
+}
 
-  for (int b0 = 0; b0 < Tq; b0 += TB) {
-    const int nb = min(TB, Tq - b0);
-    // stage TB tokens
-#pragma unroll 1
-    for (int i = tid; i < TB * KP; i += 256) {
-      const int s = i / KP, kk = i % KP;
-      float xq = 0.f, xk = 0.f, xg = 1.f;
-      if (s < nb && kk < K) {
-        const int tau = p.reverse ? (eos - 1 - (b0 + s)) : (bos + b0 + s);
-        const long a = ((long)tau * H + hh) * K + kk;
-        xq = to_f32(q[a]) * p.scale;
-        xk = to_f32(k[a]);
-        if (has_gk) xg = gexp<T>(to_f32(gk[a]));
-      }
-      sQ[i] = xq;
-      sK[i] = xk;
-      sG[i] = xg;
-    }
-#pragma unroll 1
-    for (int i = tid; i < TB * 64; i += 256) {
-      const int s = i >> 6, vv = vt * 64 + (i & 63);
-      float xv = 0.f, xg = 1.f;
-      if (s < nb && vv < V) {
-        const int tau = p.reverse ? (eos - 1 - (b0 + s)) : (bos + b0 + s);
-        const long a = ((long)tau * H + hh) * V + vv;
-        xv = to_f32(v[a]);
-        if (has_gv) xg = gexp<T>(to_f32(gv[a]));
-      }
-      sV[i] = xv;
-      sGV[i] = xg;
-    }
-    __syncthreads();
-#pragma unroll 1
-    for (int s = 0; s < nb; ++s) {
-      const float vv = sV[s * 64 + lane];
-      const float gvv = sGV[s * 64 + lane];
-      const float4* q4 = reinterpret_cast<const float4*>(sQ + s * KP + k0);
-      const float4* k4 = reinterpret_cast<const float4*>(sK + s * KP + k0);
-      const float4* g4 = reinterpret_cast<const float4*>(sG + s * KP + k0);
-      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+template <int NCG>
+__device__ __forceinline__ int lane_col(int l) { return (l & (NCG - 1)) * 4 + (l >> 4); }
+template <int NCG>
+__device__ __forceinline__ bool lane_writes(int l) { return NCG == 16 || (l & 8) == 0; }
+
+// N consecutive elements (N * sizeof(T) bytes aligned) to fp32, in one load.
+template <typename T, int N>
+__device__ __forceinline__ void ld_vec(const T* p, float (&x)[N]);
+template <>
+__device__ __forceinline__ void ld_vec<float, 1>(const float* p, float (&x)[1]) { x[0] = *p; }
+template <>
+__device__ __forceinline__ void ld_vec<float, 2>(const float* p, float (&x)[2]) {
+  const float2 v = *reinterpret_cast<const float2*>(p);
+  x[0] = v.x; x[1] = v.y;
+}
+template <>
+__device__ __forceinline__ void ld_vec<float, 4>(const float* p, float (&x)[4]) {
+  const float4 v = *reinterpret_cast<const float4*>(p);
+  x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+}
+template <>
+__device__ __forceinline__ void ld_vec<float, 8>(const float* p, float (&x)[8]) {
+  const float4 v = *reinterpret_cast<const float4*>(p);
+  const float4 u = *reinterpret_cast<const float4*>(p + 4);
+  x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w; x[4] = u.x; x[5] = u.y; x[6] = u.z; x[7] = u.w;
+}
+__device__ __forceinline__ void bf2(uint32_t u, float& lo, float& hi) {
+  lo = __uint_as_float(u << 16);
+  hi = __uint_as_float(u & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ void ld_vec<bf16, 1>(const bf16* p, float (&x)[1]) {
+  x[0] = to_f32(*p);
+}
+template <>
+__device__ __forceinline__ void ld_vec<bf16, 2>(const bf16* p, float (&x)[2]) {
+  bf2(*reinterpret_cast<const uint32_t*>(p), x[0], x[1]);
+}
+template <>
+__device__ __forceinline__ void ld_vec<bf16, 4>(const bf16* p, float (&x)[4]) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  bf2(u.x, x[0], x[1]);
+  bf2(u.y, x[2], x[3]);
+}
+template <>
+__device__ __forceinline__ void ld_vec<bf16, 8>(const bf16* p, float (&x)[8]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  bf2(u.x, x[0], x[1]);
+  bf2(u.y, x[2], x[3]);
+  bf2(u.z, x[4], x[5]);
+  bf2(u.w, x[6], x[7]);
+}
+
+// N consecutive floats to LDS (N * 4 bytes aligned).
+template <int N>
+__device__ __forceinline__ void st_vec(float* p, const float (&x)[N]) {
+  if constexpr (N % 4 == 0) {
 #pragma unroll
-      for (int j4 = 0; j4 < KPT / 4; ++j4) {
-        const float4 qq = q4[j4], kk = k4[j4];
-        float4 gg = g4[j4];
-        if (has_gv) {
-          gg.x *= gvv;
-          gg.y *= gvv;
-          gg.z *= gvv;
-          gg.w *= gvv;
-        }
-        hr[4 * j4 + 0] = fmaf(hr[4 * j4 + 0], gg.x, kk.x * vv);
-        hr[4 * j4 + 1] = fmaf(hr[4 * j4 + 1], gg.y, kk.y * vv);
-        hr[4 * j4 + 2] = fmaf(hr[4 * j4 + 2], gg.z, kk.z * vv);
-        hr[4 * j4 + 3] = fmaf(hr[4 * j4 + 3], gg.w, kk.w * vv);
-        o0 = fmaf(qq.x, hr[4 * j4 + 0], o0);
-        o1 = fmaf(qq.y, hr[4 * j4 + 1], o1);
-        o2 = fmaf(qq.z, hr[4 * j4 + 2], o2);
-        o3 = fmaf(qq.w, hr[4 * j4 + 3], o3);
-      }
-      sO[(w * TB + s) * 64 + lane] = (o0 + o1) + (o2 + o3);
-    }
-    __syncthreads();
-#pragma unroll 1
-    for (int i = tid; i < nb * 64; i += 256) {
-      const int s = i >> 6, vl = i & 63;
-      const int vv = vt * 64 + vl;
-      if (vv < V) {
-        const float val = sO[(0 * TB + s) * 64 + vl] + sO[(1 * TB + s) * 64 + vl] +
-                          sO[(2 * TB + s) * 64 + vl] + sO[(3 * TB + s) * 64 + vl];
-        const int tau = p.reverse ? (eos - 1 - (b0 + s)) : (bos + b0 + s);
-        o[((long)tau * H + hh) * V + vv] = from_f32<TO>(val);
-      }
-    }
-  }
-  if (p.ht && vvalid) {
-    float* dst = p.ht + sbase;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j)
-      if (j < kn) dst[(long)j * V] = hr[j];
+    for (int i = 0; i < N; i += 4)
+      *reinterpret_cast<float4*>(p + i) = make_float4(x[i], x[i + 1], x[i + 2], x[i + 3]);
+  } else if constexpr (N == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+  } else {
+    p[0] = x[0];
   }
 }
 
-template <typename T, typename TO, int KPT>
-static hipError_t launch_rec(const RecArgs& p, hipStream_t st) {
-  const int VT = (p.V + 63) / 64;
-  const long blocks = (long)p.si.N * p.H * VT;
+template <typename TO>
+__device__ __forceinline__ void put(void* p, long i, float x) {
+  static_cast<TO*>(p)[i] = from_f32<TO>(x);
+}
+
+}  // namespace
+
+template <typename T, typename TO, int NCG, int RPT>
+__global__ __launch_bounds__(RNT) void rec_scan_kernel(RecScanArgs p) {
+  using Cf = RecCfg<NCG, RPT>;
+  constexpr int CB = Cf::CB, RP = Cf::RP, TB = Cf::TB, RGW = Cf::RGW;
+  static_assert(RPT == 2 || RPT % 4 == 0, "rows are read as float2 / float4");
+  __shared__ __attribute__((aligned(16))) float sA[TB * RP];   // sa * a
+  __shared__ __attribute__((aligned(16))) float sGR[TB * RP];  // e^{ga} of the gate step
+  __shared__ __attribute__((aligned(16))) float sOR[TB * RP];  // so * o
+  __shared__ __attribute__((aligned(16))) float sB[TB * CB];
+  __shared__ __attribute__((aligned(16))) float sGC[TB * CB];
+  __shared__ float sXD[TB * CB];  // epilogue: gx * gxf
+  __shared__ float sY[TB * CB];   // epilogue: gy
+  __shared__ float sO[RNW * TB * CB];
+
+  const T* __restrict__ a = (const T*)p.a;
+  const T* __restrict__ ga = (const T*)p.ga;
+  const T* __restrict__ orow = (const T*)p.o;
+  const T* __restrict__ b = (const T*)p.b;
+  const T* __restrict__ gb = (const T*)p.gb;
+  const T* __restrict__ gx = (const T*)p.gx;
+  const T* __restrict__ gy = (const T*)p.gy;
+
+  const int H = p.H, R = p.R, C = p.C;
+  const int NCT = (C + CB - 1) / CB;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int ct = L % NCT;
+  const int sh = L / NCT;
+  const int seq = sh / H, hh = sh % H;
+  int bos, eos;
+  seq_bounds(p.si, seq, bos, eos);
+  const int n = eos - bos;
+  const int cg = lane % NCG;
+  const int rg = w * RGW + lane / NCG;
+  const int r0 = rg * RPT;
+  const int cbase = ct * CB;
+  const int c0 = cbase + cg * 4;
+  const bool trans = p.s_trans != 0;
+  const long sbase = ((long)seq * H + hh) * R * C;
+  const bool has_ga = ga != nullptr, has_gb = gb != nullptr;
+  const bool grad = p.dg != nullptr;
+  const long rsR = (long)H * R, rsC = (long)H * C;
+  auto tok = [&](int i) { return p.dir ? eos - 1 - i : bos + i; };
+
+  // State element (r0 + j, c0 + i), clamped into range: unconditional loads, out-of-range
+  // values dropped by a select (no per-element branches).
+  auto st_at = [&](int j, int i) {
+    return sbase + st_off(min(r0 + j, R - 1), min(c0 + i, C - 1), R, C, trans);
+  };
+  auto ok = [&](int j, int i) { return r0 + j < R && c0 + i < C; };
+  float S[RPT][4];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) S[j][i] = 0.f;
+  if (p.s0) {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = p.s0[st_at(j, i)];
+        S[j][i] = ok(j, i) ? x : 0.f;
+      }
+  }
+
+  // Epilogue constant: sum_r s0 (.) hfin over the rows of each column.
+  __shared__ float sCorr[CB];
+  if (grad && tid < CB) sCorr[tid] = 0.f;
+  if (grad && p.s0 && p.hfin) {
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] += S[j][i] * p.hfin[st_at(j, i)];  // S = 0 outside
+    const float cs = wave_colsum<NCG>(x);
+    if (lane_writes<NCG>(lane)) sO[w * CB + lane_col<NCG>(lane)] = cs;
+    __syncthreads();
+    if (tid < CB) {
+      float corr = 0.f;
+      for (int ww = 0; ww < RNW; ++ww) corr += sO[ww * CB + tid];
+      sCorr[tid] = corr;
+    }
+  }
+  float run[CB * 16 / RNT] = {};  // epilogue carries of this thread's columns
+
+  // Staging: wave w loads steps w and w + 8 of a stage, so each load has a wave-uniform
+  // token; lane l loads rows l*RL .. l*RL+RL-1 (one vector load per array when the rows are
+  // whole and aligned) and column cbase + l of the column side.
+  constexpr int RL = RP / 64;     // rows per lane
+  constexpr int SPW = TB / RNW;   // steps per wave per stage
+  static_assert(RL * 64 == RP && SPW * RNW == TB, "staging map");
+  const int row0 = lane * RL;
+  const bool vrow = row0 + RL <= R && R % RL == 0 &&
+                    (((uintptr_t)a | (uintptr_t)orow | (uintptr_t)ga) % (RL * sizeof(T))) == 0;
+  auto ld_rows = [&](const T* src, long off, float (&x)[RL]) {
+    if (vrow) {
+      ld_vec<T, RL>(src + off + row0, x);
+    } else {
+#pragma unroll
+      for (int i = 0; i < RL; ++i) {
+        const float y = to_f32(src[off + min(row0 + i, R - 1)]);
+        x[i] = row0 + i < R ? y : 0.f;
+      }
+    }
+  };
+  float pa[SPW][RL], po[SPW][RL], pg[SPW][RL], pb[SPW], pgc[SPW], pxd[SPW], py[SPW];
+  auto issue = [&](int b0) {
+    const int nb = min(TB, n - b0);
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+      const int s = w + k * RNW;   // wave-uniform
+      const bool in = s < nb;
+      const int gi = b0 + s - p.shift;
+      const bool gin = in && gi >= 0;
+      const int t = tok(min(b0 + s, n - 1)), tg = tok(max(min(gi, n - 1), 0));
+      const long ro = (long)t * rsR + (long)hh * R, rgo = (long)tg * rsR + (long)hh * R;
+      ld_rows(a, ro, pa[k]);
+      ld_rows(orow, ro, po[k]);
+      if (has_ga) ld_rows(ga, rgo, pg[k]);
+#pragma unroll
+      for (int i = 0; i < RL; ++i) {
+        pa[k][i] = in ? pa[k][i] : 0.f;
+        po[k][i] = in ? po[k][i] : 0.f;
+        pg[k][i] = (has_ga && gin) ? pg[k][i] : 0.f;   // log gate; 0 -> factor 1
+      }
+      const int c = cbase + lane;
+      const bool cin = in && lane < CB && c < C;
+      const long co = (long)t * rsC + (long)hh * C + min(c, C - 1);
+      const float xb = to_f32(b[co]);
+      pb[k] = cin ? xb : 0.f;
+      pgc[k] = 0.f;
+      if (has_gb) {
+        const float y = to_f32(gb[(long)tg * rsC + (long)hh * C + min(c, C - 1)]);
+        pgc[k] = (cin && gi >= 0) ? y : 0.f;
+      }
+      if (grad) {
+        const float xd = to_f32(gx[co]) * p.gxf[co], xy = to_f32(gy[co]);
+        pxd[k] = cin ? xd : 0.f;
+        py[k] = cin ? xy : 0.f;
+      }
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+      const int s = w + k * RNW;
+      float xa[RL], xo[RL], xg[RL];
+#pragma unroll
+      for (int i = 0; i < RL; ++i) {
+        xa[i] = p.sa * pa[k][i];
+        xo[i] = p.so * po[k][i];
+        xg[i] = has_ga ? gexp<T>(pg[k][i]) : 1.f;
+      }
+      st_vec<RL>(sA + s * RP + row0, xa);
+      st_vec<RL>(sOR + s * RP + row0, xo);
+      st_vec<RL>(sGR + s * RP + row0, xg);
+      if (lane < CB) {
+        sB[s * CB + lane] = pb[k];
+        sGC[s * CB + lane] = has_gb ? gexp<T>(pgc[k]) : 1.f;
+        if (grad) {
+          sXD[s * CB + lane] = pxd[k];
+          sY[s * CB + lane] = py[k];
+        }
+      }
+    }
+  };
+
+  if (n > 0) issue(0);
+  for (int b0 = 0; b0 < n; b0 += TB) {
+    const int nb = min(TB, n - b0);
+    __syncthreads();  // the previous stage's reads of the staged arrays and sO are done
+    commit();
+    __syncthreads();
+    if (b0 + TB < n) issue(b0 + TB);
+    // The column gate's presence is uniform: one copy of the step loop for each case.
+    // One step's LDS operands.
+    struct StepIn {
+      float a[RPT], g[RPT], o[RPT], b[4], gc[4];
+    };
+    auto load_step = [&](auto gac, auto gbc, int s, StepIn& in) {
+      constexpr bool GA = decltype(gac)::value, GB = decltype(gbc)::value;
+      const float4 bq = *reinterpret_cast<const float4*>(sB + s * CB + cg * 4);
+      in.b[0] = bq.x; in.b[1] = bq.y; in.b[2] = bq.z; in.b[3] = bq.w;
+      if (GB) {
+        const float4 gq = *reinterpret_cast<const float4*>(sGC + s * CB + cg * 4);
+        in.gc[0] = gq.x; in.gc[1] = gq.y; in.gc[2] = gq.z; in.gc[3] = gq.w;
+      }
+      const float* ra = sA + s * RP + r0;
+      const float* rgp = sGR + s * RP + r0;
+      const float* ro = sOR + s * RP + r0;
+      if (RPT == 2) {
+        const float2 a2 = *reinterpret_cast<const float2*>(ra);
+        const float2 g2 = GA ? *reinterpret_cast<const float2*>(rgp) : make_float2(1.f, 1.f);
+        const float2 o2 = *reinterpret_cast<const float2*>(ro);
+        in.a[0] = a2.x; in.a[1] = a2.y; in.g[0] = g2.x; in.g[1] = g2.y;
+        in.o[0] = o2.x; in.o[1] = o2.y;
+      } else {
+#pragma unroll
+        for (int j0 = 0; j0 < RPT; j0 += 4) {
+          const float4 a4 = *reinterpret_cast<const float4*>(ra + j0);
+          const float4 g4 = GA ? *reinterpret_cast<const float4*>(rgp + j0)
+                               : make_float4(1.f, 1.f, 1.f, 1.f);
+          const float4 o4 = *reinterpret_cast<const float4*>(ro + j0);
+          in.a[j0] = a4.x; in.a[j0 + 1] = a4.y; in.a[j0 + 2] = a4.z; in.a[j0 + 3] = a4.w;
+          in.g[j0] = g4.x; in.g[j0 + 1] = g4.y; in.g[j0 + 2] = g4.z; in.g[j0 + 3] = g4.w;
+          in.o[j0] = o4.x; in.o[j0 + 1] = o4.y; in.o[j0 + 2] = o4.z; in.o[j0 + 3] = o4.w;
+        }
+      }
+    };
+    auto step = [&](auto gac, auto gbc, int s, const StepIn& in) {
+      constexpr bool GA = decltype(gac)::value, GB = decltype(gbc)::value;
+      float x[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // in place (scale, then accumulate): no copies of the state registers
+          if (GA && GB)
+            S[j][i] *= in.g[j] * in.gc[i];
+          else if (GA)
+            S[j][i] *= in.g[j];
+          else if (GB)
+            S[j][i] *= in.gc[i];
+          S[j][i] = fmaf(in.a[j], in.b[i], S[j][i]);
+          x[i] = fmaf(in.o[j], S[j][i], x[i]);
+        }
+      const float cs = wave_colsum<NCG>(x);
+      if (lane_writes<NCG>(lane)) sO[(w * TB + s) * CB + lane_col<NCG>(lane)] = cs;
+    };
+    // Which gates exist is uniform: one copy of the step loop for each case.
+    auto steps = [&](auto gac, auto gbc) {
+#pragma unroll 1
+      for (int s = 0; s < nb; ++s) {
+        StepIn in;
+        load_step(gac, gbc, s, in);
+        step(gac, gbc, s, in);
+      }
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    if (has_ga && has_gb)
+      steps(yes(), yes());
+    else if (has_ga)
+      steps(yes(), no());
+    else if (has_gb)
+      steps(no(), yes());
+    else
+      steps(no(), no());
+    __syncthreads();
+    // Outputs: sum of the 8 waves' column sums, stored coalesced (columns fastest).
+#pragma unroll 1
+    for (int i = tid; i < TB * CB; i += RNT) {
+      const int s = i / CB, c = i % CB;
+      if (s < nb && cbase + c < C) {
+        float val = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < RNW; ++ww) val += sO[(ww * TB + s) * CB + c];
+        put<TO>(p.out, (long)tok(b0 + s) * rsC + (long)hh * C + cbase + c, val);
+        if (grad) sXD[i] -= sY[i] * val;   // this step's term of the gate gradient
+      } else if (grad) {
+        sXD[i] = 0.f;
+      }
+    }
+    if (grad) {
+      // Running sum in scan order (the gate gradient's suffix, or prefix, sum): 16 lanes
+      // per column scan the stage's 16 steps; the carry moves on to the next stage.
+      __syncthreads();
+      static_assert(TB == 16, "one 16-lane row per column and stage");
+#pragma unroll
+      for (int e = 0; e < CB * 16 / RNT; ++e) {
+        const int c = (tid >> 4) + e * (RNT / 16), s = tid & 15;
+        float d = sXD[s * CB + c];
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+          const float y = __shfl_up(d, o, 16);
+          if (s >= o) d += y;
+        }
+        sXD[s * CB + c] = run[e] + d + sCorr[c];
+        run[e] += __shfl(d, 15, 16);
+      }
+      __syncthreads();
+#pragma unroll 1
+      for (int i = tid; i < nb * CB; i += RNT) {
+        const int s = i / CB, c = i % CB;
+        if (cbase + c < C) p.dg[(long)tok(b0 + s) * rsC + (long)hh * C + cbase + c] = sXD[i];
+      }
+    }
+  }
+
+  if (p.sN) {
+    if (p.final_gate && n > 0) {
+      const int t = tok(n - 1);
+      float gcol[4], grow[RPT];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        gcol[i] = has_gb ? gexp<T>(to_f32(gb[(long)t * rsC + (long)hh * C + min(c0 + i, C - 1)]))
+                         : 1.f;
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+        grow[j] = has_ga ? gexp<T>(to_f32(ga[(long)t * rsR + (long)hh * R + min(r0 + j, R - 1)]))
+                         : 1.f;
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S[j][i] *= grow[j] * gcol[i];
+    }
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (ok(j, i)) p.sN[st_at(j, i)] = S[j][i];
+  }
+}
+
+namespace {
+
+template <typename T, typename TO, int NCG, int RPT>
+hipError_t launch_scan(const RecScanArgs& p, hipStream_t st) {
+  constexpr int CB = NCG * 4;
+  const long blocks = (long)p.si.N * p.H * ((p.C + CB - 1) / CB);
   if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL((recurrent_fwd_kernel<T, TO, KPT>), dim3((unsigned)blocks), dim3(256), 0,
+  hipLaunchKernelGGL((rec_scan_kernel<T, TO, NCG, RPT>), dim3((unsigned)blocks), dim3(RNT), 0,
                      st, p);
   return hipGetLastError();
 }
 
+// 64-column tiles (4 row groups per wave) when they give enough blocks to fill the chip;
+// 32-column tiles (8 row groups per wave, twice the blocks) otherwise and for more than 256
+// rows (at most 8 rows x 4 columns of state per thread).
 template <typename T, typename TO>
-static hipError_t dispatch_rec(const RecArgs& p, hipStream_t st) {
-  const int need = (p.K + 3) / 4;
-  if (need <= 4) return launch_rec<T, TO, 4>(p, st);
-  if (need <= 8) return launch_rec<T, TO, 8>(p, st);
-  if (need <= 16) return launch_rec<T, TO, 16>(p, st);
-  if (need <= 32) return launch_rec<T, TO, 32>(p, st);
-  if (need <= 64) return launch_rec<T, TO, 64>(p, st);
+hipError_t dispatch_scan(const RecScanArgs& p, hipStream_t st) {
+  const long blocks64 = (long)p.si.N * p.H * ((p.C + 63) / 64);
+  if (blocks64 >= 256 && p.C > 32 && p.R <= 256) {
+    if (p.R <= 64) return launch_scan<T, TO, 16, 2>(p, st);
+    if (p.R <= 128) return launch_scan<T, TO, 16, 4>(p, st);
+    return launch_scan<T, TO, 16, 8>(p, st);
+  }
+  if (p.R <= 128) return launch_scan<T, TO, 8, 2>(p, st);
+  if (p.R <= 256) return launch_scan<T, TO, 8, 4>(p, st);
+  if (p.R <= 512) return launch_scan<T, TO, 8, 8>(p, st);
   return hipErrorInvalidValue;
 }
 
-hipError_t run_recurrent_fwd(const RecArgs& p, int dtype, int o_dtype, hipStream_t st) {
-  if (dtype == DT_BF16 && o_dtype == DT_F32) return dispatch_rec<bf16, float>(p, st);
-  if (dtype == DT_BF16 && o_dtype == DT_BF16) return dispatch_rec<bf16, bf16>(p, st);
-  if (dtype == DT_F32 && o_dtype == DT_F32) return dispatch_rec<float, float>(p, st);
+hipError_t run_scan(const RecScanArgs& p, int dtype, int o_dtype, hipStream_t st) {
+  if (dtype == DT_BF16 && o_dtype == DT_F32) return dispatch_scan<bf16, float>(p, st);
+  if (dtype == DT_BF16 && o_dtype == DT_BF16) return dispatch_scan<bf16, bf16>(p, st);
+  if (dtype == DT_F32 && o_dtype == DT_F32) return dispatch_scan<float, float>(p, st);
   return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool recurrent_supported(int K, int V) { return K <= 512 && V <= 512; }
+
+hipError_t run_recurrent_fwd(const RecArgs& p, int dtype, int o_dtype, hipStream_t st) {
+  RecScanArgs s{};
+  s.H = p.H;
+  s.si = p.si;
+  s.a = p.k;
+  s.ga = p.gk;
+  s.o = p.q;
+  s.b = p.v;
+  s.gb = p.gv;
+  s.s0 = p.h0;
+  s.sN = p.ht;
+  s.out = p.o;
+  s.sa = 1.f;
+  s.so = p.scale;
+  s.R = p.K;
+  s.C = p.V;
+  s.dir = p.reverse ? 1 : 0;
+  return run_scan(s, dtype, o_dtype, st);
+}
+
+hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st) {
+  if (dtype != DT_BF16 && dtype != DT_F32) return hipErrorInvalidValue;
+  const bool need_ht = p.dht != nullptr && (p.gk != nullptr || p.gv != nullptr);
+  auto run = [&](const RecScanArgs& a) { return run_scan(a, dtype, DT_F32, st); };
+
+  // 1. dq (and h_T) : S = h^T, rows V, columns K, the forward's direction
+  RecScanArgs s{};
+  s.H = p.H;
+  s.si = p.si;
+  s.a = p.v;
+  s.ga = p.gv;
+  s.o = p.dout;
+  s.b = p.k;
+  s.gb = p.gk;
+  s.s0 = p.h0;
+  s.sN = need_ht ? p.ht_ws : nullptr;
+  s.s_trans = 1;
+  s.out = p.dq;
+  s.sa = 1.f;
+  s.so = p.scale;
+  s.R = p.V;
+  s.C = p.K;
+  s.dir = p.reverse ? 1 : 0;
+  hipError_t e = run(s);
+  if (e != hipSuccess) return e;
+
+  // 2. dk (+ dgk) : S = dh^T, rows V, columns K, opposite direction
+  RecScanArgs s2 = s;
+  s2.a = p.dout;
+  s2.o = p.v;
+  s2.b = p.q;
+  s2.s0 = p.dht;
+  s2.sN = nullptr;
+  s2.out = p.dk;
+  s2.sa = p.scale;
+  s2.so = 1.f;
+  s2.dir = p.reverse ? 0 : 1;
+  s2.shift = 1;
+  if (p.gk) {
+    s2.gx = p.q;
+    s2.gxf = p.dq;
+    s2.gy = p.k;
+    s2.hfin = need_ht ? p.ht_ws : nullptr;
+    s2.dg = p.dgk;
+  }
+  e = run(s2);
+  if (e != hipSuccess) return e;
+
+  // 3. dv (+ dgv, dh0) : S = dh, rows K, columns V, opposite direction
+  RecScanArgs s3{};
+  s3.H = p.H;
+  s3.si = p.si;
+  s3.a = p.q;
+  s3.ga = p.gk;
+  s3.o = p.k;
+  s3.b = p.dout;
+  s3.gb = p.gv;
+  s3.s0 = p.dht;
+  s3.sN = p.dh0;
+  s3.final_gate = 1;
+  s3.out = p.dv;
+  s3.sa = p.scale;
+  s3.so = 1.f;
+  s3.R = p.K;
+  s3.C = p.V;
+  s3.dir = p.reverse ? 0 : 1;
+  s3.shift = 1;
+  if (p.gv) {
+    s3.gx = p.dout;
+    s3.gxf = p.o;
+    s3.gy = p.v;
+    s3.hfin = need_ht ? p.ht_ws : nullptr;
+    s3.dg = p.dgv;
+  }
+  return run(s3);
 }
 
 }  // namespace tops

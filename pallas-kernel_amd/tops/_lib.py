@@ -47,6 +47,8 @@ _SIGS = {
                               _P, _I64, _I64, _I, _P],
     "tops_gla_fused_recurrent_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _F, _I, _I64, _I64, _I64,
                                      _I64, _I64, _P, _I64, _I, _I, _P],
+    "tops_gla_fused_recurrent_bwd": [_P] * 16 + [_F, _I, _I64, _I64, _I64, _I64, _I64, _P,
+                                                 _I64, _I, _P],
 }
 _SIGS["tops_gla_kernel_timing"] = [_I]
 _SIGS["tops_gla_kernel_ms"] = [_I]

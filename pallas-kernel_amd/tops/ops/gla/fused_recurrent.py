@@ -15,17 +15,28 @@ from ..._lib import SeqLayout, call, check_device, dtype_code, ptr, stream_of
 __all__ = ["fused_recurrent_gla", "fused_recurrent_gla_fwd", "fused_recurrent_gla_bwd"]
 
 
+def _out(B, T, H, D, dtype, dev, cu):
+    """Output buffer; tokens after the last sequence stay zero (reference :186-194)."""
+    if cu is not None and cu[-1] < T:
+        return torch.zeros(B, T, H, D, dtype=dtype, device=dev)
+    return torch.empty(B, T, H, D, dtype=dtype, device=dev)
+
+
+def _compute_dtype(*xs):
+    xs = [x for x in xs if x is not None]
+    return torch.bfloat16 if {x.dtype for x in xs} == {torch.bfloat16} else torch.float32
+
+
 def _run(q, k, v, gk, gv, scale, initial_state, output_final_state, reverse, cu_seqlens,
          out_dtype):
     B, T, H, K = q.shape
     V = v.shape[-1]
     dev = check_device(q, k, v, gk, gv, initial_state)
-    xs = [x for x in (q, k, v, gk, gv) if x is not None]
-    cdt = torch.bfloat16 if {x.dtype for x in xs} == {torch.bfloat16} else torch.float32
+    cdt = _compute_dtype(q, k, v, gk, gv)
     c = lambda x: None if x is None else x.to(cdt).contiguous()  # noqa: E731
     odt = torch.float32 if out_dtype == torch.float32 or cdt == torch.float32 else cdt
     seq = SeqLayout(B, T, 1, cu_seqlens, dev)
-    o = torch.empty(B, T, H, V, dtype=odt, device=dev)
+    o = _out(B, T, H, V, odt, dev, cu_seqlens)
     ht = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if output_final_state \
         else None
     h0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
@@ -61,19 +72,110 @@ def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state
                 torch.float32)
 
 
+class _FusedRecurrentGLAFunction(torch.autograd.Function):
+    """o, ht = fused_recurrent_gla(...); backward = ``fused_recurrent_gla_bwd``.
+
+    The reference defines no autodiff rule for ``fused_recurrent_gla``; its backward entry
+    point (``tops/ops/gla/fused_recurrent.py:879-956``) is what this rule calls.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, gk, gv, h0, scale, output_final_state, reverse, cu):
+        o, ht = _run(q, k, v, gk, gv, scale, h0, output_final_state, reverse, cu,
+                     torch.float32)
+        ctx.save_for_backward(q, k, v, gk, gv, h0, o if gv is not None else None)
+        ctx.meta = (scale, reverse, cu)
+        return o, ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        q, k, v, gk, gv, h0, o = ctx.saved_tensors
+        scale, reverse, cu = ctx.meta
+        if do is None:
+            do = torch.zeros(*v.shape, dtype=torch.float32, device=v.device)
+        dq, dk, dv, dgk, dgv, dh0 = _bwd(q, k, v, gk, gv, o, do, dht, scale, h0, reverse, cu)
+        cast = lambda g, x: None if g is None or x is None else g.to(x.dtype)  # noqa: E731
+        return (cast(dq, q), cast(dk, k), cast(dv, v), cast(dgk, gk), cast(dgv, gv),
+                cast(dh0, h0), None, None, None, None)
+
+
 def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=None,
                         output_final_state=False, reverse=False, cu_seqlens=None):
     """Fused recurrent GLA, public API. Reference: ``tops/ops/gla/fused_recurrent.py:438-481``.
+
+    Differentiable: gradients flow to q, k, v, gk, gv and initial_state through
+    ``fused_recurrent_gla_bwd``.
     """
-    return fused_recurrent_gla_fwd(q, k, v, gk=gk, gv=gv, scale=scale,
-                                   initial_state=initial_state,
-                                   output_final_state=output_final_state, reverse=reverse,
-                                   cu_seqlens=cu_seqlens)
+    if not torch.is_grad_enabled() or not any(
+            x is not None and x.requires_grad for x in (q, k, v, gk, gv, initial_state)):
+        return fused_recurrent_gla_fwd(q, k, v, gk=gk, gv=gv, scale=scale,
+                                       initial_state=initial_state,
+                                       output_final_state=output_final_state,
+                                       reverse=reverse, cu_seqlens=cu_seqlens)
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    cu = None if cu_seqlens is None else _lib.to_list(cu_seqlens)
+    N = len(cu) - 1 if cu is not None else B
+    assert tuple(k.shape) == (B, T, H, K), f"Expected k shape {(B, T, H, K)}, got {k.shape}"
+    assert tuple(v.shape) == (B, T, H, V), f"Expected v shape {(B, T, H, V)}, got {v.shape}"
+    assert (gk is None) or (tuple(gk.shape) == (B, T, H, K)), \
+        f"Expected gk shape {(B, T, H, K)}, got {gk.shape}"
+    assert (gv is None) or (tuple(gv.shape) == (B, T, H, V)), \
+        f"Expected gv shape {(B, T, H, V)}, got {gv.shape}"
+    assert (initial_state is None) or (tuple(initial_state.shape) == (N, H, K, V)), \
+        f"Expected initial_state shape {(N, H, K, V)}, got {initial_state.shape}"
+    assert (cu_seqlens is None) or (B == 1), \
+        f"Batch size must be 1 when using cu_seqlens, got {B}"
+    scale = scale if scale is not None else K ** -0.5
+    return _FusedRecurrentGLAFunction.apply(q, k, v, gk, gv, initial_state, float(scale),
+                                            bool(output_final_state), bool(reverse), cu)
+
+
+def _bwd(q, k, v, gk, gv, o, do, dht, scale, initial_state, reverse, cu):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    dev = check_device(q, k, v, gk, gv, o, do, dht, initial_state)
+    cdt = _compute_dtype(q, k, v, gk, gv, do)
+    c = lambda x: None if x is None else x.to(cdt).contiguous()  # noqa: E731
+    f = lambda x: None if x is None else x.to(torch.float32).contiguous()  # noqa: E731
+    seq = SeqLayout(B, T, 1, cu, dev)
+    dq = _out(B, T, H, K, torch.float32, dev, cu)
+    dk = _out(B, T, H, K, torch.float32, dev, cu)
+    dv = _out(B, T, H, V, torch.float32, dev, cu)
+    dgk = _out(B, T, H, K, torch.float32, dev, cu) if gk is not None else None
+    dgv = _out(B, T, H, V, torch.float32, dev, cu) if gv is not None else None
+    dh0 = (torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev)
+           if initial_state is not None else None)
+    need_ht = dht is not None and (gk is not None or gv is not None)
+    ht_ws = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if need_ht else None
+    call("tops_gla_fused_recurrent_bwd", ptr(c(q)), ptr(c(k)), ptr(c(v)), ptr(c(gk)),
+         ptr(c(gv)), ptr(f(o)), ptr(c(do)), ptr(f(dht)), ptr(f(initial_state)), ptr(dq),
+         ptr(dk), ptr(dv), ptr(dgk), ptr(dgv), ptr(dh0), ptr(ht_ws), float(scale),
+         int(bool(reverse)), B, T, H, K, V, ptr(seq.cu), seq.N, dtype_code(cdt),
+         stream_of(dev))
+    return dq, dk, dv, dgk, dgv, dh0
 
 
 def fused_recurrent_gla_bwd(q, k, v, gk=None, gv=None, o=None, do=None, dht=None, scale=None,
                             initial_state=None, reverse=False, cu_seqlens=None):
-    """Reference: ``tops/ops/gla/fused_recurrent.py:879-956``. Not yet on the HIP path."""
-    raise NotImplementedError(
-        "fused_recurrent_gla_bwd is not yet implemented on the HIP path; use chunk_gla's "
-        "backward (mathematically identical gradients)")
+    """Fused recurrent backward. Reference: ``tops/ops/gla/fused_recurrent.py:879-956``.
+
+    Returns ``(dq, dk, dv, dgk, dgv, dh0)``: float32 gradients (the reference's dtype), dgk /
+    dgv None without the matching gate, dh0 None without ``initial_state``. ``o`` (the
+    forward output) is required when ``gv`` is used.
+    """
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    cu = None if cu_seqlens is None else _lib.to_list(cu_seqlens)
+    N = len(cu) - 1 if cu is not None else B
+    scale = scale if scale is not None else K ** -0.5
+    assert tuple(k.shape) == (B, T, H, K)
+    assert tuple(v.shape) == (B, T, H, V)
+    assert do is not None and tuple(do.shape) == (B, T, H, V)
+    assert (gk is None) or (tuple(gk.shape) == (B, T, H, K))
+    assert (gv is None) or (tuple(gv.shape) == (B, T, H, V))
+    assert (initial_state is None) or (tuple(initial_state.shape) == (N, H, K, V))
+    assert (dht is None) or (tuple(dht.shape) == (N, H, K, V))
+    assert (cu_seqlens is None) or (B == 1)
+    assert gv is None or o is not None, "o (forward output) is required when gv is used"
+    return _bwd(q, k, v, gk, gv, o, do, dht, scale, initial_state, reverse, cu)

@@ -32,7 +32,7 @@ def _declared():
 
 def test_header_lists_entry_points():
     decl = _declared()
-    assert len(decl) == 14, decl
+    assert len(decl) == 15, decl
     assert set(decl) == set(_lib.EXPORTED)
 
 
@@ -95,8 +95,28 @@ def test_lds_budget_reported():
 
 def test_recurrent_rejects_large_k():
     rc, msg = _rc("tops_gla_fused_recurrent_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL,
-                  NULL, 1.0, 0, 1, 8, 1, 512, 64, NULL, 1, 1, 0, NULL)
-    assert rc == 2 and "K <= 256" in msg
+                  NULL, 1.0, 0, 1, 8, 1, 1024, 64, NULL, 1, 1, 0, NULL)
+    assert rc == 2 and "K <= 512" in msg
+
+
+def test_recurrent_bwd_validation():
+    args = lambda **kw: [kw.get(n, NULL) for n in (  # noqa: E731
+        "q", "k", "v", "gk", "gv", "o", "do", "dht", "h0", "dq", "dk", "dv", "dgk", "dgv",
+        "dh0", "ht")]
+    tail = lambda K, V: [1.0, 0, 1, 8, 1, K, V, NULL, 1, 1, NULL]  # noqa: E731
+    rc, msg = _rc("tops_gla_fused_recurrent_bwd", *args(), *tail(1024, 64))
+    assert rc == 2 and "K, V <= 512" in msg
+    buf = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    full = dict(q=buf, k=buf, v=buf, do=buf, dq=buf, dk=buf, dv=buf)
+    rc, msg = _rc("tops_gla_fused_recurrent_bwd", *args(**full, gk=buf), *tail(64, 64))
+    assert rc == 1 and "dgk must be given" in msg
+    rc, msg = _rc("tops_gla_fused_recurrent_bwd", *args(**full, gv=buf, dgv=buf), *tail(64, 64))
+    assert rc == 1 and "o (forward output) is required" in msg
+    rc, msg = _rc("tops_gla_fused_recurrent_bwd", *args(**full, gk=buf, dgk=buf, dht=buf),
+                  *tail(64, 64))
+    assert rc == 1 and "ht_ws is required" in msg
+    rc, msg = _rc("tops_gla_fused_recurrent_bwd", *args(q=buf), *tail(64, 64))
+    assert rc == 1 and "must not be NULL" in msg
 
 
 def test_cumsum_rejects_non_power_of_two():
