@@ -147,9 +147,10 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
  * Per-chunk dq, dk, dg of the backward (intra-chunk dA computed in-kernel) from the forward
  * states h and the state gradients dh (both [NC, H, K, V], dtype, as produced by
  * tops_gla_chunk_fwd_h / tops_gla_chunk_bwd_dh on raw gates g).
- * Replaces: chunk_gla_bwd_dA_ref + chunk_gla_bwd_dqk_intra_ref + chunk_gla_bwd_dqkg_ref,
- *           tops/ops/gla/chunk.py:504-539, :603-648, :656-743 (the dq/dk/dg part of
- *           chunk_gla_bwd_fused_kernel, :1423-1479).
+ * Replaces: the dq/dk/dg part of chunk_gla_bwd_fused_kernel, tops/ops/gla/chunk.py:1423-1479
+ *           (launch :1482-1550), i.e. the composition of chunk_gla_bwd_dA_ref,
+ *           chunk_gla_bwd_dqk_intra_ref and chunk_gla_bwd_dqkg_ref (:504-539, :603-743) in one
+ *           pass; tops_gla_bwd_part_* below replace those three one by one.
  */
 int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const void* g,
                             const void* h, const void* dout, const void* dh, void* dq, void* dk,
@@ -160,14 +161,39 @@ int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const v
 
 /*
  * Per-chunk dv = tril(A)^T do + (k e^{gamma - g~}) dh (A recomputed in-kernel).
- * Replaces: chunk_gla_bwd_dv_ref, tops/ops/gla/chunk.py:547-595 (the dv part of
- *           chunk_gla_bwd_fused_kernel, :1423-1479).
+ * Replaces: the dv part of chunk_gla_bwd_fused_kernel, tops/ops/gla/chunk.py:1423-1479
+ *           (chunk_gla_bwd_dv_ref :547-595 on an in-kernel A; tops_gla_bwd_part_dv takes A).
  */
 int tops_gla_chunk_bwd_dv(const void* q, const void* k, const void* g, const void* dout,
                           const void* dh, void* dv, float scale, int64_t B, int64_t T,
                           int64_t H, int64_t K, int64_t V, int chunk_size,
                           const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
                           int64_t NC, int dtype, void* stream);
+
+/*
+ * The backward's four per-chunk parts over given intermediates, for callers that hold them
+ * (the fused entry points above recompute A and dA in-kernel instead). All tensors float32,
+ * [B, T, H, *] with T a multiple of chunk_size (16, 32 or 64); A and dA [B, T, H, C];
+ * h / dh [B * T / C, H, K, V]; g_cumsum is the chunk-local cumsum of the gates.
+ * Replace the reference's jnp functions:
+ *   tops_gla_bwd_part_dA         chunk_gla_bwd_dA_ref          tops/ops/gla/chunk.py:504-539
+ *   tops_gla_bwd_part_dv         chunk_gla_bwd_dv_ref          tops/ops/gla/chunk.py:547-595
+ *   tops_gla_bwd_part_dqk_intra  chunk_gla_bwd_dqk_intra_ref   tops/ops/gla/chunk.py:603-648
+ *   tops_gla_bwd_part_dqkg       chunk_gla_bwd_dqkg_ref        tops/ops/gla/chunk.py:656-743
+ */
+int tops_gla_bwd_part_dA(const float* v, const float* dout, float* dA, float scale, int64_t B,
+                         int64_t T, int64_t H, int64_t V, int chunk_size, void* stream);
+int tops_gla_bwd_part_dv(const float* k, const float* g_cumsum, const float* A,
+                         const float* dout, const float* dh, float* dv, int64_t B, int64_t T,
+                         int64_t H, int64_t K, int64_t V, int chunk_size, void* stream);
+int tops_gla_bwd_part_dqk_intra(const float* q, const float* k, const float* g_cumsum,
+                                const float* dA, float* dq, float* dk, int64_t B, int64_t T,
+                                int64_t H, int64_t K, int chunk_size, void* stream);
+int tops_gla_bwd_part_dqkg(const float* q, const float* k, const float* v, const float* h,
+                           const float* g_cumsum, const float* dout, const float* dh,
+                           const float* dq, const float* dk, float* dq_out, float* dk_out,
+                           float* dg, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
+                           int64_t V, int chunk_size, void* stream);
 
 /*
  * Fused recurrent forward. gk [B, T, H, K] / gv [B, T, H, V] gates may be NULL; o is

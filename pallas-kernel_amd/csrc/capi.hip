@@ -674,6 +674,107 @@ int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, co
                     "fused_recurrent_fwd");
 }
 
+namespace {
+
+int part_shape(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int C,
+               std::initializer_list<const void*> ptrs, tops::PartArgs* p) {
+  if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0)
+    return fail(TOPS_GLA_EINVAL, "bad shape (B=%lld T=%lld H=%lld K=%lld V=%lld)",
+                (long long)B, (long long)T, (long long)H, (long long)K, (long long)V);
+  if (C != 16 && C != 32 && C != 64)
+    return fail(TOPS_GLA_EUNSUPPORTED, "chunk_size %d (these kernels take 16, 32, 64)", C);
+  if (T % C != 0)
+    return fail(TOPS_GLA_EINVAL, "T (%lld) must be a multiple of chunk_size (%d)", (long long)T,
+                C);
+  if (B * T * H * std::max(K, std::max(V, (int64_t)C)) > (int64_t)1 << 40)
+    return fail(TOPS_GLA_EUNSUPPORTED, "problem too large");
+  if (B * T > 0)
+    for (const void* q : ptrs)
+      if (q == nullptr) return fail(TOPS_GLA_EINVAL, "NULL buffer");
+  *p = tops::PartArgs{};
+  p->H = (int)H;
+  p->K = (int)K;
+  p->V = (int)V;
+  p->NC = (long)(B * (T / C));
+  if (p->NC * H * ((std::max(K, V) + 63) / 64) > kMaxInt)
+    return fail(TOPS_GLA_EUNSUPPORTED, "grid too large");
+  return TOPS_GLA_OK;
+}
+
+}  // namespace
+
+int tops_gla_bwd_part_dA(const float* v, const float* dout, float* dA, float scale, int64_t B,
+                         int64_t T, int64_t H, int64_t V, int chunk_size, void* stream) {
+  tops::PartArgs p;
+  int rc = part_shape(B, T, H, 1, V, chunk_size, {v, dout, dA}, &p);
+  if (rc) return rc;
+  p.v = v;
+  p.dout = dout;
+  p.out0 = dA;
+  p.scale = scale;
+  return hip_status(tops::run_bwd_part(tops::PART_DA, p, chunk_size, (hipStream_t)stream),
+                    "bwd_part_dA");
+}
+
+int tops_gla_bwd_part_dv(const float* k, const float* g_cumsum, const float* A,
+                         const float* dout, const float* dh, float* dv, int64_t B, int64_t T,
+                         int64_t H, int64_t K, int64_t V, int chunk_size, void* stream) {
+  tops::PartArgs p;
+  int rc = part_shape(B, T, H, K, V, chunk_size, {k, g_cumsum, A, dout, dh, dv}, &p);
+  if (rc) return rc;
+  p.k = k;
+  p.g = g_cumsum;
+  p.A = A;
+  p.dout = dout;
+  p.dh = dh;
+  p.out0 = dv;
+  return hip_status(tops::run_bwd_part(tops::PART_DV, p, chunk_size, (hipStream_t)stream),
+                    "bwd_part_dv");
+}
+
+int tops_gla_bwd_part_dqk_intra(const float* q, const float* k, const float* g_cumsum,
+                                const float* dA, float* dq, float* dk, int64_t B, int64_t T,
+                                int64_t H, int64_t K, int chunk_size, void* stream) {
+  tops::PartArgs p;
+  int rc = part_shape(B, T, H, K, 1, chunk_size, {q, k, g_cumsum, dA, dq, dk}, &p);
+  if (rc) return rc;
+  p.q = q;
+  p.k = k;
+  p.g = g_cumsum;
+  p.dA = dA;
+  p.out0 = dq;
+  p.out1 = dk;
+  return hip_status(
+      tops::run_bwd_part(tops::PART_DQK_INTRA, p, chunk_size, (hipStream_t)stream),
+      "bwd_part_dqk_intra");
+}
+
+int tops_gla_bwd_part_dqkg(const float* q, const float* k, const float* v, const float* h,
+                           const float* g_cumsum, const float* dout, const float* dh,
+                           const float* dq, const float* dk, float* dq_out, float* dk_out,
+                           float* dg, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
+                           int64_t V, int chunk_size, void* stream) {
+  tops::PartArgs p;
+  int rc = part_shape(B, T, H, K, V, chunk_size,
+                      {q, k, v, h, g_cumsum, dout, dh, dq, dk, dq_out, dk_out, dg}, &p);
+  if (rc) return rc;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.h = h;
+  p.g = g_cumsum;
+  p.dout = dout;
+  p.dh = dh;
+  p.dq = dq;
+  p.dk = dk;
+  p.out0 = dq_out;
+  p.out1 = dk_out;
+  p.out2 = dg;
+  p.scale = scale;
+  return hip_status(tops::run_bwd_part(tops::PART_DQKG, p, chunk_size, (hipStream_t)stream),
+                    "bwd_part_dqkg");
+}
+
 int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v, const void* gk,
                                  const void* gv, const float* o, const void* dout,
                                  const float* dht, const float* h0, float* dq, float* dk,

@@ -128,6 +128,17 @@ struct RecBwdArgs {
   int reverse;
   SeqInfo si;
 };
+// The backward's per-chunk parts over given intermediates (chunk_bwd_parts.hip), float32.
+enum { PART_DA = 0, PART_DV = 1, PART_DQK_INTRA = 2, PART_DQKG = 3 };
+struct PartArgs {
+  const float *q, *k, *v, *g, *A, *dA, *dout, *h, *dh, *dq, *dk;  // as each part needs
+  float *out0, *out1, *out2;
+  float scale;
+  int H, K, V;
+  long NC;  // chunks (B * T / C)
+};
+hipError_t run_bwd_part(int which, const PartArgs& p, int C, hipStream_t st);
+
 bool recurrent_supported(int K, int V);  // state rows K (forward) and V, K (backward)
 hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st);
 

@@ -49,6 +49,10 @@ _SIGS = {
                                      _I64, _I64, _P, _I64, _I, _I, _P],
     "tops_gla_fused_recurrent_bwd": [_P] * 16 + [_F, _I, _I64, _I64, _I64, _I64, _I64, _P,
                                                  _I64, _I, _P],
+    "tops_gla_bwd_part_dA": [_P, _P, _P, _F, _I64, _I64, _I64, _I64, _I, _P],
+    "tops_gla_bwd_part_dv": [_P] * 6 + [_I64] * 5 + [_I, _P],
+    "tops_gla_bwd_part_dqk_intra": [_P] * 6 + [_I64] * 4 + [_I, _P],
+    "tops_gla_bwd_part_dqkg": [_P] * 12 + [_F] + [_I64] * 5 + [_I, _P],
 }
 _SIGS["tops_gla_kernel_timing"] = [_I]
 _SIGS["tops_gla_kernel_ms"] = [_I]

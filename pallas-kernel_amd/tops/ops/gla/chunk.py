@@ -445,16 +445,78 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
 chunk_gla_bwd_with_pl = chunk_gla_bwd
 
 
-def _unsupported(name):
-    def f(*args, **kwargs):
-        raise NotImplementedError(
-            f"{name}: this jnp helper of the reference backward is not yet on the HIP path; "
-            "chunk_gla_bwd computes the same quantities fused")
-    f.__name__ = name
-    return f
+# ---------------------------------------------------------------------------
+# the backward's per-chunk parts over given intermediates (reference jnp exports)
+# ---------------------------------------------------------------------------
 
 
-chunk_gla_bwd_dA_ref = _unsupported("chunk_gla_bwd_dA_ref")
-chunk_gla_bwd_dv_ref = _unsupported("chunk_gla_bwd_dv_ref")
-chunk_gla_bwd_dqk_intra_ref = _unsupported("chunk_gla_bwd_dqk_intra_ref")
-chunk_gla_bwd_dqkg_ref = _unsupported("chunk_gla_bwd_dqkg_ref")
+def _parts_prep(C, T, *xs):
+    """float32 contiguous copies; result dtype = the inputs' promoted dtype (jnp's rule)."""
+    assert T % C == 0, f"T ({T}) must be a multiple of chunk_size ({C})"
+    dev = check_device(*xs)
+    rdt = xs[0].dtype
+    for x in xs[1:]:
+        rdt = torch.promote_types(rdt, x.dtype)
+    return dev, rdt, [x.to(torch.float32).contiguous() for x in xs]
+
+
+def chunk_gla_bwd_dA_ref(v, do, scale, cu_seqlens_cpu=None, chunk_size=64):
+    """``dA = scale tril(do v^T)`` per chunk, ``[B, T, H, C]``. Reference:
+    ``tops/ops/gla/chunk.py:504-539`` (which, like this, groups tokens as B * T / C chunks
+    and does not read ``cu_seqlens_cpu``)."""
+    del cu_seqlens_cpu
+    B, T, H, V = v.shape
+    C = chunk_size
+    dev, rdt, (vf, dof) = _parts_prep(C, T, v, do)
+    dA = torch.empty(B, T, H, C, dtype=torch.float32, device=dev)
+    call("tops_gla_bwd_part_dA", ptr(vf), ptr(dof), ptr(dA), float(scale), B, T, H, V, C,
+         stream_of(dev))
+    return dA.to(rdt)
+
+
+def chunk_gla_bwd_dv_ref(k, g_cumsum, A, do, dh, cu_seqlens_cpu=None, chunk_size=64):
+    """``dv = tril(A)^T do + (k e^{gn - g~}) dh``. Reference: ``tops/ops/gla/chunk.py:547-595``.
+    ``dh`` is ``[B, NT, H, K, V]`` (or ``[B * NT, H, K, V]``)."""
+    del cu_seqlens_cpu
+    B, T, H, K = k.shape
+    V = do.shape[-1]
+    C = chunk_size
+    dev, rdt, (kf, gf, Af, dof, dhf) = _parts_prep(C, T, k, g_cumsum, A, do, dh)
+    dv = torch.empty(B, T, H, V, dtype=torch.float32, device=dev)
+    call("tops_gla_bwd_part_dv", ptr(kf), ptr(gf), ptr(Af), ptr(dof), ptr(dhf), ptr(dv), B, T,
+         H, K, V, C, stream_of(dev))
+    return dv.to(rdt)
+
+
+def chunk_gla_bwd_dqk_intra_ref(q, k, g_cumsum, dA, cu_seqlens_cpu=None, chunk_size=64):
+    """Intra-chunk ``dq = e^{g~} (dA (k e^{-g~}))``, ``dk = e^{-g~} (dA^T (q e^{g~}))``.
+    Reference: ``tops/ops/gla/chunk.py:603-648``."""
+    del cu_seqlens_cpu
+    B, T, H, K = q.shape
+    C = chunk_size
+    dev, rdt, (qf, kf, gf, dAf) = _parts_prep(C, T, q, k, g_cumsum, dA)
+    dq = torch.empty(B, T, H, K, dtype=torch.float32, device=dev)
+    dk = torch.empty_like(dq)
+    call("tops_gla_bwd_part_dqk_intra", ptr(qf), ptr(kf), ptr(gf), ptr(dAf), ptr(dq), ptr(dk),
+         B, T, H, K, C, stream_of(dev))
+    return dq.to(rdt), dk.to(rdt)
+
+
+def chunk_gla_bwd_dqkg_ref(q, k, v, h, g_cumsum, do, dh, dq, dk, scale, cu_seqlens_cpu=None,
+                           chunk_size=64):
+    """Inter-chunk dq, dk added to the given intra ones, and the gate gradient
+    ``dg = revcumsum_chunk(q dq - k dk) + e^{gn} sum_v h dh + sum_c dk_inter k``.
+    Reference: ``tops/ops/gla/chunk.py:656-743``. Returns ``(dq, dk, dg)``."""
+    del cu_seqlens_cpu
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    C = chunk_size
+    dev, rdt, xs = _parts_prep(C, T, q, k, v, h, g_cumsum, do, dh, dq, dk)
+    qf, kf, vf, hf, gf, dof, dhf, dqf, dkf = xs
+    dq_out = torch.empty(B, T, H, K, dtype=torch.float32, device=dev)
+    dk_out = torch.empty_like(dq_out)
+    dg = torch.empty_like(dq_out)
+    call("tops_gla_bwd_part_dqkg", ptr(qf), ptr(kf), ptr(vf), ptr(hf), ptr(gf), ptr(dof),
+         ptr(dhf), ptr(dqf), ptr(dkf), ptr(dq_out), ptr(dk_out), ptr(dg), float(scale), B, T, H,
+         K, V, C, stream_of(dev))
+    return dq_out.to(rdt), dk_out.to(rdt), dg.to(rdt)

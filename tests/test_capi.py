@@ -32,7 +32,7 @@ def _declared():
 
 def test_header_lists_entry_points():
     decl = _declared()
-    assert len(decl) == 15, decl
+    assert len(decl) == 19, decl
     assert set(decl) == set(_lib.EXPORTED)
 
 

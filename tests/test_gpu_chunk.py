@@ -359,3 +359,156 @@ def test_segmented_scans_match_sequential():
     names = ["o", "ht", "h", "dq", "dk", "dv", "dg", "dh0"]
     for name, a, b in zip(names, *outs):
         check(name, to_np(b), to_np(a).astype(np.float64), "bf16")
+
+
+# The backward's parts over given intermediates (reference jnp exports chunk.py:504-743).
+PART_CASES = [
+    dict(B=2, T=64, H=2, K=32, V=64, C=16, seed=901),
+    dict(B=1, T=128, H=3, K=96, V=40, C=32, seed=902),
+    dict(B=1, T=128, H=2, K=130, V=70, C=64, seed=903),
+    dict(B=2, T=64, H=1, K=256, V=512, C=64, seed=904),
+]
+
+
+@pytest.mark.parametrize("cfg", PART_CASES,
+                         ids=[f"B{c['B']}T{c['T']}H{c['H']}K{c['K']}V{c['V']}C{c['C']}"
+                              for c in PART_CASES])
+def test_bwd_parts(cfg):
+    G = _gla()
+    B, T, H, K, V, C = (cfg[x] for x in ("B", "T", "H", "K", "V", "C"))
+    r = np.random.default_rng(cfg["seed"])
+    q, k = r.standard_normal((2, B, T, H, K))
+    v, do = r.standard_normal((2, B, T, H, V))
+    g = -np.logaddexp(0.0, -r.standard_normal((B, T, H, K)))   # logsigmoid
+    gc = orc.chunk_local_cumsum(g, C)
+    A = r.standard_normal((B, T, H, C))
+    dA = np.tril(r.standard_normal((B, T // C, C, H, C)).transpose(0, 1, 3, 2, 4)) \
+        .transpose(0, 1, 3, 2, 4).reshape(B, T, H, C)
+    h, dh = r.standard_normal((2, B, T // C, H, K, V)) * 0.5
+    dq0, dk0 = r.standard_normal((2, B, T, H, K))
+    scale = K ** -0.5
+    d = lambda x: to_dev(x, "f32")  # noqa: E731
+    tol = lambda ref: 1e-4 * max(1.0, float(np.abs(ref).max()))  # noqa: E731
+
+    got = G.chunk_gla_bwd_dA_ref(d(v), d(do), scale, chunk_size=C)
+    ref = orc.chunk_gla_bwd_dA(v, do, scale, C)
+    check("dA", to_np(got), ref, "f32", atol=tol(ref))
+
+    got = G.chunk_gla_bwd_dv_ref(d(k), d(gc), d(A), d(do), d(h), chunk_size=C)
+    ref = orc.chunk_gla_bwd_dv(k, gc, A, do, h, C)
+    check("dv", to_np(got), ref, "f32", atol=tol(ref))
+
+    gq, gk = G.chunk_gla_bwd_dqk_intra_ref(d(q), d(k), d(gc), d(dA), chunk_size=C)
+    rq, rk = orc.chunk_gla_bwd_dqk_intra(q, k, gc, dA, C)
+    check("dq_intra", to_np(gq), rq, "f32", atol=tol(rq))
+    check("dk_intra", to_np(gk), rk, "f32", atol=tol(rk))
+
+    out = G.chunk_gla_bwd_dqkg_ref(d(q), d(k), d(v), d(h), d(gc), d(do), d(dh), d(dq0),
+                                   d(dk0), scale, chunk_size=C)
+    ref = orc.chunk_gla_bwd_dqkg(q, k, v, h, gc, do, dh, dq0, dk0, scale, C)
+    for name, a, b in zip(("dq", "dk", "dg"), out, ref):
+        check(name, to_np(a), b, "f32", atol=tol(b))
+
+
+def test_bwd_parts_compose_to_the_fused_backward():
+    """dA -> dqk_intra -> dqkg and dv from the forward's A, h and the backward's dh give the
+    fused backward's gradients (reference chunk_gla_bwd, chunk.py:815-977)."""
+    G = _gla()
+    B, T, H, K, V, C = 1, 128, 2, 32, 48, 32
+    q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, 905, h0=True, dht=True)
+    d = lambda x: to_dev(x, "f32")  # noqa: E731
+    scale = K ** -0.5
+    gc, A, h, _, _ = G.chunk_gla_fwd(d(q), d(k), d(v), d(g), None, None, scale,
+                                      to_dev(s0, "state"), True, chunk_size=C)
+    from tops.ops.common.chunk_h import chunk_bwd_dh_ref
+
+    dh, _ = chunk_bwd_dh_ref(d(q), None, None, gc, d(do), h0=to_dev(s0, "state"),
+                             dht=to_dev(dht, "state"), scale=scale, chunk_size=C)
+    dA = G.chunk_gla_bwd_dA_ref(d(v), d(do), scale, chunk_size=C)
+    dv = G.chunk_gla_bwd_dv_ref(d(k), gc, A, d(do), dh, chunk_size=C)
+    dq, dk = G.chunk_gla_bwd_dqk_intra_ref(d(q), d(k), gc, dA, chunk_size=C)
+    dq, dk, dg = G.chunk_gla_bwd_dqkg_ref(d(q), d(k), d(v), h, gc, d(do), dh, dq, dk, scale,
+                                          chunk_size=C)
+    ref = orc.chunk_gla_bwd(q, k, v, g, None, None, scale, s0, None, None, do, dht,
+                            chunk_size=C)
+    for name, a, b in zip(("dq", "dk", "dv", "dg"), (dq, dk, dv, dg), ref):
+        check(name, to_np(a), b, "f32", atol=1e-4 * max(1.0, float(np.abs(b).max())))
+
+
+# tops.ops.common.chunk_h (reference tops/ops/common/chunk_h.py:137-697): state scans with
+# gk / scalar g / g_gamma gates, chunk sizes above 64 (run as 64-row chunks), split_size.
+CH_CASES = [
+    dict(B=2, T=128, H=2, K=32, V=64, C=64, gate="gk", seed=911),
+    dict(B=1, T=96, H=3, K=64, V=48, C=32, gate="g", seed=912),
+    dict(B=2, T=64, H=2, K=32, V=32, C=16, gate="g_gamma", seed=913),
+    dict(B=1, T=256, H=2, K=64, V=64, C=128, gate="gk", seed=914),
+    dict(B=1, T=256, H=2, K=32, V=64, C=64, S=128, gate="gk", seed=915),
+    dict(B=1, T=192, H=2, K=32, V=64, C=64, gate="gk", seed=916, cu=[0, 64, 192]),
+    dict(B=1, T=256, H=1, K=128, V=128, C=128, S=256, gate="g_gamma", seed=917),
+]
+
+
+def _ch_inputs(cfg):
+    B, T, H, K, V, C = (cfg[x] for x in ("B", "T", "H", "K", "V", "C"))
+    r = np.random.default_rng(cfg["seed"])
+    q, k = r.standard_normal((2, B, T, H, K))
+    v, do = r.standard_normal((2, B, T, H, V))
+    cu = cfg.get("cu")
+    N = len(cu) - 1 if cu else B
+    h0, dht = r.standard_normal((2, N, H, K, V))
+    gate = cfg["gate"]
+    kw, gfull = {}, None
+    if gate == "gk":
+        gfull = orc.chunk_local_cumsum(-np.logaddexp(0.0, -r.standard_normal((B, T, H, K))) / 4,
+                                       C, cu_seqlens=cu)
+        kw["gk"] = gfull
+    elif gate == "g":
+        gs = orc.chunk_local_cumsum(-np.logaddexp(0.0, -r.standard_normal((B, T, H, 1))) / 4,
+                                    C, cu_seqlens=cu)[..., 0]
+        kw["g"] = gs
+        gfull = np.repeat(gs[..., None], K, axis=-1)
+    else:
+        gg = -np.abs(r.standard_normal(H)) / 8
+        kw["g_gamma"] = gg
+        bounds = cu if cu else [0, T]
+        pos = np.concatenate([np.arange(b - a) % C + 1 for a, b in zip(bounds, bounds[1:])])
+        gfull = np.broadcast_to(pos[None, :, None, None] * gg[None, None, :, None],
+                                (B, T, H, K)).copy()
+    return q, k, v, do, h0, dht, kw, gfull, cu
+
+
+@pytest.mark.parametrize("cfg", CH_CASES, ids=[f"{c['gate']}-C{c['C']}-S{c.get('S', c['C'])}"
+                                               f"{'-varlen' if c.get('cu') else ''}"
+                                               for c in CH_CASES])
+def test_common_chunk_h(cfg):
+    from tops.ops.common import chunk_h as CH
+
+    C = cfg["C"]
+    S = cfg.get("S", C)
+    q, k, v, do, h0, dht, kw, gfull, cu = _ch_inputs(cfg)
+    d = lambda x: to_dev(x, "f32")  # noqa: E731
+    dkw = {name: d(x) for name, x in kw.items()}
+    cut = None if cu is None else torch.tensor(cu)
+    tol = lambda ref: 1e-4 * max(1.0, float(np.abs(ref).max()))  # noqa: E731
+
+    h_ref, ht_ref = orc.chunk_fwd_h(k, v, gfull, h0, True, cu_seqlens=cu, chunk_size=C)
+    h, ht = CH.chunk_fwd_h_kernel(d(k), d(v), h0=d(h0), output_final_state=True,
+                                  cu_seqlens=cut, chunk_size=C, split_size=S, **dkw)
+    check("h", to_np(h), h_ref[:, ::S // C], "f32", atol=tol(h_ref))
+    check("ht", to_np(ht), ht_ref, "f32", atol=tol(ht_ref))
+    if S == C and "gk" in kw:
+        h2, ht2 = CH.chunk_fwd_h_ref(d(k), d(v), gk=dkw["gk"], h0=d(h0), output_final_state=True,
+                                     cu_seqlens_cpu=cu, chunk_size=C)
+        check("h_ref", to_np(h2), h_ref, "f32", atol=tol(h_ref))
+
+    dh_ref, dh0_ref = orc.chunk_bwd_dh(q, gfull, do, h0, dht, 0.5, cu_seqlens=cu, chunk_size=C)
+    dh, dh0 = CH.chunk_bwd_dh_kernel(d(q), d(k), d(v), do=d(do), dht=d(dht), scale=0.5,
+                                     output_dh0=True, cu_seqlens=cut, chunk_size=C,
+                                     split_size=S, **dkw)
+    check("dh", to_np(dh), dh_ref[:, ::S // C], "f32", atol=tol(dh_ref))
+    check("dh0", to_np(dh0), dh0_ref, "f32", atol=tol(dh0_ref))
+    if S == C and "gk" in kw:
+        dh2, dh02 = CH.chunk_bwd_dh_ref(d(q), d(k), d(v), dkw["gk"], d(do), h0=d(h0), dht=d(dht),
+                                        scale=0.5, cu_seqlens_cpu=cu, chunk_size=C)
+        check("dh_ref", to_np(dh2), dh_ref, "f32", atol=tol(dh_ref))
+        check("dh0_ref", to_np(dh02), dh0_ref, "f32", atol=tol(dh0_ref))
