@@ -116,9 +116,18 @@ int64_t tops_gla_chunk_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int6
                                 int chunk_size, int varlen, int dtype);
 
 /*
- * chunk_gla forward: inter-chunk states into h_ws ([NC, H, K, V], dtype, required: it is
- * the residual the backward reuses) and the per-chunk output. h0/ht may be NULL. seg_ws
- * (256-byte aligned, seg_ws_bytes >= tops_gla_chunk_ws_bytes) may be NULL.
+ * 1 when the full-head kernels run this shape (16-byte aligned buffers assumed): the
+ * forward and the scans (backward = 0), or also the fused backward (backward = 1). On those
+ * paths tops_gla_chunk_fwd's h_ws may be NULL (no states kept) and tops_gla_chunk_bwd's
+ * dh_ws is not used (may be NULL). No counterpart in the reference (workspace sizing).
+ */
+int tops_gla_full_head(int64_t K, int64_t V, int chunk_size, int dtype, int backward);
+
+/*
+ * chunk_gla forward: inter-chunk states into h_ws ([NC, H, K, V], dtype: the residual the
+ * backward reuses) and the per-chunk output. h_ws may be NULL on the full-head path (then
+ * no states are stored); the other paths need it. h0/ht may be NULL. seg_ws (256-byte
+ * aligned, seg_ws_bytes >= tops_gla_chunk_ws_bytes) may be NULL.
  * Replaces the device part of chunk_gla_fwd, tops/ops/gla/chunk.py:1145-1166.
  */
 int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* g,
@@ -131,7 +140,8 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
 /*
  * chunk_gla backward: (dq, dk, dv, dg, dh0). `h` are the forward states ([NC, H, K, V]); if
  * NULL they are recomputed into h_ws (then required). dh_ws ([NC, H, K, V], dtype) is
- * required. h0, dht and dh0 may be NULL; seg_ws as for tops_gla_chunk_fwd.
+ * required off the fused full-head backward (tops_gla_full_head(..., 1)), which does not use
+ * it. h0, dht and dh0 may be NULL; seg_ws as for tops_gla_chunk_fwd.
  * Replaces the device part of chunk_gla_bwd_with_pl, tops/ops/gla/chunk.py:1019-1064
  * (chunk_bwd_dh_kernel + chunk_gla_bwd_fused_pl, :1482-1550).
  */

@@ -120,7 +120,8 @@ bool use_head(int dtype, int chunk, int64_t K, int64_t V, bool g_is_cumsum,
 // (state part first, then the decays); otherwise NS = 1.
 void seg_setup(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void* ws,
                int64_t ws_bytes, int& NS, int& SL, float*& st, float*& gm) {
-  tops::head_seg_plan(si.N, (int)H, si.T, si.C, si.cu != nullptr, NS, SL);
+  tops::head_seg_plan(si.N, (int)H, si.T, si.C, si.cu != nullptr, NS, SL,
+                      tops::head_vtiles((int)K, (int)V));
   const long need = tops::head_seg_ws_bytes(si.N, NS, (int)H, (int)K, (int)V);
   st = gm = nullptr;
   if (NS <= 1 || ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 255u) != 0) {
@@ -179,12 +180,19 @@ const char* tops_gla_last_error(void) { return g_err; }
 
 const char* tops_gla_version(void) { return "tops-gla-mi355x 0.1.0 (gfx950)"; }
 
+int tops_gla_full_head(int64_t K, int64_t V, int chunk_size, int dtype, int backward) {
+  if (K <= 0 || V <= 0 || K > 4096 || V > (1 << 20)) return 0;
+  if (!tops::head_supported(dtype, chunk_size, (int)K, (int)V, false)) return 0;
+  return backward ? (int)tops::head_bwd_supported((int)K, (int)V) : 1;
+}
+
 int64_t tops_gla_chunk_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
                                 int chunk_size, int varlen, int dtype) {
-  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || K > 128 || V > 128) return 0;
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || K > 256 || V > (1 << 20)) return 0;
   if (!tops::head_supported(dtype, chunk_size, (int)K, (int)V, false)) return 0;
   int NS, SL;
-  tops::head_seg_plan((int)B, (int)H, (int)T, chunk_size, varlen != 0, NS, SL);
+  tops::head_seg_plan((int)B, (int)H, (int)T, chunk_size, varlen != 0, NS, SL,
+                      tops::head_vtiles((int)K, (int)V));
   return tops::head_seg_ws_bytes((int)B, NS, (int)H, (int)K, (int)V);
 }
 
@@ -359,10 +367,13 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
   rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
   if (rc) return rc;
   if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || g == nullptr ||
-                    o == nullptr || h_ws == nullptr))
-    return fail(TOPS_GLA_EINVAL, "q, k, v, g, o and h_ws must not be NULL");
+                    o == nullptr))
+    return fail(TOPS_GLA_EINVAL, "q, k, v, g and o must not be NULL");
   hipStream_t st = (hipStream_t)stream;
-  if (use_head(dtype, chunk_size, K, V, false, {q, k, v, g, h0, o, ht, h_ws})) {
+  const bool head = use_head(dtype, chunk_size, K, V, false, {q, k, v, g, h0, o, ht, h_ws});
+  if (!head && h_ws == nullptr && B * T > 0)
+    return fail(TOPS_GLA_EINVAL, "h_ws must not be NULL off the full-head path");
+  if (head) {
     tops::HeadFwdArgs f = {};
     f.q = q;
     f.k = k;
@@ -448,13 +459,17 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   if (rc) return rc;
   if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || g == nullptr ||
                     dout == nullptr || dq == nullptr || dk == nullptr || dv == nullptr ||
-                    dg == nullptr || dh_ws == nullptr))
-    return fail(TOPS_GLA_EINVAL, "q, k, v, g, do, dq, dk, dv, dg and dh_ws must not be NULL");
+                    dg == nullptr))
+    return fail(TOPS_GLA_EINVAL, "q, k, v, g, do, dq, dk, dv and dg must not be NULL");
   if (h == nullptr && h_ws == nullptr && B * T > 0)
     return fail(TOPS_GLA_EINVAL, "h_ws is required when h is NULL");
   hipStream_t st = (hipStream_t)stream;
+  // full-head scans for the state recompute; the fused backward for K, V <= 128
   const bool head = use_head(dtype, chunk_size, K, V, false, {q, k, v, g, h0, h, dout, dht,
                                                               dh0, h_ws, dh_ws});
+  const bool head_bwd = head && tops::head_bwd_supported((int)K, (int)V);
+  if (!head_bwd && dh_ws == nullptr && B * T > 0)
+    return fail(TOPS_GLA_EINVAL, "dh_ws must not be NULL off the fused full-head backward");
   int NS = 1, SL = 0;
   float *seg_st = nullptr, *seg_gm = nullptr;
   if (head) seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, NS, SL, seg_st, seg_gm);
@@ -503,7 +518,7 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     if (rc) return rc;
     h = h_ws;
   }
-  if (head) {
+  if (head_bwd) {
     // fused: reverse dh scan and per-chunk gradients in one pass (dh_ws is not needed)
     tops::HeadBwdArgs b = {};
     b.q = q;
@@ -528,6 +543,10 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     b.V = (int)V;
     b.si = si;
     return hip_status(tops::run_head_bwd(b, st), "chunk_bwd (full-head)");
+  } else if (head) {
+    // wide heads: the full-head reverse scan stores dh for the per-chunk gradient kernels
+    rc = hip_status(head_scan(true, q, dout, dht, dh_ws, dh0, scale), "chunk_bwd (dh scan)");
+    if (rc) return rc;
   } else {
     tops::ScanArgs d;
     d.a = q;

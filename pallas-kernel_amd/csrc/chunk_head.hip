@@ -189,9 +189,12 @@ __device__ __forceinline__ float via_vgpr(float x) {
   return y;
 }
 
+// State slices: rows k < K, columns v < V of a [K][ld] row-major state (ld = V for a whole
+// state; a V tile passes its base column's address and the full row stride).
 template <int NTV, int NTK>
 __device__ __forceinline__ void load_state(f32x4 (&acc)[NTV][NTK], const float* init, int K,
-                                           int V, int vt0, int kt0, int lane) {
+                                           int V, int vt0, int kt0, int lane, int ld = -1) {
+  if (ld < 0) ld = V;
 #pragma unroll
   for (int i = 0; i < NTV; ++i)
 #pragma unroll
@@ -200,7 +203,7 @@ __device__ __forceinline__ void load_state(f32x4 (&acc)[NTV][NTK], const float* 
       const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
       if (init && kk < K && vv < V) {
         const float4 x = *reinterpret_cast<const float4*>(
-            reinterpret_cast<const char*>(init) + (uint32_t)(kk * V + vv) * 4u);
+            reinterpret_cast<const char*>(init) + (uint32_t)(kk * ld + vv) * 4u);
         acc[i][j][0] = via_vgpr(x.x);
         acc[i][j][1] = via_vgpr(x.y);
         acc[i][j][2] = via_vgpr(x.z);
@@ -211,28 +214,32 @@ __device__ __forceinline__ void load_state(f32x4 (&acc)[NTV][NTK], const float* 
 
 template <int NTV, int NTK>
 __device__ __forceinline__ void store_state_f32(const f32x4 (&acc)[NTV][NTK], float* dst,
-                                                int K, int V, int vt0, int kt0, int lane) {
+                                                int K, int V, int vt0, int kt0, int lane,
+                                                int ld = -1) {
+  if (ld < 0) ld = V;
 #pragma unroll
   for (int i = 0; i < NTV; ++i)
 #pragma unroll
     for (int j = 0; j < NTK; ++j) {
       const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
       if (kk < K && vv < V)
-        *reinterpret_cast<float4*>(reinterpret_cast<char*>(dst) + (uint32_t)(kk * V + vv) * 4u) =
+        *reinterpret_cast<float4*>(reinterpret_cast<char*>(dst) + (uint32_t)(kk * ld + vv) * 4u) =
             make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
     }
 }
 
 template <int NTV, int NTK>
 __device__ __forceinline__ void store_state_bf16(const f32x4 (&acc)[NTV][NTK], bf16* dst,
-                                                 int K, int V, int vt0, int kt0, int lane) {
+                                                 int K, int V, int vt0, int kt0, int lane,
+                                                 int ld = -1) {
+  if (ld < 0) ld = V;
 #pragma unroll
   for (int i = 0; i < NTV; ++i)
 #pragma unroll
     for (int j = 0; j < NTK; ++j) {
       const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
       if (kk < K && vv < V)
-        st8(dst, (uint32_t)(kk * V + vv) * 2u,
+        st8(dst, (uint32_t)(kk * ld + vv) * 2u,
             make_uint2(pack2_bf16(acc[i][j][0], acc[i][j][1]),
                        pack2_bf16(acc[i][j][2], acc[i][j][3])));
     }
@@ -240,10 +247,13 @@ __device__ __forceinline__ void store_state_bf16(const f32x4 (&acc)[NTV][NTK], b
 
 // acc = acc * decay[k] + X^T Y over the chunk: X = b [c][v] (sB), Y = a [c][k] (sA), both
 // read with transposed fragments.
+// With `post`, the result is then scaled by post[k] (the update then reads
+// acc = post (.) (acc * decay + X^T Y)).
 template <int NTV, int NTK>
 __device__ __forceinline__ void state_update(f32x4 (&acc)[NTV][NTK], const bf16* sB, int PB,
                                              const bf16* sA, int PA, const float* decay,
-                                             int vt0, int kt0, int lane) {
+                                             int vt0, int kt0, int lane,
+                                             const float* post = nullptr) {
 #pragma unroll
   for (int j = 0; j < NTK; ++j) {
     const float d = decay[(kt0 + j) * 16 + (lane & 15)];
@@ -262,6 +272,20 @@ __device__ __forceinline__ void state_update(f32x4 (&acc)[NTV][NTK], const bf16*
 #pragma unroll
       for (int j = 0; j < NTK; ++j) mma(acc[i][j], x[i], y[j]);
   }
+  if (post) {
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) {
+      const float d = post[(kt0 + j) * 16 + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) acc[i][j] *= d;
+    }
+  }
+}
+
+// V tile width of the full-head kernels for a K-wide head: the state slice K x VP stays in
+// the block's MFMA accumulators (8 tiles of 16 x 16 per wave for every supported shape).
+__host__ __device__ constexpr int head_vp(int KP, int V) {
+  return KP > 128 ? 64 : (V <= 64 ? 64 : 128);
 }
 
 }  // namespace
@@ -290,7 +314,10 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   const int H = p.H, K = p.K, V = p.V;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, scalar
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int L0 = xcd_remap(blockIdx.x, gridDim.x);
+  const int VT = (V + VP - 1) / VP;            // V tiles (blocks of one segment and head)
+  const int vt = L0 % VT, L = L0 / VT;
+  const int cv = vt * VP, Vw = min(VP, V - cv);   // this tile's first column and width
   const int hh = L % H;
   const int nsl = p.ns_launch;
   const int s = p.s_begin + (L / H) % nsl;
@@ -303,17 +330,17 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 
   const int cg = tid % MA::NCG, rs = tid / MA::NCG;    // a / g mapping
   const int vg = tid % MB::NCG, vrs = tid / MB::NCG;   // b mapping
-  const bool colA = cg * 8 < K, colB = vg * 8 < V;
+  const bool colA = cg * 8 < K, colB = vg * 8 < Vw;
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
   f32x4 acc[NTV][NTK];
   {
     const float* init = nullptr;
     if (first_seg)
-      init = p.s_init ? p.s_init + ((long)sg.seq * H + hh) * KV : nullptr;
+      init = p.s_init ? p.s_init + ((long)sg.seq * H + hh) * KV + cv : nullptr;
     else if (p.pass == 3)
-      init = p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV;
-    load_state<NTV, NTK>(acc, init, K, V, vt0, kt0, lane);
+      init = p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV + cv;
+    load_state<NTV, NTK>(acc, init, K, Vw, vt0, kt0, lane, V);
   }
 
   struct Regs {
@@ -327,7 +354,8 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     const long oa = (long)t0 * rsK + (long)hh * K;
     hload<RPT>(R.a, a + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
-    hload<VRPT>(R.b, b + (long)t0 * rsV + (long)hh * V, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
+    hload<VRPT>(R.b, b + (long)t0 * rsV + (long)hh * V + cv, (uint32_t)rsV, vrs * VRPT, len,
+                vg * 8, Vw);
   };
 
   float gsum[8];   // pass 1: total base-2 decay of the segment
@@ -373,8 +401,8 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     issue(step + 2, R);
     __syncthreads();
     if (s_all)   // state entering the chunk (forward) / leaving it (reverse)
-      store_state_bf16<NTV, NTK>(acc, s_all + ((long)(sg.c0 + ci) * H + hh) * KV, K, V, vt0,
-                                 kt0, lane);
+      store_state_bf16<NTV, NTK>(acc, s_all + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K, Vw,
+                                 vt0, kt0, lane, V);
     state_update<NTV, NTK>(acc, sB, PVP, sA, PKP, sGam, vt0, kt0, lane);
   };
 
@@ -393,13 +421,13 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   }
 
   if (p.pass == 1) {
-    store_state_f32<NTV, NTK>(acc, p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV, K,
-                              V, vt0, kt0, lane);
-    if (rs == 0 && colA)
+    store_state_f32<NTV, NTK>(acc, p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV + cv,
+                              K, Vw, vt0, kt0, lane, V);
+    if (vt == 0 && rs == 0 && colA)   // the decays are the same for every V tile
       st_f8(p.seg_gam + ((long)(sg.seq * p.NS + s) * H + hh) * K + cg * 8, gsum);
   } else if (last_seg && p.s_final) {
-    store_state_f32<NTV, NTK>(acc, p.s_final + ((long)sg.seq * H + hh) * KV, K, V, vt0, kt0,
-                              lane);
+    store_state_f32<NTV, NTK>(acc, p.s_final + ((long)sg.seq * H + hh) * KV + cv, K, Vw, vt0,
+                              kt0, lane, V);
   }
 }
 
@@ -445,21 +473,27 @@ __global__ __launch_bounds__(256) void head_combine_kernel(float* __restrict__ s
 //   qg = q 2^{g~-r}, kg = k 2^{r-g~}, kd = kg 2^{gamma-r}, A = scale tril(qg kg^T),
 //   o = A v + qg (scale 2^r h), h <- 2^{gamma} h + kd^T v.
 // ---------------------------------------------------------------------------
+// KD: kd is staged in LDS (K <= 128). Wider heads (K = 256) do not have the room; their
+// update runs on kg with the column factors split around the product:
+// h <- 2^{gamma-r} (.) (2^r h + kg^T v)  (= 2^gamma h + kd^T v).
 template <int KP, int VP>
 struct HFLayout {
+  static constexpr bool KD = KP <= 128;
   static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP),
                        PA = pitch_of<bf16>(HC);
   static constexpr int qg = 0;
   static constexpr int kg = qg + HC * PKP * 2;
   static constexpr int kd = kg + HC * PKP * 2;
-  static constexpr int v = kd + HC * PKP * 2;
+  static constexpr int v = kd + (KD ? HC * PKP * 2 : 0);
   static constexpr int hk = v + HC * PVP * 2;      // h' [k][v]
   static constexpr int a = hk + KP * PVP * 2;      // A  [i][j]
   static constexpr int tot = a + HC * PA * 2;
   static constexpr int first = tot + HNW * KP * 4;
   static constexpr int gam = first + KP * 4;
   static constexpr int rsc = gam + KP * 4;
-  static constexpr int bytes = rsc + KP * 4;
+  static constexpr int pre = rsc + KP * 4;        // 2^r          (!KD)
+  static constexpr int post = pre + KP * 4;       // 2^{gamma-r}  (!KD)
+  static constexpr int bytes = post + KP * 4;
 };
 
 template <int KP, int VP>
@@ -471,6 +505,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   constexpr int RPT = M::RPT, VRPT = MV::RPT;
   constexpr int PKP = Lay::PKP, PVP = Lay::PVP, PA = Lay::PA;
   constexpr int NTV = TL::NTV, NTK = TL::NTK;
+  // chunks of inputs in flight: two register sets, one for the wide head (K = 256), whose
+  // rows take twice the registers
+  constexpr int PF = KP > 128 ? 1 : 2;
   static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
@@ -483,6 +520,8 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   float* sFirst = reinterpret_cast<float*>(smem + Lay::first);
   float* sGam = reinterpret_cast<float*>(smem + Lay::gam);
   float* sRs = reinterpret_cast<float*>(smem + Lay::rsc);
+  float* sPre = reinterpret_cast<float*>(smem + Lay::pre);
+  float* sPost = reinterpret_cast<float*>(smem + Lay::post);
 
   const bf16* __restrict__ q = (const bf16*)p.q;
   const bf16* __restrict__ k = (const bf16*)p.k;
@@ -493,7 +532,10 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   const int H = p.H, K = p.K, V = p.V;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, scalar
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int L0 = xcd_remap(blockIdx.x, gridDim.x);
+  const int VT = (V + VP - 1) / VP;            // V tiles (blocks of one segment and head)
+  const int vt = L0 % VT, L = L0 / VT;
+  const int cv = vt * VP, Vw = min(VP, V - cv);   // this tile's first column and width
   const int hh = L % H;
   const int s = (L / H) % p.NS;
   const Seg sg = seg_of(p.si, (L / H) / p.NS, s, p.NS, p.SL);
@@ -503,7 +545,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 
   const int cg = tid % M::NCG, rs = tid / M::NCG;
   const int vg = tid % MV::NCG, vrs = tid / MV::NCG;
-  const bool colA = cg * 8 < K, colB = vg * 8 < V;
+  const bool colA = cg * 8 < K, colB = vg * 8 < Vw;
 
   // zero A once (its upper triangle is never written)
   for (int i = tid; i < HC * PA / 8; i += HNT)
@@ -512,9 +554,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
   f32x4 acc[NTV][NTK];
   {
-    const float* init = s == 0 ? (p.h0 ? p.h0 + ((long)sg.seq * H + hh) * KV : nullptr)
-                               : p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV;
-    load_state<NTV, NTK>(acc, init, K, V, vt0, kt0, lane);
+    const float* init = s == 0 ? (p.h0 ? p.h0 + ((long)sg.seq * H + hh) * KV + cv : nullptr)
+                               : p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV + cv;
+    load_state<NTV, NTK>(acc, init, K, Vw, vt0, kt0, lane, V);
   }
 
   struct Regs {
@@ -528,7 +570,8 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     hload<RPT>(R.q, q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<RPT>(R.k, k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
-    hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
+    hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V + cv, (uint32_t)rsV, vrs * VRPT, len,
+                vg * 8, Vw);
   };
 
   auto body = [&](int step, Regs& R) {
@@ -565,7 +608,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       }
       *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pack8(xq);
       *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pack8(xk);
-      *reinterpret_cast<uint4*>(sKd + row * PKP + cg * 8) = pack8(xd);
+      if (Lay::KD) *reinterpret_cast<uint4*>(sKd + row * PKP + cg * 8) = pack8(xd);
     }
 #pragma unroll
     for (int j = 0; j < VRPT; ++j) {
@@ -582,8 +625,15 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       }
       st_f8(sGam + cg * 8, eg);
       st_f8(sRs + cg * 8, er);
+      if (!Lay::KD) {
+        float ep[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ep[e] = exp2_hw(r[e]);
+        st_f8(sPre + cg * 8, ep);
+        st_f8(sPost + cg * 8, fkd);
+      }
     }
-    issue(step + 2, R);
+    issue(step + PF, R);
     __syncthreads();
 
     // ---- (2) A (lower tiles), h_n to HBM, h' = scale 2^r h into LDS ----
@@ -600,8 +650,8 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       }
     }
     if (hout)
-      store_state_bf16<NTV, NTK>(acc, hout + ((long)(sg.c0 + ci) * H + hh) * KV, K, V, vt0,
-                                 kt0, lane);
+      store_state_bf16<NTV, NTK>(acc, hout + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K, Vw,
+                                 vt0, kt0, lane, V);
 #pragma unroll
     for (int j = 0; j < NTK; ++j) {
       const int kk = (kt0 + j) * 16 + (lane & 15);
@@ -628,15 +678,18 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
                                      lane);
         const int row = it * 16 + (lane & 15);
         const int vv = vt * 16 + 4 * (lane >> 4);
-        if (row < len && vv < V)
-          st8(o + (long)t0 * rsV + (long)hh * V, ((uint32_t)row * (uint32_t)rsV + vv) * 2u,
+        if (row < len && vv < Vw)
+          st8(o + (long)t0 * rsV + (long)hh * V + cv, ((uint32_t)row * (uint32_t)rsV + vv) * 2u,
               make_uint2(pack2_bf16(ot[0], ot[1]), pack2_bf16(ot[2], ot[3])));
       }
     }
-    state_update<NTV, NTK>(acc, sV, PVP, sKd, PKP, sGam, vt0, kt0, lane);
+    if (Lay::KD)
+      state_update<NTV, NTK>(acc, sV, PVP, sKd, PKP, sGam, vt0, kt0, lane);
+    else
+      state_update<NTV, NTK>(acc, sV, PVP, sKg, PKP, sPre, vt0, kt0, lane, sPost);
   };
 
-  if (nsteps > 0) {
+  if (nsteps > 0 && PF == 2) {
     Regs R0, R1;
     issue(0, R0);
     __builtin_amdgcn_sched_barrier(0);
@@ -646,10 +699,15 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       body(step, R1);
       if (step + 1 < nsteps) body(step + 1, R0);
     }
+  } else if (nsteps > 0) {
+    Regs R0;
+    issue(0, R0);
+    for (int step = 0; step < nsteps; ++step) body(step, R0);
   }
 
   if (s == p.NS - 1 && p.ht)
-    store_state_f32<NTV, NTK>(acc, p.ht + ((long)sg.seq * H + hh) * KV, K, V, vt0, kt0, lane);
+    store_state_f32<NTV, NTK>(acc, p.ht + ((long)sg.seq * H + hh) * KV + cv, K, Vw, vt0, kt0,
+                              lane, V);
 }
 
 
@@ -1108,16 +1166,26 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 // host side
 // ---------------------------------------------------------------------------
 bool head_supported(int dtype, int C, int K, int V, bool g_is_cumsum) {
-  return dtype == DT_BF16 && C == HC && K >= 8 && V >= 8 && K <= 128 && V <= 128 &&
-         K % 8 == 0 && V % 8 == 0 && !g_is_cumsum;
+  return dtype == DT_BF16 && C == HC && K >= 8 && V >= 8 && K <= 256 && K % 8 == 0 &&
+         V % 8 == 0 && !g_is_cumsum;
 }
 
-void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL) {
+bool head_bwd_supported(int K, int V) { return K <= 128 && V <= 128; }
+
+static int head_kp(int K) { return K <= 64 ? 64 : K <= 128 ? 128 : 256; }
+
+int head_vtiles(int K, int V) {
+  const int vp = head_vp(head_kp(K), V);
+  return (V + vp - 1) / vp;
+}
+
+void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL, int VT) {
   NS = 1;
   SL = 0;
   if (varlen || N <= 0 || H <= 0) return;
   const int nt = (T + C - 1) / C;
-  const long want = (512 + (long)N * H - 1) / ((long)N * H);   // about two blocks per CU
+  const long nh = (long)N * H * (VT > 0 ? VT : 1);
+  const long want = (512 + nh - 1) / nh;   // about two blocks per CU
   long ns = want < nt / 8 ? want : nt / 8;                     // segments of >= 8 chunks
   if (ns <= 1) return;
   SL = (int)((nt + ns - 1) / ns);
@@ -1145,11 +1213,14 @@ static hipError_t launch_head_scan(const HeadScanArgs& p, hipStream_t st, long b
 
 template <bool REV>
 static hipError_t head_scan_kp(const HeadScanArgs& p, hipStream_t st, long blocks) {
-  const bool k64 = p.K <= 64, v64 = p.V <= 64;
-  if (k64 && v64) return launch_head_scan<64, 64, REV>(p, st, blocks);
-  if (k64) return launch_head_scan<64, 128, REV>(p, st, blocks);
-  if (v64) return launch_head_scan<128, 64, REV>(p, st, blocks);
-  return launch_head_scan<128, 128, REV>(p, st, blocks);
+  blocks *= head_vtiles(p.K, p.V);
+  const int kp = head_kp(p.K);
+  if (kp == 256) return launch_head_scan<256, 64, REV>(p, st, blocks);
+  const bool v64 = head_vp(kp, p.V) == 64;
+  if (kp == 64) return v64 ? launch_head_scan<64, 64, REV>(p, st, blocks)
+                           : launch_head_scan<64, 128, REV>(p, st, blocks);
+  return v64 ? launch_head_scan<128, 64, REV>(p, st, blocks)
+             : launch_head_scan<128, 128, REV>(p, st, blocks);
 }
 
 static hipError_t head_scan_launch(HeadScanArgs p, bool reverse, hipStream_t st, int pass,
@@ -1197,7 +1268,7 @@ hipError_t run_head_scan(const HeadScanArgs& p0, bool reverse, hipStream_t st) {
 template <int KP, int VP>
 static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   using Lay = HFLayout<KP, VP>;
-  const long blocks = (long)p.si.N * p.NS * p.H;
+  const long blocks = (long)p.si.N * p.NS * p.H * ((p.V + VP - 1) / VP);
   if (blocks == 0) return hipSuccess;
   hipError_t e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
@@ -1230,11 +1301,11 @@ hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
     hipError_t e = head_prepare_segments(s, false, st);
     if (e != hipSuccess) return e;
   }
-  const bool k64 = p.K <= 64, v64 = p.V <= 64;
-  if (k64 && v64) return launch_head_fwd<64, 64>(p, st);
-  if (k64) return launch_head_fwd<64, 128>(p, st);
-  if (v64) return launch_head_fwd<128, 64>(p, st);
-  return launch_head_fwd<128, 128>(p, st);
+  const int kp = head_kp(p.K);
+  if (kp == 256) return launch_head_fwd<256, 64>(p, st);
+  const bool v64 = head_vp(kp, p.V) == 64;
+  if (kp == 64) return v64 ? launch_head_fwd<64, 64>(p, st) : launch_head_fwd<64, 128>(p, st);
+  return v64 ? launch_head_fwd<128, 64>(p, st) : launch_head_fwd<128, 128>(p, st);
 }
 
 // K = V = 128 runs with 16 waves (4 per SIMD, 128 registers each), smaller heads with 8.

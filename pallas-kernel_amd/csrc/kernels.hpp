@@ -142,11 +142,14 @@ hipError_t run_bwd_part(int which, const PartArgs& p, int C, hipStream_t st);
 bool recurrent_supported(int K, int V);  // state rows K (forward) and V, K (backward)
 hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st);
 
-// Full-head kernels (chunk_head.hip): bf16, chunk 64, K and V <= 128 (multiples of 8,
-// 16-byte aligned rows), raw gates. Optional sequence segments (fixed-length sequences):
-// seg_state [N, NS, H, K, V] f32 and seg_gam [N, NS, H, K] f32 workspaces.
-bool head_supported(int dtype, int C, int K, int V, bool g_is_cumsum);
-void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL);
+// Full-head kernels (chunk_head.hip): bf16, chunk 64, raw gates, K and V multiples of 8
+// (16-byte aligned rows); scans and forward for K <= 256 and any V (V tiles of 64 or 128
+// columns), the fused backward for K, V <= 128. Optional sequence segments (fixed-length
+// sequences): seg_state [N, NS, H, K, V] f32 and seg_gam [N, NS, H, K] f32 workspaces.
+bool head_supported(int dtype, int C, int K, int V, bool g_is_cumsum);   // scans, forward
+bool head_bwd_supported(int K, int V);                                     // + backward
+int head_vtiles(int K, int V);   // V tiles (blocks per segment and head)
+void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL, int VT);
 long head_seg_ws_bytes(int N, int NS, int H, int K, int V);
 
 struct HeadScanArgs {

@@ -49,6 +49,7 @@ _SIGS = {
                                      _I64, _I64, _P, _I64, _I, _I, _P],
     "tops_gla_fused_recurrent_bwd": [_P] * 16 + [_F, _I, _I64, _I64, _I64, _I64, _I64, _P,
                                                  _I64, _I, _P],
+    "tops_gla_full_head": [_I64, _I64, _I, _I, _I],
     "tops_gla_bwd_part_dA": [_P, _P, _P, _F, _I64, _I64, _I64, _I64, _I, _P],
     "tops_gla_bwd_part_dv": [_P] * 6 + [_I64] * 5 + [_I, _P],
     "tops_gla_bwd_part_dqk_intra": [_P] * 6 + [_I64] * 4 + [_I, _P],
@@ -101,6 +102,11 @@ def call(name, *args):
         if rc == 2:
             raise NotImplementedError(f"{name}: {msg}")
         raise RuntimeError(f"{name}: {msg}")
+
+
+def full_head(K, V, chunk, dtype, backward):
+    """True when the full-head kernels run this shape (see tops_gla_full_head)."""
+    return bool(load().tops_gla_full_head(K, V, chunk, dtype_code(dtype), int(bool(backward))))
 
 
 def seg_workspace(B, T, H, K, V, chunk, varlen, dtype, device):

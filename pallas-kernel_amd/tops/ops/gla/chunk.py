@@ -43,14 +43,15 @@ _MFMA_CHUNKS = (16, 32, 64)
 
 
 def _kernel_chunk(chunk_size: int) -> int:
-    """Chunk size used by the kernels for chunk-size-independent results (o, grads).
+    """Chunk size used by the kernels for chunk-size-independent results (o, ht, grads).
 
-    16/32/64 run as given; smaller powers of two run as 16 and larger ones as 64 (the
-    outputs are mathematically independent of the chunk size).
+    The outputs are mathematically independent of the chunk size, so every power of two
+    runs on 64-row chunks: the full-head kernels' size, and the most work per chunk for
+    the others.
     """
     c = int(chunk_size)
     assert c > 0 and c & (c - 1) == 0, "chunk_size must be power of 2"
-    return min(max(c, 16), 64)
+    return 64
 
 
 def _compute_dtype(*xs):
@@ -65,6 +66,14 @@ def _c(x, dt=None):
     if dt is not None and x.dtype != dt:
         x = x.to(dt)
     return x.contiguous()
+
+
+def _full_head(K, V, C, dtype, backward, *tensors):
+    """The full-head kernels will run (shape and 16-byte aligned buffers): state
+    workspaces they do not use need not be allocated."""
+    if any(t is not None and t.data_ptr() % 16 for t in tensors):
+        return False
+    return _lib.full_head(K, V, C, dtype, backward)
 
 
 def _default_scale(scale, K):
@@ -113,7 +122,11 @@ class _ChunkGLAFunction(torch.autograd.Function):
         o = torch.empty_like(v)
         ht = (torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev)
               if output_final_state else None)
-        h_ws = torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev)
+        # the states are the backward's residual: not kept when no gradient is wanted (the
+        # full-head path then stores none; the other paths read them back themselves)
+        keep = any(ctx.needs_input_grad[:5])
+        h_ws = (torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev)
+                if keep or not _full_head(K, V, chunk, q.dtype, False, q, k, v, g, h0) else None)
         ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list is not None, q.dtype, dev)
         call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(o), ptr(ht),
              ptr(h_ws), ptr(ws), nws, scale, B, T, H, K, V, chunk, *seq.args(), dt,
@@ -137,7 +150,8 @@ class _ChunkGLAFunction(torch.autograd.Function):
         dq, dk, dv, dg = (torch.empty_like(x) for x in (q, k, v, g))
         need_dh0 = h0 is not None and ctx.needs_input_grad[4]
         dh0 = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if need_dh0 else None
-        dh_ws = torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev)
+        dh_ws = (None if _full_head(K, V, chunk, q.dtype, True, q, k, v, g, h0, h_ws, do, dht)
+                 else torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev))
         ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list is not None, q.dtype, dev)
         call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(h_ws), ptr(do),
              ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None, ptr(dh_ws), ptr(ws),
@@ -423,7 +437,8 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
     want_dh0 = initial_state is not None or dht is not None
     dh0 = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if want_dh0 else None
     h_ws = None if h is not None else torch.empty(seq.NC, H, K, V, dtype=cdt, device=dev)
-    dh_ws = torch.empty(seq.NC, H, K, V, dtype=cdt, device=dev)
+    dh_ws = (None if _full_head(K, V, C, cdt, True, qq, kk, vv, gg, dd, h, dht, initial_state)
+             else torch.empty(seq.NC, H, K, V, dtype=cdt, device=dev))
     ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list is not None, cdt, dev)
     call("tops_gla_chunk_bwd", ptr(qq), ptr(kk), ptr(vv), ptr(gg),
          ptr(_c(initial_state, torch.float32)), ptr(h), ptr(dd), ptr(_c(dht, torch.float32)),

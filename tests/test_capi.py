@@ -32,7 +32,7 @@ def _declared():
 
 def test_header_lists_entry_points():
     decl = _declared()
-    assert len(decl) == 19, decl
+    assert len(decl) == 20, decl
     assert set(decl) == set(_lib.EXPORTED)
 
 
@@ -171,4 +171,7 @@ def test_segment_workspace_query():
     assert q(4, 8192, 16, 128, 128, 64, 0, 0) == 0      # float32: other kernels
     assert q(4, 8192, 16, 128, 128, 32, 0, 1) == 0      # chunk 32: other kernels
     assert q(1, 256, 2, 64, 64, 64, 0, 1) == 0          # 4 chunks: too short to split
-    assert q(4, 8192, 16, 256, 128, 64, 0, 1) == 0      # K > 128
+    # K = 256: V tiles of 64 columns (2 per head) -> 4 segments of 32 chunks
+    st2, gm2 = 4 * 4 * 16 * 256 * 128 * 4, 4 * 4 * 16 * 256 * 4
+    assert q(4, 8192, 16, 256, 128, 64, 0, 1) == st2 + (gm2 + 255) // 256 * 256
+    assert q(4, 8192, 16, 320, 128, 64, 0, 1) == 0      # K > 256: other kernels

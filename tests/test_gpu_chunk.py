@@ -55,6 +55,10 @@ FWD_CASES = [
     dict(B=2, T=2048, H=2, K=128, V=128, seed=801, C=64, h0=True, gate_div=16.0),
     dict(B=1, T=2000, H=3, K=64, V=128, seed=802, C=64, h0=True),
     dict(B=2, T=1536, H=1, K=96, V=40, seed=803, C=64, h0=True, gate_div=4.0),
+    # wide heads on the full-head forward: K = 256 in 64-column V tiles (a partial last
+    # tile), segmented (1024 tokens -> 2 segments x 3 V tiles)
+    dict(B=1, T=1024, H=2, K=256, V=160, seed=804, C=64, h0=True, gate_div=16.0),
+    dict(B=1, T=300, H=2, K=200, V=72, seed=805, C=64, h0=True),
 ]
 
 
@@ -141,6 +145,8 @@ BWD_CASES = [
     dict(B=2, T=1536, H=1, K=96, V=40, seed=813, C=64, dht=True, gate_div=4.0),
     # 128 x 64 state tiles: the backward's fp32 exchange must not alias the A / dA tiles
     dict(B=1, T=1024, H=2, K=128, V=64, seed=814, C=64, h0=True, dht=True, gate_div=4.0),
+    # wide head: full-head forward and dh scan (V tiles, segments), per-chunk gradients
+    dict(B=1, T=1024, H=2, K=256, V=192, seed=815, C=64, h0=True, dht=True, gate_div=16.0),
 ]
 
 
