@@ -237,6 +237,57 @@ int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v, co
                                  int dtype, void* stream);
 
 /*
+ * The GLA layer's stages around the attention core (rows = tokens x heads, D features per
+ * row, D % 8 == 0, 16-byte aligned buffers; x, g, y, dy, dx, dg in `dtype`, w / dw float32):
+ * RMSNorm with optional weight w and SiLU gate g:  y = x rsqrt(mean(x^2) + eps) [w] [silu(g)].
+ * The forward keeps rstd [rows] (float32, may be NULL) for the backward. The backward writes
+ * dx, dg (when g is given) and dw (when w is given; it needs dw_ws of
+ * tops_gla_rmsnorm_ws_bytes(rows, D) bytes).
+ * Replaces: FusedRMSNormGated.__call__, tops/modules/fused_norm_gate.py:28-37, and
+ *           RMSNorm.__call__, tops/modules/layernorm.py:28-35 (g = NULL).
+ */
+int tops_gla_rmsnorm_gated_fwd(const void* x, const void* g, const float* w, void* y,
+                               float* rstd, int64_t rows, int64_t D, float eps, int dtype,
+                               void* stream);
+int tops_gla_rmsnorm_gated_bwd(const void* x, const void* g, const float* w, const float* rstd,
+                               const void* dy, void* dx, void* dg, float* dw, void* dw_ws,
+                               int64_t dw_ws_bytes, int64_t rows, int64_t D, int dtype,
+                               void* stream);
+int64_t tops_gla_rmsnorm_ws_bytes(int64_t rows, int64_t D);
+
+/*
+ * Key-wise decay gate: y = max(log_sigmoid(x) / normalizer, clamp_min) (clamp when
+ * has_clamp), element-wise over count elements; the backward writes
+ * dx = dy sigmoid(-x) / normalizer where y was not clamped.
+ * Replaces: tops/layers/gla.py:286-288 (jax.nn.log_sigmoid(gk) / gate_logit_normalizer,
+ *           jnp.clip(gk, a_min=clamp_min)).
+ */
+int tops_gla_gate_logsigmoid_fwd(const void* x, void* y, int64_t count, float normalizer,
+                                 int has_clamp, float clamp_min, int dtype, void* stream);
+int tops_gla_gate_logsigmoid_bwd(const void* x, const void* dy, void* dx, int64_t count,
+                                 float normalizer, int has_clamp, float clamp_min, int dtype,
+                                 void* stream);
+
+/*
+ * Causal depthwise convolution of a [B, T, D] sequence (varlen: B = 1 and cu_seqlens [N+1];
+ * max_len = the longest sequence), kernel width W <= 8, weight w [D][W] float32, optional
+ * bias [D] float32, optional SiLU; rows before a sequence's first token read as zero.
+ * D % 8 == 0, 16-byte aligned buffers. The backward writes dx and, when dw_db is given,
+ * dw [D][W] then db [D] (float32) using ws of tops_gla_short_conv_ws_bytes bytes.
+ * Replaces: ShortConvolution._causal_conv1d, tops/modules/convolution.py:46-78.
+ */
+int tops_gla_short_conv_fwd(const void* x, const float* w, const float* bias, void* y,
+                            int64_t B, int64_t T, int64_t D, int W, int silu,
+                            const int32_t* cu_seqlens, int64_t N, int64_t max_len, int dtype,
+                            void* stream);
+int tops_gla_short_conv_bwd(const void* x, const float* w, const float* bias, const void* dy,
+                            void* dx, float* dw_db, void* ws, int64_t ws_bytes, int64_t B,
+                            int64_t T, int64_t D, int W, int silu, const int32_t* cu_seqlens,
+                            int64_t N, int64_t max_len, int dtype, void* stream);
+int64_t tops_gla_short_conv_ws_bytes(int64_t B, int64_t T, int64_t D, int W, int64_t N,
+                                     int64_t max_len, int varlen);
+
+/*
  * Measurement hook (no counterpart in the reference): with timing enabled, HIP events are
  * recorded on the launch stream around the fused full-head forward (which = 0) and
  * backward (which = 1) kernels of tops_gla_chunk_fwd / tops_gla_chunk_bwd.

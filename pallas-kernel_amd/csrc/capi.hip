@@ -794,6 +794,176 @@ int tops_gla_bwd_part_dqkg(const float* q, const float* k, const float* v, const
                     "bwd_part_dqkg");
 }
 
+namespace {
+
+int norm_check(int64_t rows, int64_t D, int dtype, std::initializer_list<const void*> need,
+               std::initializer_list<const void*> aligned) {
+  if (!dtype_ok(dtype)) return fail(TOPS_GLA_EINVAL, "bad dtype");
+  if (rows < 0 || D <= 0 || D % 8 != 0 || D > 8192)
+    return fail(TOPS_GLA_EINVAL, "rows >= 0 and D a positive multiple of 8 up to 8192 "
+                "(rows=%lld, D=%lld)", (long long)rows, (long long)D);
+  if (rows > 0)
+    for (const void* q : need)
+      if (q == nullptr) return fail(TOPS_GLA_EINVAL, "NULL buffer");
+  for (const void* q : aligned)
+    if (!aligned16(q)) return fail(TOPS_GLA_EUNSUPPORTED, "buffers must be 16-byte aligned");
+  return TOPS_GLA_OK;
+}
+
+}  // namespace
+
+int64_t tops_gla_rmsnorm_ws_bytes(int64_t rows, int64_t D) {
+  if (rows <= 0 || D <= 0) return 0;
+  return tops::norm_gate_bwd_blocks((long)rows) * D * 4;
+}
+
+int tops_gla_rmsnorm_gated_fwd(const void* x, const void* g, const float* w, void* y,
+                               float* rstd, int64_t rows, int64_t D, float eps, int dtype,
+                               void* stream) {
+  int rc = norm_check(rows, D, dtype, {x, y}, {x, g, w, y});
+  if (rc) return rc;
+  tops::NormGateArgs p = {};
+  p.x = x;
+  p.g = g;
+  p.w = w;
+  p.y = y;
+  p.rstd = rstd;
+  p.rows = (long)rows;
+  p.D = (int)D;
+  p.eps = eps;
+  return hip_status(tops::run_norm_gate_fwd(p, dtype, (hipStream_t)stream), "rmsnorm_gated_fwd");
+}
+
+int tops_gla_rmsnorm_gated_bwd(const void* x, const void* g, const float* w, const float* rstd,
+                               const void* dy, void* dx, void* dg, float* dw, void* dw_ws,
+                               int64_t dw_ws_bytes, int64_t rows, int64_t D, int dtype,
+                               void* stream) {
+  int rc = norm_check(rows, D, dtype, {x, rstd, dy, dx}, {x, g, w, dy, dx, dg});
+  if (rc) return rc;
+  if (g != nullptr && dg == nullptr && rows > 0)
+    return fail(TOPS_GLA_EINVAL, "dg is required when g is given");
+  if (w != nullptr && dw != nullptr && rows > 0 &&
+      (dw_ws == nullptr || dw_ws_bytes < tops_gla_rmsnorm_ws_bytes(rows, D)))
+    return fail(TOPS_GLA_EINVAL, "dw needs dw_ws of tops_gla_rmsnorm_ws_bytes bytes");
+  tops::NormGateArgs p = {};
+  p.x = x;
+  p.g = g;
+  p.w = w;
+  p.rstd = const_cast<float*>(rstd);
+  p.dy = dy;
+  p.dx = dx;
+  p.dg = dg;
+  p.dw_part = dw ? (float*)dw_ws : nullptr;
+  p.rows = (long)rows;
+  p.D = (int)D;
+  return hip_status(tops::run_norm_gate_bwd(p, dw, dtype, (hipStream_t)stream),
+                    "rmsnorm_gated_bwd");
+}
+
+int tops_gla_gate_logsigmoid_fwd(const void* x, void* y, int64_t count, float normalizer,
+                                 int has_clamp, float clamp_min, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(TOPS_GLA_EINVAL, "bad dtype");
+  if (count < 0 || normalizer == 0.f) return fail(TOPS_GLA_EINVAL, "bad count or normalizer");
+  if (count > 0 && (x == nullptr || y == nullptr)) return fail(TOPS_GLA_EINVAL, "NULL buffer");
+  if (!aligned16(x) || !aligned16(y))
+    return fail(TOPS_GLA_EUNSUPPORTED, "buffers must be 16-byte aligned");
+  return hip_status(tops::run_gate(x, nullptr, y, (long)count, 1.f / normalizer, has_clamp,
+                                   clamp_min, dtype, (hipStream_t)stream),
+                    "gate_logsigmoid_fwd");
+}
+
+int tops_gla_gate_logsigmoid_bwd(const void* x, const void* dy, void* dx, int64_t count,
+                                 float normalizer, int has_clamp, float clamp_min, int dtype,
+                                 void* stream) {
+  if (!dtype_ok(dtype)) return fail(TOPS_GLA_EINVAL, "bad dtype");
+  if (count < 0 || normalizer == 0.f) return fail(TOPS_GLA_EINVAL, "bad count or normalizer");
+  if (count > 0 && (x == nullptr || dy == nullptr || dx == nullptr))
+    return fail(TOPS_GLA_EINVAL, "NULL buffer");
+  if (!aligned16(x) || !aligned16(dy) || !aligned16(dx))
+    return fail(TOPS_GLA_EUNSUPPORTED, "buffers must be 16-byte aligned");
+  return hip_status(tops::run_gate(x, dy, dx, (long)count, 1.f / normalizer, has_clamp,
+                                   clamp_min, dtype, (hipStream_t)stream),
+                    "gate_logsigmoid_bwd");
+}
+
+namespace {
+
+int conv_setup(int64_t B, int64_t T, int64_t D, int W, const int32_t* cu, int64_t N,
+               int64_t max_len, int dtype, tops::ShortConvArgs* p) {
+  if (!dtype_ok(dtype)) return fail(TOPS_GLA_EINVAL, "bad dtype");
+  if (D <= 0 || D % 8 != 0 || D > (1 << 20))
+    return fail(TOPS_GLA_EINVAL, "D must be a positive multiple of 8 (D=%lld)", (long long)D);
+  if (W < 1 || W > 8) return fail(TOPS_GLA_EUNSUPPORTED, "kernel width W in 1..8 (W=%d)", W);
+  tops::SeqInfo si;
+  const int64_t NC = cu ? 0 : B * T;
+  int rc = make_seq(B, T, 1, 1, cu, nullptr, N, NC, false, &si);
+  if (rc) return rc;
+  if (cu && (max_len < 0 || max_len > T)) return fail(TOPS_GLA_EINVAL, "bad max_len");
+  *p = tops::ShortConvArgs{};
+  p->D = (int)D;
+  p->W = W;
+  p->max_len = (int)(cu ? max_len : T);
+  p->si = si;
+  return TOPS_GLA_OK;
+}
+
+}  // namespace
+
+int64_t tops_gla_short_conv_ws_bytes(int64_t B, int64_t T, int64_t D, int W, int64_t N,
+                                     int64_t max_len, int varlen) {
+  if (B <= 0 || T <= 0 || D <= 0 || W < 1 || W > 8) return 0;
+  const long rows = varlen ? tops::short_conv_part_rows((long)N, (long)max_len)
+                           : tops::short_conv_part_rows((long)B, (long)T);
+  return (int64_t)rows * (W + 1) * D * 4;
+}
+
+int tops_gla_short_conv_fwd(const void* x, const float* w, const float* bias, void* y,
+                            int64_t B, int64_t T, int64_t D, int W, int silu,
+                            const int32_t* cu_seqlens, int64_t N, int64_t max_len, int dtype,
+                            void* stream) {
+  tops::ShortConvArgs p;
+  int rc = conv_setup(B, T, D, W, cu_seqlens, N, max_len, dtype, &p);
+  if (rc) return rc;
+  if (B * T > 0 && (x == nullptr || w == nullptr || y == nullptr))
+    return fail(TOPS_GLA_EINVAL, "x, w and y must not be NULL");
+  if (!aligned16(x) || !aligned16(y))
+    return fail(TOPS_GLA_EUNSUPPORTED, "buffers must be 16-byte aligned");
+  p.x = x;
+  p.y = y;
+  p.w = w;
+  p.bias = bias;
+  p.silu = silu != 0;
+  return hip_status(tops::run_short_conv(p, false, dtype, (hipStream_t)stream), "short_conv_fwd");
+}
+
+int tops_gla_short_conv_bwd(const void* x, const float* w, const float* bias, const void* dy,
+                            void* dx, float* dw_db, void* ws, int64_t ws_bytes, int64_t B,
+                            int64_t T, int64_t D, int W, int silu, const int32_t* cu_seqlens,
+                            int64_t N, int64_t max_len, int dtype, void* stream) {
+  tops::ShortConvArgs p;
+  int rc = conv_setup(B, T, D, W, cu_seqlens, N, max_len, dtype, &p);
+  if (rc) return rc;
+  if (B * T > 0 && (x == nullptr || w == nullptr || dy == nullptr || dx == nullptr))
+    return fail(TOPS_GLA_EINVAL, "x, w, dy and dx must not be NULL");
+  if (!aligned16(x) || !aligned16(dy) || !aligned16(dx))
+    return fail(TOPS_GLA_EUNSUPPORTED, "buffers must be 16-byte aligned");
+  p.x = x;
+  p.dy = dy;
+  p.dx = dx;
+  p.w = w;
+  p.bias = bias;
+  p.silu = silu != 0;
+  if (dw_db) {
+    const int64_t need = tops_gla_short_conv_ws_bytes(B, T, D, W, N, max_len,
+                                                      cu_seqlens != nullptr);
+    if (ws == nullptr || ws_bytes < need)
+      return fail(TOPS_GLA_EINVAL, "dw_db needs ws of tops_gla_short_conv_ws_bytes bytes");
+    p.part = (float*)ws;
+    p.dwb = dw_db;
+  }
+  return hip_status(tops::run_short_conv(p, true, dtype, (hipStream_t)stream), "short_conv_bwd");
+}
+
 int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v, const void* gk,
                                  const void* gv, const float* o, const void* dout,
                                  const float* dht, const float* h0, float* dq, float* dk,

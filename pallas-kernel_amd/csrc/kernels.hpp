@@ -139,6 +139,43 @@ struct PartArgs {
 };
 hipError_t run_bwd_part(int which, const PartArgs& p, int C, hipStream_t st);
 
+// RMSNorm with optional SiLU gate and weight, and the log-sigmoid gate (norm_gate.hip).
+struct NormGateArgs {
+  const void *x, *g;     // [rows, D] input dtype; g nullable
+  const float* w;        // [D] nullable
+  void* y;               // forward output
+  float* rstd;           // [rows] (forward: nullable; backward: input)
+  const void* dy;        // backward
+  void *dx, *dg;         // backward outputs (dg when g is given)
+  float* dw_part;        // [norm_gate_bwd_blocks(rows), D] workspace for dw (nullable)
+  long rows;
+  int D;
+  float eps;
+};
+long norm_gate_bwd_blocks(long rows);
+hipError_t run_norm_gate_fwd(const NormGateArgs& p, int dtype, hipStream_t st);
+hipError_t run_norm_gate_bwd(const NormGateArgs& p, float* dw, int dtype, hipStream_t st);
+hipError_t run_gate(const void* x, const void* dy, void* out, long count, float inv_n,
+                    int has_clamp, float clamp, int dtype, hipStream_t st);
+
+// out[c] = sum_b part[b][c] for c < M (deterministic column sums of per-block partials).
+hipError_t run_rows_sum(const float* part, int nblk, int M, float* out, hipStream_t st);
+
+// Causal depthwise convolution with optional bias and SiLU (short_conv.hip).
+struct ShortConvArgs {
+  const void *x, *dy;   // [tokens, D] input dtype
+  void *y, *dx;
+  const float* w;       // [D][W]
+  const float* bias;    // [D] nullable
+  float* part;          // backward: [short_conv_part_rows, (W + 1) * D] (nullable: no dw/db)
+  float* dwb;           // backward: dw [D][W] then db [D]
+  int D, W, silu;
+  int max_len;          // longest sequence (varlen grid)
+  SeqInfo si;           // C unused
+};
+long short_conv_part_rows(long nseq, long len);   // len: T, or the longest sequence
+hipError_t run_short_conv(const ShortConvArgs& p, bool backward, int dtype, hipStream_t st);
+
 bool recurrent_supported(int K, int V);  // state rows K (forward) and V, K (backward)
 hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st);
 

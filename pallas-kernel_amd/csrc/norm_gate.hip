@@ -1,0 +1,324 @@
+// The GLA layer's element-wise stages around the attention core:
+//   * RMSNorm with an optional SiLU output gate, per row of D features:
+//       y = x rsqrt(mean(x^2) + eps) [* w] [* silu(g)]
+//     Reference: FusedRMSNormGated.__call__, tops/modules/fused_norm_gate.py:28-37, and
+//     RMSNorm.__call__, tops/modules/layernorm.py:28-35 (no gate).
+//   * the gate activation of the key-wise decay, y = max(log_sigmoid(x) / n, clamp_min),
+//     tops/layers/gla.py:286-288.
+// One wave per row (D up to 8192 features, 8 per lane and pass, 16-byte accesses), fp32
+// arithmetic, output in the input dtype. The backward of the norm reduces dw over rows in
+// two steps: each block sums its rows into its own partial row of a caller workspace, a
+// second kernel sums the partials (deterministic, no atomics).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace tops {
+
+namespace {
+
+constexpr int NG_NT = 256;            // 4 waves, one row each at a time
+constexpr int NG_ROWS = 16;           // forward: rows per block (4 per wave)
+constexpr int NG_BWD_BLOCKS = 1024;   // backward grid (blocks stride over the rows)
+
+template <typename T>
+struct Vec8;
+template <>
+struct Vec8<bf16> {
+  static __device__ __forceinline__ void load(const bf16* p, float (&x)[8]) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ void store(bf16* p, const float (&x)[8]) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]),
+                                              pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
+  }
+};
+template <>
+struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float* p, float (&x)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&x)[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(x[0], x[1], x[2], x[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(x[4], x[5], x[6], x[7]);
+  }
+};
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
+
+}  // namespace
+
+// y = x * rstd * w * silu(g); rstd per row is kept for the backward (may be NULL).
+template <typename T>
+__global__ __launch_bounds__(NG_NT) void norm_gate_fwd_kernel(NormGateArgs p) {
+  const T* __restrict__ x = (const T*)p.x;
+  const T* __restrict__ g = (const T*)p.g;
+  T* __restrict__ y = (T*)p.y;
+  const int D = p.D, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const long r0 = (long)blockIdx.x * NG_ROWS;
+  for (int rr = w; rr < NG_ROWS; rr += NG_NT / 64) {
+    const long row = r0 + rr;
+    if (row >= p.rows) break;
+    const T* xr = x + row * D;
+    float ss = 0.f;
+    for (int c = lane * 8; c < D; c += 512) {
+      float v[8];
+      Vec8<T>::load(xr + c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+    }
+    const float rstd = rsqrtf(wave_sum(ss) / (float)D + p.eps);
+    if (p.rstd && lane == 0) p.rstd[row] = rstd;
+    for (int c = lane * 8; c < D; c += 512) {
+      float v[8];
+      Vec8<T>::load(xr + c, v);
+      float wv[8];
+      if (p.w) {
+        Vec8<float>::load(p.w + c, wv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wv[e] = 1.f;
+      }
+      float gv[8];
+      if (g) Vec8<T>::load(g + row * D + c, gv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] = v[e] * rstd * wv[e];
+        if (g) v[e] *= gv[e] * sigmoidf(gv[e]);
+      }
+      Vec8<T>::store(y + row * D + c, v);
+    }
+  }
+}
+
+// n = x rstd, a = n w, s = silu(g), y = a s:
+//   dg = dy a silu'(g), silu'(g) = sig(g) (1 + g (1 - sig(g)))
+//   dn = dy s w, dx = rstd (dn - n mean(dn n)), dw_part[block] = sum_rows dy s n
+template <typename T>
+__global__ __launch_bounds__(NG_NT) void norm_gate_bwd_kernel(NormGateArgs p) {
+  __shared__ float sDw[NG_NT / 64][1024];   // per-wave dw partials of a 1024-feature slab
+  const T* __restrict__ x = (const T*)p.x;
+  const T* __restrict__ g = (const T*)p.g;
+  const T* __restrict__ dy = (const T*)p.dy;
+  T* __restrict__ dx = (T*)p.dx;
+  T* __restrict__ dg = (T*)p.dg;
+  const int D = p.D, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const bool want_dw = p.w && p.dw_part;
+  for (int c0 = 0; c0 < D; c0 += 1024) {   // dw slabs: the row loop runs once per slab
+    const int cend = want_dw ? min(D, c0 + 1024) : D;   // without dw: one pass, whole rows
+    if (want_dw) {
+      for (int i = threadIdx.x; i < (NG_NT / 64) * 1024; i += NG_NT) (&sDw[0][0])[i] = 0.f;
+      __syncthreads();
+    }
+    for (long row = (long)blockIdx.x * (NG_NT / 64) + w; row < p.rows;
+         row += (long)gridDim.x * (NG_NT / 64)) {   // a wave per row, rows interleaved
+      const float rstd = p.rstd[row];
+      const T* xr = x + row * D;
+      // mean(dn n) over the whole row (every slab needs it)
+      float dot = 0.f;
+      for (int c = lane * 8; c < D; c += 512) {
+        float v[8], d[8], wv[8], gv[8];
+        Vec8<T>::load(xr + c, v);
+        Vec8<T>::load(dy + row * D + c, d);
+        if (p.w) Vec8<float>::load(p.w + c, wv);
+        if (g) Vec8<T>::load(g + row * D + c, gv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float dn = d[e] * (p.w ? wv[e] : 1.f);
+          if (g) dn *= gv[e] * sigmoidf(gv[e]);
+          dot += dn * v[e] * rstd;
+        }
+      }
+      const float mdot = wave_sum(dot) / (float)D;
+      for (int c = c0 + lane * 8; c < cend; c += 512) {
+        float v[8], d[8], wv[8], gv[8], ox[8], og[8];
+        Vec8<T>::load(xr + c, v);
+        Vec8<T>::load(dy + row * D + c, d);
+        if (p.w) Vec8<float>::load(p.w + c, wv);
+        if (g) Vec8<T>::load(g + row * D + c, gv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float n = v[e] * rstd, ww = p.w ? wv[e] : 1.f;
+          float s = 1.f;
+          if (g) {
+            const float sg = sigmoidf(gv[e]);
+            s = gv[e] * sg;
+            og[e] = d[e] * n * ww * sg * (1.f + gv[e] * (1.f - sg));
+          }
+          const float dn = d[e] * s * ww;
+          ox[e] = rstd * (dn - n * mdot);
+          if (want_dw) sDw[w][c - c0 + e] += d[e] * s * n;
+        }
+        Vec8<T>::store(dx + row * D + c, ox);
+        if (g) Vec8<T>::store(dg + row * D + c, og);
+      }
+    }
+    if (want_dw) {
+      __syncthreads();
+      for (int i = threadIdx.x; i < min(1024, D - c0); i += NG_NT) {
+        float t = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < NG_NT / 64; ++ww) t += sDw[ww][i];
+        p.dw_part[(long)blockIdx.x * D + c0 + i] = t;
+      }
+      __syncthreads();
+    }
+    if (!want_dw) break;   // without dw the first pass already wrote every slab
+  }
+}
+
+// dw[c] = sum over the partial rows: block = 64 columns, its 4 waves split the rows.
+__global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ part, int nblk,
+                                                        int D, float* __restrict__ dw) {
+  __shared__ float s[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  float t = 0.f;
+  if (c < D)
+    for (int b = w; b < nblk; b += 4) t += part[(long)b * D + c];
+  s[w][lane] = t;
+  __syncthreads();
+  if (w == 0 && c < D) dw[c] = (s[0][lane] + s[1][lane]) + (s[2][lane] + s[3][lane]);
+}
+
+// y = max(log_sigmoid(x) / n, clamp) ; dx = dy sig(-x) / n where y is not clamped.
+template <typename T>
+__global__ __launch_bounds__(256) void gate_fwd_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                       long count, float inv_n, int has_clamp,
+                                                       float clamp) {
+  const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i0 >= count) return;
+  float v[8];
+  if (i0 + 8 <= count) {
+    Vec8<T>::load(x + i0, v);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = i0 + e < count ? to_f32(x[i0 + e]) : 0.f;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    // log_sigmoid(x) = min(x, 0) - log1p(exp(-|x|))
+    float r = (fminf(v[e], 0.f) - log1pf(__expf(-fabsf(v[e])))) * inv_n;
+    if (has_clamp) r = fmaxf(r, clamp);
+    v[e] = r;
+  }
+  if (i0 + 8 <= count) {
+    Vec8<T>::store(y + i0, v);
+  } else {
+    for (int e = 0; e < 8 && i0 + e < count; ++e) y[i0 + e] = from_f32<T>(v[e]);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void gate_bwd_kernel(const T* __restrict__ x,
+                                                       const T* __restrict__ dy,
+                                                       T* __restrict__ dx, long count,
+                                                       float inv_n, int has_clamp, float clamp) {
+  const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i0 >= count) return;
+  float v[8], d[8];
+  if (i0 + 8 <= count) {
+    Vec8<T>::load(x + i0, v);
+    Vec8<T>::load(dy + i0, d);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[e] = i0 + e < count ? to_f32(x[i0 + e]) : 0.f;
+      d[e] = i0 + e < count ? to_f32(dy[i0 + e]) : 0.f;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float gr = sigmoidf(-v[e]) * inv_n;
+    if (has_clamp) {
+      const float r = (fminf(v[e], 0.f) - log1pf(__expf(-fabsf(v[e])))) * inv_n;
+      if (r < clamp) gr = 0.f;   // clamped: no gradient (jnp.clip passes none below a_min)
+    }
+    v[e] = d[e] * gr;
+  }
+  if (i0 + 8 <= count) {
+    Vec8<T>::store(dx + i0, v);
+  } else {
+    for (int e = 0; e < 8 && i0 + e < count; ++e) dx[i0 + e] = from_f32<T>(v[e]);
+  }
+}
+
+static long norm_gate_blocks(long rows) { return (rows + NG_ROWS - 1) / NG_ROWS; }
+long norm_gate_bwd_blocks(long rows) {
+  const long b = norm_gate_blocks(rows);
+  return b < NG_BWD_BLOCKS ? b : NG_BWD_BLOCKS;
+}
+
+hipError_t run_norm_gate_fwd(const NormGateArgs& p, int dtype, hipStream_t st) {
+  const long blocks = norm_gate_blocks(p.rows);
+  if (blocks == 0) return hipSuccess;
+  if (dtype == DT_BF16)
+    hipLaunchKernelGGL((norm_gate_fwd_kernel<bf16>), dim3((unsigned)blocks), dim3(NG_NT), 0, st,
+                       p);
+  else
+    hipLaunchKernelGGL((norm_gate_fwd_kernel<float>), dim3((unsigned)blocks), dim3(NG_NT), 0,
+                       st, p);
+  return hipGetLastError();
+}
+
+hipError_t run_norm_gate_bwd(const NormGateArgs& p, float* dw, int dtype, hipStream_t st) {
+  const long blocks = norm_gate_bwd_blocks(p.rows);
+  if (blocks == 0) return hipSuccess;
+  if (dtype == DT_BF16)
+    hipLaunchKernelGGL((norm_gate_bwd_kernel<bf16>), dim3((unsigned)blocks), dim3(NG_NT), 0, st,
+                       p);
+  else
+    hipLaunchKernelGGL((norm_gate_bwd_kernel<float>), dim3((unsigned)blocks), dim3(NG_NT), 0,
+                       st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !dw || !p.w || !p.dw_part) return e;
+  hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)((p.D + 63) / 64)), dim3(256), 0, st,
+                     p.dw_part, (int)blocks, p.D, dw);
+  return hipGetLastError();
+}
+
+hipError_t run_rows_sum(const float* part, int nblk, int M, float* out, hipStream_t st) {
+  if (M <= 0) return hipSuccess;
+  hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)((M + 63) / 64)), dim3(256), 0, st, part,
+                     nblk, M, out);
+  return hipGetLastError();
+}
+
+hipError_t run_gate(const void* x, const void* dy, void* out, long count, float inv_n,
+                    int has_clamp, float clamp, int dtype, hipStream_t st) {
+  const long blocks = (count + 2047) / 2048;
+  if (blocks == 0) return hipSuccess;
+  if (dy == nullptr) {
+    if (dtype == DT_BF16)
+      hipLaunchKernelGGL((gate_fwd_kernel<bf16>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const bf16*)x, (bf16*)out, count, inv_n, has_clamp, clamp);
+    else
+      hipLaunchKernelGGL((gate_fwd_kernel<float>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const float*)x, (float*)out, count, inv_n, has_clamp, clamp);
+  } else {
+    if (dtype == DT_BF16)
+      hipLaunchKernelGGL((gate_bwd_kernel<bf16>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const bf16*)x, (const bf16*)dy, (bf16*)out, count, inv_n, has_clamp,
+                         clamp);
+    else
+      hipLaunchKernelGGL((gate_bwd_kernel<float>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const float*)x, (const float*)dy, (float*)out, count, inv_n,
+                         has_clamp, clamp);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace tops

@@ -50,6 +50,16 @@ _SIGS = {
     "tops_gla_fused_recurrent_bwd": [_P] * 16 + [_F, _I, _I64, _I64, _I64, _I64, _I64, _P,
                                                  _I64, _I, _P],
     "tops_gla_full_head": [_I64, _I64, _I, _I, _I],
+    "tops_gla_rmsnorm_gated_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _F, _I, _P],
+    "tops_gla_rmsnorm_gated_bwd": [_P] * 9 + [_I64, _I64, _I64, _I, _P],
+    "tops_gla_rmsnorm_ws_bytes": [_I64, _I64],
+    "tops_gla_gate_logsigmoid_fwd": [_P, _P, _I64, _F, _I, _F, _I, _P],
+    "tops_gla_gate_logsigmoid_bwd": [_P, _P, _P, _I64, _F, _I, _F, _I, _P],
+    "tops_gla_short_conv_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _I64, _I64, _I,
+                                _P],
+    "tops_gla_short_conv_bwd": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P,
+                                _I64, _I64, _I, _P],
+    "tops_gla_short_conv_ws_bytes": [_I64, _I64, _I64, _I, _I64, _I64, _I],
     "tops_gla_bwd_part_dA": [_P, _P, _P, _F, _I64, _I64, _I64, _I64, _I, _P],
     "tops_gla_bwd_part_dv": [_P] * 6 + [_I64] * 5 + [_I, _P],
     "tops_gla_bwd_part_dqk_intra": [_P] * 6 + [_I64] * 4 + [_I, _P],
@@ -59,7 +69,9 @@ _SIGS["tops_gla_kernel_timing"] = [_I]
 _SIGS["tops_gla_kernel_ms"] = [_I]
 
 # entry points that do not return a status code
-_RESTYPE = {"tops_gla_chunk_ws_bytes": ctypes.c_int64, "tops_gla_kernel_ms": ctypes.c_float}
+_RESTYPE = {"tops_gla_chunk_ws_bytes": ctypes.c_int64, "tops_gla_kernel_ms": ctypes.c_float,
+            "tops_gla_rmsnorm_ws_bytes": ctypes.c_int64,
+            "tops_gla_short_conv_ws_bytes": ctypes.c_int64}
 
 EXPORTED = ["tops_gla_last_error", "tops_gla_version"] + list(_SIGS)
 

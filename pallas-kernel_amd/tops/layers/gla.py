@@ -1,0 +1,253 @@
+"""Gated Linear Attention layer on the MI355X kernels.
+
+Reference: ``GatedLinearAttention``, ``tops/layers/gla.py:71-345`` (a Flax NNX module); this
+is the same layer as a ``torch.nn.Module`` with the same constructor arguments, call
+signature and return convention ``(o, None, past_key_values)``. The attention core runs on
+the HIP kernels (``chunk_gla`` / ``fused_chunk_gla``, ``fused_recurrent_gla`` for q_len <= 64),
+the key-wise gate activation and the output RMSNorm * SiLU gate on their own HIP kernels,
+the projections on hipBLASLt through ``torch.nn.functional.linear``.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+
+from ..modules import FusedRMSNormGated, RMSNorm
+from ..modules._norm import GateLogSigmoidFn
+from ..modules.convolution import ShortConvolution
+from ..ops.gla import chunk_gla, fused_chunk_gla, fused_recurrent_gla
+
+__all__ = ["GatedLinearAttention", "LayerCache"]
+
+ACT2FN = {
+    "swish": F.silu,
+    "silu": F.silu,
+    "gelu": F.gelu,
+    "relu": F.relu,
+    "sigmoid": torch.sigmoid,
+    "tanh": torch.tanh,
+}
+
+
+class Linear(torch.nn.Module):
+    """Dense layer with Flax's conventions: default init lecun-normal (truncated normal,
+    std 1/sqrt(fan_in)), zero bias, and jnp-style dtype promotion of input and weight."""
+
+    def __init__(self, in_features, out_features, use_bias=False, *, generator=None,
+                 device=None, dtype=torch.float32):
+        super().__init__()
+        self.in_features, self.out_features = in_features, out_features
+        w = torch.empty(out_features, in_features, dtype=torch.float32)
+        std = 1.0 / math.sqrt(in_features) / 0.87962566103423978   # variance-preserving
+        torch.nn.init.trunc_normal_(w, std=std, a=-2 * std, b=2 * std, generator=generator)
+        self.weight = torch.nn.Parameter(w.to(device=device, dtype=dtype))
+        if use_bias:
+            self.bias = torch.nn.Parameter(torch.zeros(out_features, device=device, dtype=dtype))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x):
+        dt = torch.promote_types(x.dtype, self.weight.dtype)
+        b = None if self.bias is None else self.bias.to(dt)
+        return F.linear(x.to(dt), self.weight.to(dt), b)
+
+
+def _to_heads(x, head_dim):
+    """... (h d) -> ... h d"""
+    return x.reshape(*x.shape[:-1], x.shape[-1] // head_dim, head_dim)
+
+
+def _from_heads(x):
+    """... h d -> ... (h d)"""
+    return x.reshape(*x.shape[:-2], x.shape[-2] * x.shape[-1])
+
+
+def _repeat_kv(x, groups, head_dim):
+    """... (h d) -> ... (h g) d (reference ``_repeat_kv``, gla.py:49-66)."""
+    x = _to_heads(x, head_dim)
+    return x.unsqueeze(-2).expand(*x.shape[:-1], groups, head_dim).reshape(
+        *x.shape[:-2], x.shape[-2] * groups, head_dim)
+
+
+class LayerCache:
+    """Minimal per-layer cache with the interface the layer uses (``len``, indexing by
+    layer_idx, ``update(recurrent_state=, conv_state=, layer_idx=, offset=)``)."""
+
+    def __init__(self):
+        self.states: list[dict] = []
+        self.seen_tokens = 0
+
+    def __len__(self):
+        return len(self.states)
+
+    def __getitem__(self, i):
+        return self.states[i]
+
+    def update(self, recurrent_state=None, conv_state=None, layer_idx=0, offset=1):
+        while len(self.states) <= layer_idx:
+            self.states.append({"recurrent_state": None, "conv_state": None})
+        self.states[layer_idx] = {"recurrent_state": recurrent_state, "conv_state": conv_state}
+        if layer_idx == 0:
+            self.seen_tokens += offset
+
+
+class GatedLinearAttention(torch.nn.Module):
+    r"""Gated Linear Attention (https://arxiv.org/abs/2312.06635).
+
+    Arguments mirror ``tops/layers/gla.py:81-103``. ``rngs`` (keyword) may be an int seed or
+    a ``torch.Generator`` for the weight init; ``device`` and ``dtype`` (parameter dtype,
+    default float32 like Flax) are torch additions.
+    """
+
+    def __init__(self, mode="chunk", hidden_size=1024, expand_k=0.5, expand_v=1.0,
+                 num_heads=4, num_kv_heads=None, feature_map=None, use_short_conv=False,
+                 conv_size=4, conv_bias=False, use_output_gate=True, gate_fn="swish",
+                 elementwise_affine=True, norm_eps=1e-5, gate_logit_normalizer=16,
+                 gate_low_rank_dim=16, clamp_min=None, fuse_norm=True, layer_idx=None, *,
+                 rngs=None, device=None, dtype=torch.float32):
+        super().__init__()
+        gen = rngs if isinstance(rngs, torch.Generator) else torch.Generator().manual_seed(
+            0 if rngs is None else int(rngs))
+        self.mode = mode
+        self.hidden_size = hidden_size
+        self.expand_k = expand_k
+        self.expand_v = expand_v
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads if num_kv_heads is not None else num_heads
+        self.num_kv_groups = self.num_heads // self.num_kv_heads
+        self.feature_map_fn = ACT2FN[feature_map] if feature_map is not None else None
+        self.use_short_conv = use_short_conv
+        self.conv_size = conv_size
+        self.conv_bias = conv_bias
+        self.use_output_gate = use_output_gate
+        self.key_dim = int(hidden_size * expand_k)
+        self.value_dim = int(hidden_size * expand_v)
+        self.key_dim_per_group = self.key_dim // self.num_kv_groups
+        self.value_dim_per_group = self.value_dim // self.num_kv_groups
+        self.clamp_min = clamp_min
+        self.layer_idx = layer_idx
+
+        assert mode in ["chunk", "fused_recurrent", "fused_chunk"], \
+            f"Not supported mode `{mode}`."
+        assert self.key_dim % num_heads == 0, \
+            f"key dim must be divisible by num_heads of {num_heads}"
+        assert self.value_dim % num_heads == 0, \
+            f"value dim must be divisible by num_heads of {num_heads}"
+        self.head_k_dim = self.key_dim // num_heads
+        self.head_v_dim = self.value_dim // num_heads
+
+        lin = lambda i, o, b=False: Linear(i, o, b, generator=gen, device=device,  # noqa: E731
+                                           dtype=dtype)
+        self.q_proj = lin(hidden_size, self.key_dim)
+        self.k_proj = lin(hidden_size, self.key_dim_per_group)
+        self.v_proj = lin(hidden_size, self.value_dim_per_group)
+        if self.use_output_gate:
+            self.g_proj = lin(hidden_size, self.value_dim)
+        if use_short_conv:
+            conv = lambda d: ShortConvolution(d, conv_size, bias=conv_bias,  # noqa: E731
+                                              activation="silu", rngs=gen, device=device,
+                                              dtype=dtype)
+            self.q_conv1d = conv(self.key_dim)
+            self.k_conv1d = conv(self.key_dim_per_group)
+            self.v_conv1d = conv(self.value_dim_per_group)
+        self.gk_proj = torch.nn.Sequential(lin(hidden_size, gate_low_rank_dim),
+                                           lin(gate_low_rank_dim, self.key_dim_per_group, True))
+        self.o_proj = lin(self.value_dim, hidden_size)
+        if gate_fn == "swish" and fuse_norm and use_output_gate:
+            self.g_norm_swish_gate = FusedRMSNormGated(self.head_v_dim, elementwise_affine,
+                                                       norm_eps, device=device)
+            self.fuse_norm_and_gate = True
+        else:
+            self.fuse_norm_and_gate = False
+            self.g_norm = RMSNorm(self.head_v_dim, elementwise_affine, norm_eps, device=device)
+            self.gate_fn_act = ACT2FN[gate_fn]
+        self.gate_logit_normalizer = gate_logit_normalizer
+
+    def forward(self, hidden_states, attention_mask=None, past_key_values: Any | None = None,
+                use_cache=False, output_attentions=False, **kwargs):
+        """Reference: ``GatedLinearAttention.__call__``, ``tops/layers/gla.py:224-345``."""
+        if attention_mask is not None:
+            assert attention_mask.dim() == 2, \
+                "Expected attention_mask as a 0-1 matrix with shape [batch_size, seq_len]."
+        batch_size, q_len, _ = hidden_states.shape
+        mode = "fused_recurrent" if q_len <= 64 else self.mode
+
+        last_state = None
+        if past_key_values is not None and len(past_key_values) > self.layer_idx:
+            last_state = past_key_values[self.layer_idx]
+        cu_seqlens = kwargs.get("cu_seqlens")
+        chunk_size = 16
+
+        conv_state_q = conv_state_k = conv_state_v = None
+        if self.use_short_conv:
+            if last_state is not None and last_state.get("conv_state") is not None:
+                conv_state_q, conv_state_k, conv_state_v = last_state["conv_state"]
+            q, conv_state_q = self.q_conv1d(self.q_proj(hidden_states), cache=conv_state_q,
+                                            output_final_state=use_cache, cu_seqlens=cu_seqlens)
+            k, conv_state_k = self.k_conv1d(self.k_proj(hidden_states), cache=conv_state_k,
+                                            output_final_state=use_cache, cu_seqlens=cu_seqlens)
+            v, conv_state_v = self.v_conv1d(self.v_proj(hidden_states), cache=conv_state_v,
+                                            output_final_state=use_cache, cu_seqlens=cu_seqlens)
+        else:
+            q = self.q_proj(hidden_states)
+            k = self.k_proj(hidden_states)
+            v = self.v_proj(hidden_states)
+        gk = self.gk_proj(hidden_states)
+
+        q = _to_heads(q, self.head_k_dim)
+        if self.num_kv_groups > 1:
+            k = _repeat_kv(k, self.num_kv_groups, self.head_k_dim)
+            gk = _repeat_kv(gk, self.num_kv_groups, self.head_k_dim)
+            v = _repeat_kv(v, self.num_kv_groups, self.head_v_dim)
+        else:
+            k = _to_heads(k, self.head_k_dim)
+            gk = _to_heads(gk, self.head_k_dim)
+            v = _to_heads(v, self.head_v_dim)
+
+        gk = GateLogSigmoidFn.apply(gk, self.gate_logit_normalizer, self.clamp_min)
+
+        if self.feature_map_fn is not None:
+            q = self.feature_map_fn(q)
+            k = self.feature_map_fn(k)
+
+        recurrent_state = last_state["recurrent_state"] if last_state is not None else None
+        if mode == "fused_recurrent":
+            o, recurrent_state = fused_recurrent_gla(q=q, k=k, v=v, gk=gk,
+                                                     initial_state=recurrent_state,
+                                                     output_final_state=use_cache,
+                                                     cu_seqlens=cu_seqlens)
+        elif mode == "fused_chunk":
+            o, recurrent_state = fused_chunk_gla(q=q, k=k, v=v, g=gk,
+                                                 initial_state=recurrent_state,
+                                                 output_final_state=use_cache,
+                                                 cu_seqlens=cu_seqlens)
+        elif mode == "chunk":
+            o, recurrent_state = chunk_gla(q=q, k=k, v=v, g=gk, initial_state=recurrent_state,
+                                           output_final_state=use_cache, cu_seqlens=cu_seqlens,
+                                           chunk_size=chunk_size)
+        else:
+            raise NotImplementedError(f"Not supported mode `{mode}`.")
+
+        if past_key_values is not None:
+            past_key_values.update(
+                recurrent_state=recurrent_state,
+                conv_state=(conv_state_q, conv_state_k, conv_state_v)
+                if self.use_short_conv else None,
+                layer_idx=self.layer_idx, offset=q_len)
+
+        if self.use_output_gate:
+            g = self.g_proj(hidden_states)
+            if self.fuse_norm_and_gate:
+                g = _to_heads(g, self.head_v_dim)
+                o = _from_heads(self.g_norm_swish_gate(o, g))
+            else:
+                o = _from_heads(self.g_norm(o))
+                o = o * self.gate_fn_act(g)
+        else:
+            o = _from_heads(self.g_norm(o))
+        o = self.o_proj(o)
+        return o, None, past_key_values

@@ -32,7 +32,7 @@ def _declared():
 
 def test_header_lists_entry_points():
     decl = _declared()
-    assert len(decl) == 20, decl
+    assert len(decl) == 28, decl
     assert set(decl) == set(_lib.EXPORTED)
 
 

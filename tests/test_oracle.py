@@ -399,3 +399,73 @@ def test_fused_recurrent_bwd_equals_autograd(gate, reverse):
             assert y is None, name
             continue
         np.testing.assert_allclose(x, y, rtol=1e-9, atol=1e-9, err_msg=name)
+
+
+# ---------------------------------------------------------------------------
+# the layer restatement (oracle/layer.py)
+# ---------------------------------------------------------------------------
+
+
+def test_layer_recurrence_matches_numpy_naive():
+    """The torch recurrence of the layer oracle equals the pinned numpy naive recurrence."""
+    import torch
+
+    from oracle import layer as L
+
+    r = np.random.default_rng(31)
+    B, T, H, K, V = 2, 9, 2, 4, 3
+    q, k = r.standard_normal((2, B, T, H, K))
+    v = r.standard_normal((B, T, H, V))
+    g = -np.logaddexp(0.0, -r.standard_normal((B, T, H, K)))
+    s0 = r.standard_normal((B, H, K, V))
+    t = lambda x: torch.tensor(x, dtype=torch.float64)  # noqa: E731
+    o, ht = L.recurrence(t(q), t(k), t(v), t(g), 0.5, t(s0))
+    on, hn = orc.naive_recurrent_gla(q, k, v, g, scale=0.5, initial_state=s0,
+                                     output_final_state=True)
+    np.testing.assert_allclose(o.numpy(), on, atol=1e-12)
+    np.testing.assert_allclose(ht.numpy(), hn, atol=1e-12)
+    cu = [0, 4, 9]
+    o2, h2 = L.recurrence(t(q[:1]), t(k[:1]), t(v[:1]), t(g[:1]), 0.5, t(s0), cu)
+    on2, hn2 = orc.naive_recurrent_gla(q[:1], k[:1], v[:1], g[:1], scale=0.5, initial_state=s0,
+                                       output_final_state=True, cu_seqlens=cu)
+    np.testing.assert_allclose(o2.numpy(), on2, atol=1e-12)
+    np.testing.assert_allclose(h2.numpy(), hn2, atol=1e-12)
+
+
+def test_layer_norm_gate_and_conv_closed_forms():
+    import torch
+    import torch.nn.functional as F
+
+    from oracle import layer as L
+
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(5, 16, generator=g, dtype=torch.float64)
+    y = L.rms_norm(x, eps=0.0)
+    np.testing.assert_allclose((y * y).mean(-1).numpy(), 1.0, atol=1e-12)   # unit RMS rows
+    gate = torch.randn(5, 16, generator=g, dtype=torch.float64)
+    np.testing.assert_allclose(L.rms_norm(x, None, 0.0, gate).numpy(),
+                               (y * gate * torch.sigmoid(gate)).numpy(), atol=1e-12)
+    # log_sigmoid gate: log(1/(1+e^-x)) / n, clipped
+    z = torch.linspace(-30, 30, 61, dtype=torch.float64)
+    np.testing.assert_allclose(L.gate_logsigmoid(z, 16).numpy(),
+                               (-np.log1p(np.exp(-z.numpy())) / 16), atol=1e-12)
+    assert float(L.gate_logsigmoid(z, 16, -0.5).min()) == -0.5
+    # causal depthwise conv == brute-force taps over the zero-padded past
+    W, D, T = 3, 4, 7
+    xx = torch.randn(2, T, D, generator=g, dtype=torch.float64)
+    w = torch.randn(D, 1, W, generator=g, dtype=torch.float64)
+    b = torch.randn(D, generator=g, dtype=torch.float64)
+    yy = L.short_conv(xx, w, b, activation=None)
+    ref = torch.zeros_like(xx)
+    for t in range(T):
+        for j in range(W):
+            ts = t - W + 1 + j
+            if ts >= 0:
+                ref[:, t] += w[:, 0, j] * xx[:, ts]
+    ref += b
+    np.testing.assert_allclose(yy.numpy(), ref.numpy(), atol=1e-12)
+    # varlen restarts at every sequence
+    yv = L.short_conv(xx[:1], w, b, activation=None, cu_seqlens=[0, 3, 7])
+    np.testing.assert_allclose(yv[:, 3:].numpy(), L.short_conv(xx[:1, 3:], w, b, None).numpy(),
+                               atol=1e-12)
+    assert torch.allclose(L.short_conv(xx, w, b, "silu"), F.silu(yy))
