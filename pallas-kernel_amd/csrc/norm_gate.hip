@@ -181,14 +181,16 @@ __global__ __launch_bounds__(NG_NT) void norm_gate_bwd_kernel(NormGateArgs p) {
 }
 
 // dw[c] = sum over the partial rows: block = 64 columns, its 4 waves split the rows.
+// (rows b of part are `stride` floats apart; columns c < D are summed)
 __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ part, int nblk,
-                                                        int D, float* __restrict__ dw) {
+                                                        int D, long stride,
+                                                        float* __restrict__ dw) {
   __shared__ float s[4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
   float t = 0.f;
   if (c < D)
-    for (int b = w; b < nblk; b += 4) t += part[(long)b * D + c];
+    for (int b = w; b < nblk; b += 4) t += part[(long)b * stride + c];
   s[w][lane] = t;
   __syncthreads();
   if (w == 0 && c < D) dw[c] = (s[0][lane] + s[1][lane]) + (s[2][lane] + s[3][lane]);
@@ -210,8 +212,9 @@ __global__ __launch_bounds__(256) void gate_fwd_kernel(const T* __restrict__ x, 
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    // log_sigmoid(x) = min(x, 0) - log1p(exp(-|x|))
-    float r = (fminf(v[e], 0.f) - log1pf(__expf(-fabsf(v[e])))) * inv_n;
+    // log_sigmoid(x) = min(x, 0) - log(1 + exp(-|x|)) (hardware exp / log: the second term
+    // is below 1 ulp of the first wherever 1 + exp(-|x|) rounds to 1)
+    float r = (fminf(v[e], 0.f) - __logf(1.f + __expf(-fabsf(v[e])))) * inv_n;
     if (has_clamp) r = fmaxf(r, clamp);
     v[e] = r;
   }
@@ -244,7 +247,7 @@ __global__ __launch_bounds__(256) void gate_bwd_kernel(const T* __restrict__ x,
   for (int e = 0; e < 8; ++e) {
     float gr = sigmoidf(-v[e]) * inv_n;
     if (has_clamp) {
-      const float r = (fminf(v[e], 0.f) - log1pf(__expf(-fabsf(v[e])))) * inv_n;
+      const float r = (fminf(v[e], 0.f) - __logf(1.f + __expf(-fabsf(v[e])))) * inv_n;
       if (r < clamp) gr = 0.f;   // clamped: no gradient (jnp.clip passes none below a_min)
     }
     v[e] = d[e] * gr;
@@ -285,15 +288,41 @@ hipError_t run_norm_gate_bwd(const NormGateArgs& p, float* dw, int dtype, hipStr
                        st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !dw || !p.w || !p.dw_part) return e;
-  hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)((p.D + 63) / 64)), dim3(256), 0, st,
-                     p.dw_part, (int)blocks, p.D, dw);
-  return hipGetLastError();
+  return run_rows_sum(p.dw_part, (int)blocks, p.D, dw, st);
+}
+
+// Many partial rows: each of G groups of rows is summed by its own blocks into a second-level
+// row (written over the group's first row), then the G rows are summed.
+__global__ __launch_bounds__(256) void rows_sum_stage_kernel(float* __restrict__ part, int nblk,
+                                                             int M, int per) {
+  __shared__ float s[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane, grp = blockIdx.y;
+  const int b0 = grp * per, b1 = min(nblk, b0 + per);
+  float t = 0.f;
+  if (c < M)
+    for (int b = b0 + w; b < b1; b += 4) t += part[(long)b * M + c];
+  s[w][lane] = t;
+  __syncthreads();
+  if (w == 0 && c < M) part[(long)b0 * M + c] = (s[0][lane] + s[1][lane]) + (s[2][lane] + s[3][lane]);
 }
 
 hipError_t run_rows_sum(const float* part, int nblk, int M, float* out, hipStream_t st) {
   if (M <= 0) return hipSuccess;
-  hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)((M + 63) / 64)), dim3(256), 0, st, part,
-                     nblk, M, out);
+  const unsigned cb = (unsigned)((M + 63) / 64);
+  if (nblk > 64) {
+    const int per = 64, groups = (nblk + per - 1) / per;
+    float* p = const_cast<float*>(part);
+    hipLaunchKernelGGL(rows_sum_stage_kernel, dim3(cb, (unsigned)groups), dim3(256), 0, st, p,
+                       nblk, M, per);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // the group sums sit in rows 0, per, 2 per, ...: a row stride of per * M
+    hipLaunchKernelGGL(dw_reduce_kernel, dim3(cb), dim3(256), 0, st, part, groups, M,
+                       (long)per * M, out);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(dw_reduce_kernel, dim3(cb), dim3(256), 0, st, part, nblk, M, (long)M, out);
   return hipGetLastError();
 }
 

@@ -130,9 +130,19 @@ def seg_workspace(B, T, H, K, V, chunk, varlen, dtype, device):
     return torch.empty(n, dtype=torch.uint8, device=device), n
 
 
+class _DevPtr(ctypes.c_void_p):
+    """A tensor's device pointer that keeps the tensor alive: ``ptr(x.contiguous())`` inside
+    an argument list must not let a temporary go back to the caching allocator (and be
+    handed to the next temporary) before the entry point has enqueued its kernels."""
+
+
 def ptr(t):
-    """Device pointer of a tensor (None -> NULL)."""
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """Device pointer of a tensor (None -> NULL); holds a reference to the tensor."""
+    if t is None:
+        return None
+    p = _DevPtr(t.data_ptr())
+    p.tensor = t
+    return p
 
 
 def dtype_code(dt):

@@ -182,21 +182,21 @@ class GatedLinearAttention(torch.nn.Module):
         cu_seqlens = kwargs.get("cu_seqlens")
         chunk_size = 16
 
+        q = self.q_proj(hidden_states)
+        k = self.k_proj(hidden_states)
+        v = self.v_proj(hidden_states)
+        gk = self.gk_proj(hidden_states)
+
         conv_state_q = conv_state_k = conv_state_v = None
         if self.use_short_conv:
             if last_state is not None and last_state.get("conv_state") is not None:
                 conv_state_q, conv_state_k, conv_state_v = last_state["conv_state"]
-            q, conv_state_q = self.q_conv1d(self.q_proj(hidden_states), cache=conv_state_q,
-                                            output_final_state=use_cache, cu_seqlens=cu_seqlens)
-            k, conv_state_k = self.k_conv1d(self.k_proj(hidden_states), cache=conv_state_k,
-                                            output_final_state=use_cache, cu_seqlens=cu_seqlens)
-            v, conv_state_v = self.v_conv1d(self.v_proj(hidden_states), cache=conv_state_v,
-                                            output_final_state=use_cache, cu_seqlens=cu_seqlens)
-        else:
-            q = self.q_proj(hidden_states)
-            k = self.k_proj(hidden_states)
-            v = self.v_proj(hidden_states)
-        gk = self.gk_proj(hidden_states)
+            q, conv_state_q = self.q_conv1d(q, cache=conv_state_q, output_final_state=use_cache,
+                                            cu_seqlens=cu_seqlens)
+            k, conv_state_k = self.k_conv1d(k, cache=conv_state_k, output_final_state=use_cache,
+                                            cu_seqlens=cu_seqlens)
+            v, conv_state_v = self.v_conv1d(v, cache=conv_state_v, output_final_state=use_cache,
+                                            cu_seqlens=cu_seqlens)
 
         q = _to_heads(q, self.head_k_dim)
         if self.num_kv_groups > 1:

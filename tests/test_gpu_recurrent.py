@@ -279,3 +279,27 @@ def test_fused_recurrent_bwd_c2_shape_slices():
             if r_ is not None:
                 gs = st(g_) if name == "dh0" else sl(g_)
                 check(name, gs, r_, "f32", atol=1e-4 * max(1.0, float(np.abs(r_).max())))
+
+
+def test_non_contiguous_inputs():
+    """Strided views (the layer's split projections) as inputs: the host layer's contiguous
+    copies must stay alive until the kernels are enqueued (regression: temporaries passed as
+    device pointers were freed and their memory reused by the next copy)."""
+    import tops.ops.gla as G
+
+    r = np.random.default_rng(77)
+    B, T, H, K, V = 2, 40, 2, 16, 32
+    big = r.standard_normal((B, T, H, 2 * K + V + K)).astype(np.float32)
+    q, k, v, gk = (big[..., :K], big[..., K:2 * K], big[..., 2 * K:2 * K + V],
+                   logsigmoid(big[..., 2 * K + V:]))
+    s0 = r.standard_normal((B, H, K, V))
+    d = torch.tensor(big).cuda()
+    dq, dk, dv = d[..., :K], d[..., K:2 * K], d[..., 2 * K:2 * K + V]
+    dg = torch.nn.functional.logsigmoid(d[..., 2 * K + V:])
+    assert not dq.is_contiguous()
+    o, ht = G.fused_recurrent_gla(dq, dk, dv, gk=dg, initial_state=to_dev(s0, "state"),
+                                  output_final_state=True)
+    torch.cuda.synchronize()
+    on, hn = orc.fused_recurrent_gla(q, k, v, gk=gk, initial_state=s0, output_final_state=True)
+    check("o", to_np(o), on, "f32", atol=1e-4 * max(1.0, float(np.abs(on).max())))
+    check("ht", to_np(ht), hn, "f32", atol=1e-4 * max(1.0, float(np.abs(hn).max())))
