@@ -1185,7 +1185,9 @@ void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL, in
   if (varlen || N <= 0 || H <= 0) return;
   const int nt = (T + C - 1) / C;
   const long nh = (long)N * H * (VT > 0 ? VT : 1);
-  const long want = (512 + nh - 1) / nh;   // about two blocks per CU
+  // one block per CU (MI355X: 256 CUs): the full-head kernels hold one block per CU (LDS),
+  // so a second round of blocks would run as a tail
+  const long want = 256 / nh;
   long ns = want < nt / 8 ? want : nt / 8;                     // segments of >= 8 chunks
   if (ns <= 1) return;
   SL = (int)((nt + ns - 1) / ns);

@@ -163,15 +163,16 @@ def test_segment_workspace_query():
     """Host-only: the segment workspace covers [N, NS, H, K, V] f32 states + decays."""
     lib = _lib.load()
     q = lib.tops_gla_chunk_ws_bytes
-    # B4 T8192 H16 K=V=128 chunk 64 bf16: 128 chunks per sequence, 8 segments of 16
-    st = 4 * 8 * 16 * 128 * 128 * 4
-    gm = 4 * 8 * 16 * 128 * 4
+    # B4 T8192 H16 K=V=128 chunk 64 bf16: 128 chunks per sequence; 64 (sequence, head) blocks
+    # -> 4 segments of 32 chunks (one block per CU of 256)
+    st = 4 * 4 * 16 * 128 * 128 * 4
+    gm = 4 * 4 * 16 * 128 * 4
     assert q(4, 8192, 16, 128, 128, 64, 0, 1) == st + (gm + 255) // 256 * 256
     assert q(4, 8192, 16, 128, 128, 64, 1, 1) == 0      # varlen: unsegmented
     assert q(4, 8192, 16, 128, 128, 64, 0, 0) == 0      # float32: other kernels
     assert q(4, 8192, 16, 128, 128, 32, 0, 1) == 0      # chunk 32: other kernels
     assert q(1, 256, 2, 64, 64, 64, 0, 1) == 0          # 4 chunks: too short to split
-    # K = 256: V tiles of 64 columns (2 per head) -> 4 segments of 32 chunks
-    st2, gm2 = 4 * 4 * 16 * 256 * 128 * 4, 4 * 4 * 16 * 256 * 4
+    # K = 256: V tiles of 64 columns (2 per head) -> 2 segments of 64 chunks
+    st2, gm2 = 4 * 2 * 16 * 256 * 128 * 4, 4 * 2 * 16 * 256 * 4
     assert q(4, 8192, 16, 256, 128, 64, 0, 1) == st2 + (gm2 + 255) // 256 * 256
     assert q(4, 8192, 16, 320, 128, 64, 0, 1) == 0      # K > 256: other kernels
