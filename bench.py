@@ -3,7 +3,7 @@
 chunk 64, h0 and dht (its headline metric).
 
 One step = chunk_gla forward (o, ht) + backward (dq, dk, dv, dg, dh0) on synthetic inputs
-already resident in HBM (numpy default_rng(seed=4), draw order
+already resident in HBM (the benchmark's input recipe: numpy default_rng(seed=4), draw order
 q, k, v, g_raw, h0, do, dht; g = logsigmoid(g_raw) / 16; h0, dht ~ N(0, 0.1^2)).
 
 Prints ONE JSON line with the driver's fields plus
@@ -38,7 +38,8 @@ SEED = 4
 METRIC = "chunk_gla fwd+bwd tokens/s & % bf16 MFMA peak, B4 T8192 H16 K=V=128"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK = 2.517e15
-# algorithmic flops per token-head: fwd 4KV + 2C(K+V), bwd twice that
+# algorithmic flops per token-head (full C x C tiles, no recompute): fwd 4KV + 2C(K+V), bwd
+# twice that
 FLOPS_STEP = B * T * H * (12 * K * V + 6 * C * (K + V))
 # state traffic (h/dht fp32) counted once per use
 STATE_BYTES = B * H * K * V * 4

@@ -5,7 +5,7 @@
  * primatrix/pallas-kernel). The reference has no native boundary: its Python functions
  * lower to `pl.pallas_call` custom calls. Each entry point below replaces one of those
  * launch sites (cited per function) and is what an XLA typed-FFI handler or a ctypes
- * binding calls (see INTEGRATION.md).
+ * binding calls.
  *
  * Conventions (all entry points):
  *  - Tensors are device pointers (HBM), row-major, in the reference layout: q/k/g

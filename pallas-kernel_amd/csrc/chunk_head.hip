@@ -717,14 +717,15 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 // Reference: chunk_gla_bwd_with_pl, tops/ops/gla/chunk.py:1019-1064 (dh scan
 // chunk_h.py:495-591, fused gradients chunk.py:1423-1479). Per chunk, base-2 gates,
 // r = (g~_first + gamma) / 2 per column, fr = scale 2^r, fe = 2^{gamma-r}:
-//   qg = q 2^{g~-r}, kg = k 2^{r-g~}, kd = k 2^{gamma-g~}
+//   qg = q 2^{g~-r}, kg = k 2^{r-g~}, dh' = fe (.) dh (rows k; kd = k 2^{gamma-g~} = kg fe)
 //   A = scale tril(qg kg^T), dA = scale tril(do v^T)
-//   dv = A^T do + kd dh
+//   dv = A^T do + kg dh'
 //   dq = 2^{g~-r} [dA kg + fr do h^T]
-//   dk = 2^{r-g~} [dA^T qg + fe v dh^T]
-//   dg = revcumsum_rows(q dq - k dk) + 2^gamma sum_v h dh + sum_v dh (kd^T v)
+//   dk = 2^{r-g~} [dA^T qg + v dh'^T]
+//   dg = revcumsum_rows(q dq - k dk) + 2^r sum_v h dh' + sum_rows kg (.) (v dh'^T)
 //   dh <- 2^gamma dh + (scale q 2^{g~})^T do
-// (the last dg term is sum_rows k dk_inter, reduced from the dh accumulators.)
+// (2^r sum_v h dh' = 2^gamma sum_v h dh; the last term is sum_rows k dk_inter, summed from
+// the dk pre-factor while it is still in registers.)
 // h (state entering the chunk) comes from the forward's per-chunk states; its MFMA
 // fragments are read straight from HBM (16 bytes per lane).
 // Waves: dq/dk own KTW k tiles x RT row tiles, dv^T VTW v tiles x JT row tiles, dh as in
@@ -738,26 +739,26 @@ struct HBLayout {
                        PA = pitch_of<bf16>(HC);
   static constexpr int PX = KP + 4;                // fp32 exchange pitch
   // small fp32 arrays first: the exchange aliases the tiles only
+  // row groups of the dq / dk tiles (waves sharing a k tile)
+  static constexpr int NKT = KP / 16, KTW = NKT > NW ? NKT / NW : 1, NRG = NW / (NKT / KTW);
   static constexpr int tot = 0;                    // [NW][KP] cumsum wave totals
   static constexpr int suf = tot + NW * KP * 4;    // [NW][KP] dg suffix wave totals
   static constexpr int first = suf + NW * KP * 4;
-  static constexpr int eg = first + KP * 4;        // 2^gamma
-  static constexpr int fr = eg + KP * 4;           // scale 2^r
+  static constexpr int fr = first + KP * 4;        // scale 2^r
   static constexpr int fe = fr + KP * 4;           // 2^{gamma-r}
-  static constexpr int hd = fe + KP * 4;           // sum_v h dh
-  static constexpr int dkc = hd + KP * 4;          // [2][KP] sum_v dh (kd^T v), per v half
-  static constexpr int qg = dkc + 2 * KP * 4;
+  static constexpr int hd = fe + KP * 4;           // 2^gamma sum_v h dh
+  static constexpr int dkc = hd + KP * 4;          // [NRG][KP] sum_rows kg (v dh'^T)
+  static constexpr int qg = dkc + NRG * KP * 4;
   static constexpr int kg = qg + HC * PKP * 2;
-  static constexpr int kd = kg + HC * PKP * 2;
-  static constexpr int v = kd + HC * PKP * 2;
+  static constexpr int v = kg + HC * PKP * 2;
   static constexpr int dout = v + HC * PVP * 2;
-  static constexpr int dh = dout + HC * PVP * 2;   // dh [k][v] bf16
+  static constexpr int dh = dout + HC * PVP * 2;   // dh' [k][v] bf16
   static constexpr int a = dh + KP * PVP * 2;
   static constexpr int da = a + HC * PA * 2;
   static constexpr int end_tiles = da + HC * PA * 2;
-  // exchange [HC][PX] x 2 from kd on (qg, kg stay intact for the epilogue); it may reach
+  // exchange [HC][PX] x 2 from v on (qg, kg stay intact for the epilogue); it may reach
   // A / dA, which are therefore rewritten in full (zero upper tiles) every chunk
-  static constexpr int xq = kd;
+  static constexpr int xq = v;
   static constexpr int xk = xq + HC * PX * 4;
   static constexpr int end_x = xk + HC * PX * 4;
   static constexpr int bytes = end_tiles > end_x ? end_tiles : end_x;
@@ -778,20 +779,19 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   constexpr int KTW = NKT > NW ? NKT / NW : 1, NKG = NKT / KTW, RT = 4 * NKG / NW;
   constexpr int VTW = NVT > NW ? NVT / NW : 1, NVG = NVT / VTW, JT = 4 * NVG / NW;
   static_assert(NTK >= 1 && RT >= 1 && JT >= 1, "tile split");
+  static_assert(Lay::NRG == NW / NKG, "row groups of the dq / dk tiles");
   constexpr int NHF = VP / 32;                      // h fragments per lane
   static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* sTot = reinterpret_cast<float*>(smem + Lay::tot);
   float* sSuf = reinterpret_cast<float*>(smem + Lay::suf);
   float* sFirst = reinterpret_cast<float*>(smem + Lay::first);
-  float* sEg = reinterpret_cast<float*>(smem + Lay::eg);
   float* sFr = reinterpret_cast<float*>(smem + Lay::fr);
   float* sFe = reinterpret_cast<float*>(smem + Lay::fe);
   float* sHd = reinterpret_cast<float*>(smem + Lay::hd);
   float* sDkc = reinterpret_cast<float*>(smem + Lay::dkc);
   bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
   bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
-  bf16* sKd = reinterpret_cast<bf16*>(smem + Lay::kd);
   bf16* sV = reinterpret_cast<bf16*>(smem + Lay::v);
   bf16* sDo = reinterpret_cast<bf16*>(smem + Lay::dout);
   bf16* sDh = reinterpret_cast<bf16*>(smem + Lay::dh);
@@ -872,16 +872,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
     issue_main(step);
     issue_h(step);
 
-    // ---- (1) dh to LDS, cumsum, gating ----
-#pragma unroll
-    for (int j = 0; j < NTK; ++j)
-#pragma unroll
-      for (int i = 0; i < NTV; ++i) {
-        const int kk = (kt0 + j) * 16 + (lane & 15), vv = (vt0 + i) * 16 + 4 * (lane >> 4);
-        *reinterpret_cast<uint2*>(sDh + kk * PVP + vv) =
-            make_uint2(pack2_bf16(acc[i][j][0], acc[i][j][1]),
-                       pack2_bf16(acc[i][j][2], acc[i][j][3]));
-      }
+    // ---- (1) cumsum, gating; dh' = fe (.) dh to LDS ----
     float dd[RPT][8];   // g~ - r (base 2)
     {
       uint4 gmk[RPT], qm[RPT], km[RPT];
@@ -894,25 +885,39 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       }
       float gam[8], first[8];
       head_cumsum<KP, NT>(gmk, dd, gam, first, sTot, sFirst, cg, rs, lane, w);
+      // gamma of this lane's dh rows from the wave totals (same order of sums as gam)
+#pragma unroll
+      for (int j = 0; j < NTK; ++j) {
+        const int kk = (kt0 + j) * 16 + (lane & 15);
+        float gk = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) gk += sTot[ww * KP + kk];
+        const float fe = exp2_hw(0.5f * (gk - sFirst[kk]));
+#pragma unroll
+        for (int i = 0; i < NTV; ++i) {
+          const int vv = (vt0 + i) * 16 + 4 * (lane >> 4);
+          *reinterpret_cast<uint2*>(sDh + kk * PVP + vv) =
+              make_uint2(pack2_bf16(acc[i][j][0] * fe, acc[i][j][1] * fe),
+                         pack2_bf16(acc[i][j][2] * fe, acc[i][j][3] * fe));
+        }
+      }
       float r[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = 0.5f * (first[e] + gam[e]);
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
         const int row = rs * RPT + j;
-        float xq[8], xk[8], xd[8];
+        float xq[8], xk[8];
         unpack8(qm[j], xq);
         unpack8(km[j], xk);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          xd[e] = xk[e] * exp2_hw(gam[e] - dd[j][e]);
           dd[j][e] -= r[e];
           xq[e] *= exp2_hw(dd[j][e]);
           xk[e] *= exp2_hw(-dd[j][e]);
         }
         *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pack8(xq);
         *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pack8(xk);
-        *reinterpret_cast<uint4*>(sKd + row * PKP + cg * 8) = pack8(xd);
       }
 #pragma unroll
       for (int j = 0; j < VRPT; ++j) {
@@ -922,14 +927,12 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         *reinterpret_cast<uint4*>(sDo + row * PVP + vg * 8) = mask16(Rd[j], m);
       }
       if (rs == 0) {
-        float a8[8], b8[8], c8[8];
+        float b8[8], c8[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          a8[e] = exp2_hw(gam[e]);
           b8[e] = p.scale * exp2_hw(r[e]);
-          c8[e] = exp2_hw(gam[e] - r[e]);
+          c8[e] = exp2_hw(0.5f * (gam[e] - first[e]));
         }
-        st_f8(sEg + cg * 8, a8);
         st_f8(sFr + cg * 8, b8);
         st_f8(sFe + cg * 8, c8);
       }
@@ -955,9 +958,9 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         dst[ii * PA + jj] = from_f32<bf16>(jj <= ii ? at[rr] * p.scale : 0.f);
       }
     }
-    // dq pre: fr do h^T (h fragments from HBM); dk pre: fe v dh^T
+    // dq pre: fr do h^T (h fragments from HBM); dk pre: v dh'^T
     f32x4 aq[KTW][RT], ak[KTW][RT];
-    float hdp[KTW];
+    float hdp[KTW], dkc[KTW];
 #pragma unroll
     for (int t = 0; t < KTW; ++t) {
       const int hk = (kq0 + t) * 16 + (lane & 15);
@@ -985,58 +988,77 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       }
       hdp[t] += __shfl_xor(hdp[t], 16);
       hdp[t] += __shfl_xor(hdp[t], 32);
-      const float fr = sFr[hk], fe = sFe[hk];
+      const float fr = sFr[hk];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) aq[t][i] *= fr;
+      // sum over this wave's rows of kg (.) ak: kg read in the accumulator layout (rows
+      // 4 (lane >> 4) + 0..3 of column lane & 15 of each 16 x 16 tile) by transposed reads
+      dkc[t] = 0.f;
 #pragma unroll
       for (int i = 0; i < RT; ++i) {
-        aq[t][i] *= fr;
-        ak[t][i] *= fe;
+        const bf16* pk = sKg + ((rt0 + i) * 16 + 4 * (lane >> 4) + ((lane & 15) >> 2)) * PKP +
+                         (kq0 + t) * 16 + 4 * (lane & 3);
+        const s4_t kv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s4_t*)(pk));
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          dkc[t] += __uint_as_float((uint32_t)(uint16_t)kv[rr] << 16) * ak[t][i][rr];
       }
+      dkc[t] += __shfl_xor(dkc[t], 16);
+      dkc[t] += __shfl_xor(dkc[t], 32);
     }
 
-    // sum_v dh (kd^T v) per k, from the dh accumulators (before their update)
-    float dkc[NTK];
-#pragma unroll
-    for (int j = 0; j < NTK; ++j) {
-      dkc[j] = 0.f;
-#pragma unroll
-      for (int i = 0; i < NTV; ++i) {
-        f32x4 u = zero4();
-        mma_tile2<bf16, true, true>(u, sV + (vt0 + i) * 16, PVP, sKd + (kt0 + j) * 16, PKP, HC,
-                                    lane);
-        dkc[j] += acc[i][j][0] * u[0] + acc[i][j][1] * u[1] + acc[i][j][2] * u[2] +
-                  acc[i][j][3] * u[3];
-      }
-      dkc[j] += __shfl_xor(dkc[j], 16);
-      dkc[j] += __shfl_xor(dkc[j], 32);
-    }
     __syncthreads();
 
     // ---- (3) products with A / dA; dv out; dh update ----
+    // (operand fragments shared by a wave's tiles are read once)
 #pragma unroll
-    for (int t = 0; t < KTW; ++t)
+    for (int t = 0; t < KTW; ++t) {
+      const int kq = kq0 + t;
+      Frag<bf16> fk[HC / 32], fq[HC / 32];   // kg^T, qg^T of this k tile
 #pragma unroll
-      for (int i = 0; i < RT; ++i) {
-        const int ro = (rt0 + i) * 16, kq = kq0 + t;
-        // dq += dA kg (kg read transposed); dk += dA^T qg (both read transposed)
-        mma_tile2<bf16, false, true>(aq[t][i], sdA + ro * PA, PA, sKg + kq * 16, PKP, HC, lane);
-        mma_tile2<bf16, true, true>(ak[t][i], sdA + ro, PA, sQg + kq * 16, PKP, HC, lane);
+      for (int kk = 0; kk < HC / 32; ++kk) {
+        fk[kk] = ld_frag_t(sKg + kk * 32 * PKP + kq * 16, PKP, lane);
+        fq[kk] = ld_frag_t(sQg + kk * 32 * PKP + kq * 16, PKP, lane);
       }
 #pragma unroll
-    for (int u = 0; u < VTW; ++u)
+      for (int i = 0; i < RT; ++i) {
+        const int ro = (rt0 + i) * 16;
+        // dq += dA kg; dk += dA^T qg
+#pragma unroll
+        for (int kk = 0; kk < HC / 32; ++kk) {
+          mma(aq[t][i], ld_frag(sdA + (ro + (lane & 15)) * PA + (lane >> 4) * 8 + kk * 32),
+              fk[kk]);
+          mma(ak[t][i], ld_frag_t(sdA + kk * 32 * PA + ro, PA, lane), fq[kk]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VTW; ++u) {
+      const int vd = vd0 + u;
+      Frag<bf16> fh[KP / 32], fd[HC / 32];   // dh'^T, do^T of this v tile
+#pragma unroll
+      for (int kk = 0; kk < KP / 32; ++kk) fh[kk] = ld_frag_t(sDh + kk * 32 * PVP + vd * 16, PVP, lane);
+#pragma unroll
+      for (int kk = 0; kk < HC / 32; ++kk) fd[kk] = ld_frag_t(sDo + kk * 32 * PVP + vd * 16, PVP, lane);
 #pragma unroll
       for (int i = 0; i < JT; ++i) {
-        const int jt = jt0 + i, vd = vd0 + u;
-        // dv^T = dh^T kd^T (dh read transposed) + do^T A (both read transposed)
+        const int jt = jt0 + i;
+        // dv^T = dh'^T kg^T + do^T A
         f32x4 avt = zero4();
-        mma_tile2<bf16, true, false>(avt, sDh + vd * 16, PVP, sKd + jt * 16 * PKP, PKP, KP,
-                                     lane);
-        mma_tile2<bf16, true, true>(avt, sDo + vd * 16, PVP, sA + jt * 16, PA, HC, lane);
+#pragma unroll
+        for (int kk = 0; kk < KP / 32; ++kk)
+          mma(avt, fh[kk], ld_frag(sKg + (jt * 16 + (lane & 15)) * PKP + (lane >> 4) * 8 + kk * 32));
+#pragma unroll
+        for (int kk = 0; kk < HC / 32; ++kk)
+          mma(avt, fd[kk], ld_frag_t(sA + kk * 32 * PA + jt * 16, PA, lane));
         const int jj = jt * 16 + (lane & 15);
         const int vv = vd * 16 + 4 * (lane >> 4);
         if (jj < len && vv < V)
           st8(dv + (long)t0 * rsV + (long)hh * V, ((uint32_t)jj * (uint32_t)rsV + vv) * 2u,
               make_uint2(pack2_bf16(avt[0], avt[1]), pack2_bf16(avt[2], avt[3])));
       }
+    }
     // dh <- 2^gamma dh + (scale q 2^{g~})^T do = fr * (dh fe / scale + qg^T do)
 #pragma unroll
     for (int j = 0; j < NTK; ++j) {
@@ -1077,11 +1099,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
           XK[ro * PX + hk] = ak[t][i][rr];
         }
       }
-      if (w < NKG && lane < 16) sHd[hk] = hdp[t];
-    }
-    if (lane < 16) {
-#pragma unroll
-      for (int j = 0; j < NTK; ++j) sDkc[(w & 1) * KP + (kt0 + j) * 16 + lane] = dkc[j];
+      if (w < NKG && lane < 16) sHd[hk] = hdp[t] * (sFr[hk] / p.scale);   // 2^r sum h dh'
+      if (lane < 16) sDkc[(w / NKG) * KP + hk] = dkc[t];
     }
     __syncthreads();
 
@@ -1136,14 +1155,15 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) off[e] += t8[e];
       }
-      ld_f8(sEg + cg * 8, t8);
       ld_f8(sHd + cg * 8, u8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) off[e] += t8[e] * u8[e];
-      ld_f8(sDkc + cg * 8, t8);
-      ld_f8(sDkc + KP + cg * 8, u8);
+      for (int e = 0; e < 8; ++e) off[e] += u8[e];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) off[e] += t8[e] + u8[e];
+      for (int gi = 0; gi < Lay::NRG; ++gi) {
+        ld_f8(sDkc + gi * KP + cg * 8, t8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) off[e] += t8[e];
+      }
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
         const int row = rs * RPT + j;
@@ -1310,7 +1330,6 @@ hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   return v64 ? launch_head_fwd<128, 64>(p, st) : launch_head_fwd<128, 128>(p, st);
 }
 
-// K = V = 128 runs with 16 waves (4 per SIMD, 128 registers each), smaller heads with 8.
 template <int KP, int VP>
 static hipError_t launch_head_bwd(const HeadBwdArgs& p, hipStream_t st) {
   constexpr int NT = HNT;
