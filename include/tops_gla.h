@@ -154,6 +154,43 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
                        int64_t NC, int dtype, void* stream);
 
 /*
+ * Scalar-gate (simple GLA) forward on the full-head kernels: the gate of token t (global row
+ * of the [B * T] token axis) and head h is gs[t * gs_ts + h] for every key column (float32;
+ * gs_ts = H for per-token gates [B * T, H], 0 for a per-head constant [H] such as g_gamma),
+ * raw per-step log-decays (the kernels take their chunk-local cumsum). Otherwise as
+ * tops_gla_chunk_fwd; only shapes with tops_gla_full_head(K, V, 64, dtype, 0) == 1 are taken
+ * (TOPS_GLA_EUNSUPPORTED otherwise).
+ * Replaces the device part of chunk_simple_gla_fwd, tops/ops/simple_gla/chunk.py:471-519
+ * (chunk_fwd_h_kernel with g / g_gamma, tops/ops/common/chunk_h.py:82-91, and
+ * chunk_fwd_o, tops/ops/common/chunk_o.py:165-240), and chunk_gla's g_gamma path,
+ * tops/ops/gla/chunk.py:1134-1143.
+ */
+int tops_gla_simple_chunk_fwd(const void* q, const void* k, const void* v, const float* gs,
+                              int64_t gs_ts, const float* h0, void* o, float* ht, void* h_ws,
+                              void* seg_ws, int64_t seg_ws_bytes, float scale, int64_t B,
+                              int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
+                              const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                              int64_t NC, int dtype, void* stream);
+
+/*
+ * Scalar-gate backward: (dq, dk, dv[, dg][, dh0]) with gates as tops_gla_simple_chunk_fwd.
+ * dg ([B, T, H, K], dtype: the gradient of the per-column gates, whose sum over the key
+ * columns is the scalar gate's gradient) may be NULL. h / h_ws as tops_gla_chunk_bwd. Only
+ * shapes with tops_gla_full_head(K, V, 64, dtype, 1) == 1 (TOPS_GLA_EUNSUPPORTED otherwise).
+ * Replaces the device part of chunk_simple_gla_bwd, tops/ops/simple_gla/chunk.py:538-615
+ * (chunk_bwd_dh_kernel with g_gamma, chunk_h.py:552-563, and chunk_simple_gla_bwd_o_pl,
+ * tops/ops/common/chunk_o.py:19-163).
+ */
+int tops_gla_simple_chunk_bwd(const void* q, const void* k, const void* v, const float* gs,
+                              int64_t gs_ts, const float* h0, const void* h, const void* dout,
+                              const float* dht, void* dq, void* dk, void* dv, void* dg,
+                              float* dh0, void* h_ws, void* seg_ws, int64_t seg_ws_bytes,
+                              float scale, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                              int chunk_size, const int32_t* cu_seqlens,
+                              const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                              void* stream);
+
+/*
  * Per-chunk dq, dk, dg of the backward (intra-chunk dA computed in-kernel) from the forward
  * states h and the state gradients dh (both [NC, H, K, V], dtype, as produced by
  * tops_gla_chunk_fwd_h / tops_gla_chunk_bwd_dh on raw gates g).

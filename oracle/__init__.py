@@ -12,3 +12,4 @@ module docstring and exercised by ``tests/test_oracle.py``.
 
 from .gla import *  # noqa: F401,F403
 from . import layer  # noqa: F401  (the GLA layer and its modules, float64 torch)
+from . import simple_gla  # noqa: F401  (scalar-gate GLA)

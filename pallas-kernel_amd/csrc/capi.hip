@@ -586,6 +586,135 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   return hip_status(tops::run_chunk_bwd(p, dtype, st), "chunk_bwd (gradients)");
 }
 
+// ---------------------------------------------------------------------------
+// Scalar gates (simple GLA): the full-head kernels with gate(t, h) = gs[t * gs_ts + h]
+// ---------------------------------------------------------------------------
+namespace {
+
+int check_scalar_gate(const float* gs, int64_t gs_ts, int64_t H) {
+  if (gs == nullptr) return fail(TOPS_GLA_EINVAL, "gs must not be NULL");
+  if (gs_ts != 0 && gs_ts != H) return fail(TOPS_GLA_EINVAL, "gs_ts must be 0 or H");
+  return 0;
+}
+
+}  // namespace
+
+int tops_gla_simple_chunk_fwd(const void* q, const void* k, const void* v, const float* gs,
+                              int64_t gs_ts, const float* h0, void* o, float* ht, void* h_ws,
+                              void* seg_ws, int64_t seg_ws_bytes, float scale, int64_t B,
+                              int64_t T, int64_t H, int64_t K, int64_t V, int chunk_size,
+                              const int32_t* cu_seqlens, const int32_t* chunk_offsets, int64_t N,
+                              int64_t NC, int dtype, void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (B * T == 0) return 0;
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr)
+    return fail(TOPS_GLA_EINVAL, "q, k, v and o must not be NULL");
+  if ((rc = check_scalar_gate(gs, gs_ts, H))) return rc;
+  if (!use_head(dtype, chunk_size, K, V, false, {q, k, v, h0, o, ht, h_ws}))
+    return fail(TOPS_GLA_EUNSUPPORTED,
+                "scalar gates run on the full-head kernels (tops_gla_full_head(..., 0) == 1)");
+  tops::HeadFwdArgs f = {};
+  f.q = q;
+  f.k = k;
+  f.v = v;
+  f.g = nullptr;
+  f.gs = gs;
+  f.gs_ts = (long)gs_ts;
+  f.h0 = h0;
+  f.o = o;
+  f.h_out = h_ws;
+  f.ht = ht;
+  seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, f.NS, f.SL, f.seg_state, f.seg_gam);
+  f.scale = scale;
+  f.H = (int)H;
+  f.K = (int)K;
+  f.V = (int)V;
+  f.si = si;
+  return hip_status(tops::run_head_fwd(f, (hipStream_t)stream), "simple_chunk_fwd");
+}
+
+int tops_gla_simple_chunk_bwd(const void* q, const void* k, const void* v, const float* gs,
+                              int64_t gs_ts, const float* h0, const void* h, const void* dout,
+                              const float* dht, void* dq, void* dk, void* dv, void* dg,
+                              float* dh0, void* h_ws, void* seg_ws, int64_t seg_ws_bytes,
+                              float scale, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                              int chunk_size, const int32_t* cu_seqlens,
+                              const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                              void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (B * T == 0) return 0;
+  if (q == nullptr || k == nullptr || v == nullptr || dout == nullptr || dq == nullptr ||
+      dk == nullptr || dv == nullptr)
+    return fail(TOPS_GLA_EINVAL, "q, k, v, do, dq, dk and dv must not be NULL");
+  if ((rc = check_scalar_gate(gs, gs_ts, H))) return rc;
+  if (h == nullptr && h_ws == nullptr)
+    return fail(TOPS_GLA_EINVAL, "h_ws is required when h is NULL");
+  if (!use_head(dtype, chunk_size, K, V, false,
+                {q, k, v, h0, h, dout, dht, dq, dk, dv, dg, dh0, h_ws}) ||
+      !tops::head_bwd_supported((int)K, (int)V))
+    return fail(TOPS_GLA_EUNSUPPORTED,
+                "scalar gates run on the full-head kernels (tops_gla_full_head(..., 1) == 1)");
+  hipStream_t st = (hipStream_t)stream;
+  int NS = 1, SL = 0;
+  float *seg_st = nullptr, *seg_gm = nullptr;
+  seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, NS, SL, seg_st, seg_gm);
+  if (h == nullptr) {
+    tops::HeadScanArgs s = {};
+    s.a = k;
+    s.b = v;
+    s.g = nullptr;
+    s.gs = gs;
+    s.gs_ts = (long)gs_ts;
+    s.s_init = h0;
+    s.s_all = h_ws;
+    s.seg_state = seg_st;
+    s.seg_gam = seg_gm;
+    s.NS = NS;
+    s.SL = SL;
+    s.scale = 1.f;
+    s.H = (int)H;
+    s.K = (int)K;
+    s.V = (int)V;
+    s.si = si;
+    rc = hip_status(tops::run_head_scan(s, false, st), "simple_chunk_bwd (state recompute)");
+    if (rc) return rc;
+    h = h_ws;
+  }
+  tops::HeadBwdArgs b = {};
+  b.q = q;
+  b.k = k;
+  b.v = v;
+  b.g = nullptr;
+  b.gs = gs;
+  b.gs_ts = (long)gs_ts;
+  b.dout = dout;
+  b.h = h;
+  b.dht = dht;
+  b.dq = dq;
+  b.dk = dk;
+  b.dv = dv;
+  b.dg = dg;
+  b.dh0 = dh0;
+  b.seg_state = seg_st;
+  b.seg_gam = seg_gm;
+  b.NS = NS;
+  b.SL = SL;
+  b.scale = scale;
+  b.H = (int)H;
+  b.K = (int)K;
+  b.V = (int)V;
+  b.si = si;
+  return hip_status(tops::run_head_bwd(b, st), "simple_chunk_bwd");
+}
+
 int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const void* g,
                             const void* h, const void* dout, const void* dh, void* dq, void* dk,
                             void* dg, float scale, int64_t B, int64_t T, int64_t H, int64_t K,

@@ -127,17 +127,18 @@ __device__ __forceinline__ Seg seg_of(const SeqInfo& si, int seq, int s, int NS,
 }
 
 // Base-2 chunk-local cumsum of an [HC x KP] gate tile held as RPT rows x 8 columns per
-// thread (raw, already masked). Out: gt = g~ log2 e, gam = its last row, first = its row 0.
-// sTot [NT/64][KP], sFirst [KP]. One barrier.
+// thread: gt holds the raw gates (already masked) on entry and g~ log2 e on return; gam =
+// its last row, first = its row 0. sTot [NT/64][KP], sFirst [KP]. One barrier.
+template <int KP, int NT>
+using GateRows = float[HMap<KP, NT>::RPT][8];
+
 template <int KP, int NT = HNT>
-__device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP, NT>::RPT],
-                                            float (&gt)[HMap<KP, NT>::RPT][8], float (&gam)[8],
-                                            float (&first)[8], float* sTot, float* sFirst,
-                                            int cg, int rs, int lane, int w) {
+__device__ __forceinline__ void head_cumsum_f(GateRows<KP, NT>& gt, float (&gam)[8],
+                                              float (&first)[8], float* sTot, float* sFirst,
+                                              int cg, int rs, int lane, int w) {
   using M = HMap<KP, NT>;
 #pragma unroll
   for (int j = 0; j < M::RPT; ++j) {
-    unpack8(graw[j], gt[j]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) gt[j][e] = gt[j][e] * kLog2e + (j ? gt[j - 1][e] : 0.f);
   }
@@ -178,6 +179,40 @@ __device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP, NT>::RP
   for (int j = 0; j < M::RPT; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) gt[j][e] += off[e];
+}
+
+// The same from the raw bf16 tile (16 bytes = 8 columns per row).
+template <int KP, int NT = HNT>
+__device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP, NT>::RPT],
+                                            float (&gt)[HMap<KP, NT>::RPT][8], float (&gam)[8],
+                                            float (&first)[8], float* sTot, float* sFirst,
+                                            int cg, int rs, int lane, int w) {
+#pragma unroll
+  for (int j = 0; j < HMap<KP, NT>::RPT; ++j) unpack8(graw[j], gt[j]);
+  head_cumsum_f<KP, NT>(gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+}
+
+// Scalar gates (simple GLA, g_gamma): one float per row and head, the same for every key
+// column: gate(t, h) = gs[t * gs_ts + h] (gs_ts = 0: a per-head constant). Loads of rows
+// past the chunk are clamped to its last row; the caller masks them.
+template <int RPT>
+__device__ __forceinline__ void sg_load(float (&x)[RPT], const float* gs, long gs_ts, int t0,
+                                        int row0, int len, int h) {
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) x[j] = gs[(long)(t0 + min(row0 + j, len - 1)) * gs_ts + h];
+}
+
+// Scalar gates in the fused kernels: lane l of every wave holds row l of the chunk, and the
+// wave's inclusive scan gives G_l, the base-2 chunk-local cumsum at row l (rows past the
+// chunk add 0). Every wave computes it for itself: no LDS, no barrier.
+__device__ __forceinline__ float sg_row_cumsum(float graw, int lane, int len) {
+  float x = lane < len ? graw * kLog2e : 0.f;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  return x;
 }
 
 // A float routed through a VGPR. An accumulator initialised straight from a global load is
@@ -293,7 +328,7 @@ __host__ __device__ constexpr int head_vp(int KP, int V) {
 // ---------------------------------------------------------------------------
 // State scan: forward h (a = k, b = v) or reverse dh (a = q, b = do)
 // ---------------------------------------------------------------------------
-template <int KP, int VP, bool REV, int NT>
+template <int KP, int VP, bool REV, int NT, bool SG>
 __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   using MA = HMap<KP, NT>;
   using MB = HMap<VP, NT>;
@@ -345,6 +380,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 
   struct Regs {
     uint4 a[RPT], g[RPT], b[VRPT];
+    float gs[RPT];
   };
   auto issue = [&](int step, Regs& R) {
     const int st = min(step, nsteps - 1);
@@ -353,7 +389,10 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     const int len = min(HC, sg.eos - t0);
     const long oa = (long)t0 * rsK + (long)hh * K;
     hload<RPT>(R.a, a + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
-    hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    if constexpr (SG)
+      sg_load<RPT>(R.gs, p.gs, p.gs_ts, t0, rs * RPT, len, hh);
+    else
+      hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<VRPT>(R.b, b + (long)t0 * rsV + (long)hh * V + cv, (uint32_t)rsV, vrs * VRPT, len,
                 vg * 8, Vw);
   };
@@ -366,12 +405,22 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     const int ci = REV ? (sg.ce - 1 - step) : (sg.cb + step);
     const int t0 = sg.bos + ci * HC;
     const int len = min(HC, sg.eos - t0);
-    uint4 gm[RPT];
-#pragma unroll
-    for (int j = 0; j < RPT; ++j)
-      gm[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
     float gt[RPT][8], gam[8], first[8];
-    head_cumsum<KP, NT>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+    if constexpr (SG) {
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const float x = (colA && rs * RPT + j < len) ? R.gs[j] : 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gt[j][e] = x;
+      }
+      head_cumsum_f<KP, NT>(gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+    } else {
+      uint4 gm[RPT];
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+        gm[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
+      head_cumsum<KP, NT>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+    }
     (void)first;
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
@@ -476,7 +525,8 @@ __global__ __launch_bounds__(256) void head_combine_kernel(float* __restrict__ s
 // KD: kd is staged in LDS (K <= 128). Wider heads (K = 256) do not have the room; their
 // update runs on kg with the column factors split around the product:
 // h <- 2^{gamma-r} (.) (2^r h + kg^T v)  (= 2^gamma h + kd^T v).
-template <int KP, int VP>
+// SG (scalar gates): v2 = v 2^{gamma - G_j} for the state update and G (one float per row).
+template <int KP, int VP, bool SG = false>
 struct HFLayout {
   static constexpr bool KD = KP <= 128;
   static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP),
@@ -493,15 +543,17 @@ struct HFLayout {
   static constexpr int rsc = gam + KP * 4;
   static constexpr int pre = rsc + KP * 4;        // 2^r          (!KD)
   static constexpr int post = pre + KP * 4;       // 2^{gamma-r}  (!KD)
-  static constexpr int bytes = post + KP * 4;
+  static constexpr int v2 = post + KP * 4;        // SG only
+  static constexpr int grow = v2 + (SG ? HC * PVP * 2 : 0);
+  static constexpr int bytes = grow + (SG ? HC * 4 : 0);
 };
 
-template <int KP, int VP>
+template <int KP, int VP, bool SG>
 __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   using M = HMap<KP>;
   using MV = HMap<VP>;
   using TL = HTiles<KP, VP>;
-  using Lay = HFLayout<KP, VP>;
+  using Lay = HFLayout<KP, VP, SG>;
   constexpr int RPT = M::RPT, VRPT = MV::RPT;
   constexpr int PKP = Lay::PKP, PVP = Lay::PVP, PA = Lay::PA;
   constexpr int NTV = TL::NTV, NTK = TL::NTK;
@@ -522,6 +574,8 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   float* sRs = reinterpret_cast<float*>(smem + Lay::rsc);
   float* sPre = reinterpret_cast<float*>(smem + Lay::pre);
   float* sPost = reinterpret_cast<float*>(smem + Lay::post);
+  bf16* sV2 = reinterpret_cast<bf16*>(smem + Lay::v2);
+  float* sG = reinterpret_cast<float*>(smem + Lay::grow);
 
   const bf16* __restrict__ q = (const bf16*)p.q;
   const bf16* __restrict__ k = (const bf16*)p.k;
@@ -561,6 +615,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 
   struct Regs {
     uint4 q[RPT], k[RPT], g[RPT], v[VRPT];
+    float gs;   // SG: the gate of row `lane`
   };
   auto issue = [&](int step, Regs& R) {
     const int st = min(step, nsteps - 1);
@@ -569,7 +624,10 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     const long oa = (long)t0 * rsK + (long)hh * K;
     hload<RPT>(R.q, q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<RPT>(R.k, k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
-    hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    if constexpr (SG)
+      R.gs = p.gs[(long)(t0 + min(lane, len - 1)) * p.gs_ts + hh];
+    else
+      hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V + cv, (uint32_t)rsV, vrs * VRPT, len,
                 vg * 8, Vw);
   };
@@ -580,57 +638,97 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     const int len = min(HC, sg.eos - t0);
 
     // ---- (1) cumsum, gating ----
-    uint4 gmk[RPT];
+    float Gl = 0.f, gam_s = 0.f;   // SG: G of row `lane`, the chunk's total (base 2)
+    if constexpr (SG) {
+      // scalar gates: A's decay 2^{G_i - G_j} is applied after q k^T, the inter term's 2^{G_i}
+      // after q h', and the update runs on v 2^{gamma - G_j}; every factor is <= 1 for
+      // decaying gates, whatever their size
+      __syncthreads();   // the previous chunk's reads of the tiles are done
+      Gl = sg_row_cumsum(R.gs, lane, len);
+      gam_s = __shfl(Gl, len - 1);
 #pragma unroll
-    for (int j = 0; j < RPT; ++j)
-      gmk[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
-    float gt[RPT][8], gam[8], first[8];
-    head_cumsum<KP>(gmk, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
-    float r[8], fkd[8];
+      for (int j = 0; j < RPT; ++j) {
+        const int row = rs * RPT + j;
+        const uint32_t m = (colA && row < len) ? ~0u : 0u;
+        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = mask16(R.q[j], m);
+        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = mask16(R.k[j], m);
+      }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      r[e] = 0.5f * (first[e] + gam[e]);
-      fkd[e] = exp2_hw(gam[e] - r[e]);
-    }
+      for (int j = 0; j < VRPT; ++j) {
+        const int row = vrs * VRPT + j;
+        const uint4 vm = mask16(R.v[j], (colB && row < len) ? ~0u : 0u);
+        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) = vm;
+        const float f = exp2_hw(gam_s - __shfl(Gl, row));
+        float x[8];
+        unpack8(vm, x);
 #pragma unroll
-    for (int j = 0; j < RPT; ++j) {
-      const int row = rs * RPT + j;
-      const uint32_t m = (colA && row < len) ? ~0u : 0u;
-      float xq[8], xk[8], xd[8];
-      unpack8(mask16(R.q[j], m), xq);
-      unpack8(mask16(R.k[j], m), xk);
+        for (int e = 0; e < 8; ++e) x[e] *= f;
+        *reinterpret_cast<uint4*>(sV2 + row * PVP + vg * 8) = pack8(x);
+      }
+      if (w == 0) sG[lane] = Gl;
+      if (rs == 0) {
+        float eg[8], er[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          eg[e] = exp2_hw(gam_s);
+          er[e] = p.scale;
+        }
+        st_f8(sGam + cg * 8, eg);
+        st_f8(sRs + cg * 8, er);
+      }
+    } else {
+      float gt[RPT][8], gam[8], first[8];
+      uint4 gmk[RPT];
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+        gmk[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
+      head_cumsum<KP>(gmk, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+      float r[8], fkd[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float d = gt[j][e] - r[e];
-        xq[e] *= exp2_hw(d);
-        xk[e] *= exp2_hw(-d);
-        xd[e] = xk[e] * fkd[e];
+        r[e] = 0.5f * (first[e] + gam[e]);
+        fkd[e] = exp2_hw(gam[e] - r[e]);
       }
-      *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pack8(xq);
-      *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pack8(xk);
-      if (Lay::KD) *reinterpret_cast<uint4*>(sKd + row * PKP + cg * 8) = pack8(xd);
-    }
 #pragma unroll
-    for (int j = 0; j < VRPT; ++j) {
-      const int row = vrs * VRPT + j;
-      *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) =
-          mask16(R.v[j], (colB && row < len) ? ~0u : 0u);
-    }
-    if (rs == 0) {
-      float eg[8], er[8];
+      for (int j = 0; j < RPT; ++j) {
+        const int row = rs * RPT + j;
+        const uint32_t m = (colA && row < len) ? ~0u : 0u;
+        float xq[8], xk[8], xd[8];
+        unpack8(mask16(R.q[j], m), xq);
+        unpack8(mask16(R.k[j], m), xk);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        eg[e] = exp2_hw(gam[e]);
-        er[e] = p.scale * exp2_hw(r[e]);
+        for (int e = 0; e < 8; ++e) {
+          const float d = gt[j][e] - r[e];
+          xq[e] *= exp2_hw(d);
+          xk[e] *= exp2_hw(-d);
+          xd[e] = xk[e] * fkd[e];
+        }
+        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pack8(xq);
+        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pack8(xk);
+        if (Lay::KD) *reinterpret_cast<uint4*>(sKd + row * PKP + cg * 8) = pack8(xd);
       }
-      st_f8(sGam + cg * 8, eg);
-      st_f8(sRs + cg * 8, er);
-      if (!Lay::KD) {
-        float ep[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ep[e] = exp2_hw(r[e]);
-        st_f8(sPre + cg * 8, ep);
-        st_f8(sPost + cg * 8, fkd);
+      for (int j = 0; j < VRPT; ++j) {
+        const int row = vrs * VRPT + j;
+        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) =
+            mask16(R.v[j], (colB && row < len) ? ~0u : 0u);
+      }
+      if (rs == 0) {
+        float eg[8], er[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          eg[e] = exp2_hw(gam[e]);
+          er[e] = p.scale * exp2_hw(r[e]);
+        }
+        st_f8(sGam + cg * 8, eg);
+        st_f8(sRs + cg * 8, er);
+        if (!Lay::KD) {
+          float ep[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ep[e] = exp2_hw(r[e]);
+          st_f8(sPre + cg * 8, ep);
+          st_f8(sPost + cg * 8, fkd);
+        }
       }
     }
     issue(step + PF, R);
@@ -646,7 +744,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int ii = mi * 16 + 4 * (lane >> 4) + rr;
-        sA[ii * PA + jj] = from_f32<bf16>(jj <= ii ? at[rr] * p.scale : 0.f);
+        float a = at[rr] * p.scale;
+        if constexpr (SG) a *= exp2_hw(jj <= ii ? sG[ii] - sG[jj] : 0.f);
+        sA[ii * PA + jj] = from_f32<bf16>(jj <= ii ? a : 0.f);
       }
     }
     if (hout)
@@ -673,9 +773,16 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       for (int i = 0; i < NTV; ++i) {
         const int vt = vt0 + i;
         f32x4 ot = zero4();
-        mma_tile2<bf16, true, false>(ot, sV + vt * 16, PVP, sA + it * 16 * PA, PA, HC, lane);
-        mma_tile2<bf16, true, false>(ot, sHk + vt * 16, PVP, sQg + it * 16 * PKP, PKP, KP,
-                                     lane);
+        if constexpr (SG) {   // inter term first, scaled by 2^{G_i} (column i of o^T)
+          mma_tile2<bf16, true, false>(ot, sHk + vt * 16, PVP, sQg + it * 16 * PKP, PKP, KP,
+                                       lane);
+          ot *= exp2_hw(sG[it * 16 + (lane & 15)]);
+          mma_tile2<bf16, true, false>(ot, sV + vt * 16, PVP, sA + it * 16 * PA, PA, HC, lane);
+        } else {
+          mma_tile2<bf16, true, false>(ot, sV + vt * 16, PVP, sA + it * 16 * PA, PA, HC, lane);
+          mma_tile2<bf16, true, false>(ot, sHk + vt * 16, PVP, sQg + it * 16 * PKP, PKP, KP,
+                                       lane);
+        }
         const int row = it * 16 + (lane & 15);
         const int vv = vt * 16 + 4 * (lane >> 4);
         if (row < len && vv < Vw)
@@ -683,7 +790,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
               make_uint2(pack2_bf16(ot[0], ot[1]), pack2_bf16(ot[2], ot[3])));
       }
     }
-    if (Lay::KD)
+    if constexpr (SG)
+      state_update<NTV, NTK>(acc, sV2, PVP, sKg, PKP, sGam, vt0, kt0, lane);
+    else if (Lay::KD)
       state_update<NTV, NTK>(acc, sV, PVP, sKd, PKP, sGam, vt0, kt0, lane);
     else
       state_update<NTV, NTK>(acc, sV, PVP, sKg, PKP, sPre, vt0, kt0, lane, sPost);
@@ -733,7 +842,8 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 // registers left to hold the next chunk in flight, and spilling them costs far more than
 // the exposed load latency (the block's 8 waves and the other blocks keep HBM busy).
 // ---------------------------------------------------------------------------
-template <int KP, int VP, int NW>
+// SG (scalar gates): q2 = scale q 2^{G_i} for the dh update and G (one float per row).
+template <int KP, int VP, int NW, bool SG = false>
 struct HBLayout {
   static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP),
                        PA = pitch_of<bf16>(HC);
@@ -755,7 +865,9 @@ struct HBLayout {
   static constexpr int dh = dout + HC * PVP * 2;   // dh' [k][v] bf16
   static constexpr int a = dh + KP * PVP * 2;
   static constexpr int da = a + HC * PA * 2;
-  static constexpr int end_tiles = da + HC * PA * 2;
+  static constexpr int q2 = da + HC * PA * 2;      // SG only
+  static constexpr int grow = q2 + (SG ? HC * PKP * 2 : 0);
+  static constexpr int end_tiles = grow + (SG ? HC * 4 : 0);
   // exchange [HC][PX] x 2 from v on (qg, kg stay intact for the epilogue); it may reach
   // A / dA, which are therefore rewritten in full (zero upper tiles) every chunk
   static constexpr int xq = v;
@@ -764,12 +876,12 @@ struct HBLayout {
   static constexpr int bytes = end_tiles > end_x ? end_tiles : end_x;
 };
 
-template <int KP, int VP, int NT>
+template <int KP, int VP, int NT, bool SG>
 __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   constexpr int NW = NT / 64;
   using M = HMap<KP, NT>;
   using MV = HMap<VP, NT>;
-  using Lay = HBLayout<KP, VP, NW>;
+  using Lay = HBLayout<KP, VP, NW, SG>;
   constexpr int RPT = M::RPT, VRPT = MV::RPT;
   constexpr int PKP = Lay::PKP, PVP = Lay::PVP, PA = Lay::PA, PX = Lay::PX;
   constexpr int NKT = KP / 16, NVT = VP / 16;
@@ -799,6 +911,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   bf16* sdA = reinterpret_cast<bf16*>(smem + Lay::da);
   float* XQ = reinterpret_cast<float*>(smem + Lay::xq);
   float* XK = reinterpret_cast<float*>(smem + Lay::xk);
+  bf16* sQ2 = reinterpret_cast<bf16*>(smem + Lay::q2);
+  float* sG = reinterpret_cast<float*>(smem + Lay::grow);
 
   const bf16* __restrict__ q = (const bf16*)p.q;
   const bf16* __restrict__ k = (const bf16*)p.k;
@@ -837,6 +951,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   }
 
   uint4 Rq[RPT], Rk[RPT], Rg[RPT], Rv[VRPT], Rd[VRPT], Rh[KTW][NHF];
+  float Rs = 0.f;   // SG: the gate of row `lane`
   auto chunk_of = [&](int step, int& t0, int& len, int& ci) {
     ci = sg.ce - 1 - min(step, nsteps - 1);
     t0 = sg.bos + ci * HC;
@@ -848,7 +963,10 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
     const long oa = (long)t0 * rsK + (long)hh * K, ov = (long)t0 * rsV + (long)hh * V;
     hload<RPT>(Rq, q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<RPT>(Rk, k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
-    hload<RPT>(Rg, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    if constexpr (SG)
+      Rs = p.gs[(long)(t0 + min(lane, len - 1)) * p.gs_ts + hh];
+    else
+      hload<RPT>(Rg, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<VRPT>(Rv, v + ov, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
     hload<VRPT>(Rd, dout + ov, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
   };
@@ -874,17 +992,67 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 
     // ---- (1) cumsum, gating; dh' = fe (.) dh to LDS ----
     float dd[RPT][8];   // g~ - r (base 2)
-    {
-      uint4 gmk[RPT], qm[RPT], km[RPT];
+    float gam_s = 0.f;  // SG: the chunk's total gate (base 2)
+    if constexpr (SG) {
+      // scalar gates: raw q, k; the pairwise decays go on A and dA, the row factors on the
+      // inter terms and on q for the dh update (all <= 1 for decaying gates)
+      __syncthreads();   // the previous chunk's epilogue reads are done
+      const float Gl = sg_row_cumsum(Rs, lane, len);
+      gam_s = __shfl(Gl, len - 1);
+#pragma unroll
+      for (int j = 0; j < NTK; ++j) {
+        const int kk = (kt0 + j) * 16 + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < NTV; ++i) {
+          const int vv = (vt0 + i) * 16 + 4 * (lane >> 4);
+          *reinterpret_cast<uint2*>(sDh + kk * PVP + vv) =
+              make_uint2(pack2_bf16(acc[i][j][0], acc[i][j][1]),
+                         pack2_bf16(acc[i][j][2], acc[i][j][3]));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const int row = rs * RPT + j;
+        const uint32_t m = (colA && row < len) ? ~0u : 0u;
+        const uint4 qm = mask16(Rq[j], m);
+        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = qm;
+        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = mask16(Rk[j], m);
+        const float f = p.scale * exp2_hw(__shfl(Gl, row));
+        float x[8];
+        unpack8(qm, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= f;
+        *reinterpret_cast<uint4*>(sQ2 + row * PKP + cg * 8) = pack8(x);
+      }
+#pragma unroll
+      for (int j = 0; j < VRPT; ++j) {
+        const int row = vrs * VRPT + j;
+        const uint32_t m = (colB && row < len) ? ~0u : 0u;
+        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) = mask16(Rv[j], m);
+        *reinterpret_cast<uint4*>(sDo + row * PVP + vg * 8) = mask16(Rd[j], m);
+      }
+      if (w == 0) sG[lane] = Gl;
+      if (rs == 0) {   // fr = scale 2^gamma (the 2^gamma sum_v h dh term), fe = 2^gamma
+        float b8[8], c8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          c8[e] = exp2_hw(gam_s);
+          b8[e] = p.scale * c8[e];
+        }
+        st_f8(sFr + cg * 8, b8);
+        st_f8(sFe + cg * 8, c8);
+      }
+    } else {
+      uint4 qm[RPT], km[RPT];
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
         const uint32_t m = (colA && rs * RPT + j < len) ? ~0u : 0u;
-        gmk[j] = mask16(Rg[j], m);
+        unpack8(mask16(Rg[j], m), dd[j]);
         qm[j] = mask16(Rq[j], m);
         km[j] = mask16(Rk[j], m);
       }
       float gam[8], first[8];
-      head_cumsum<KP, NT>(gmk, dd, gam, first, sTot, sFirst, cg, rs, lane, w);
+      head_cumsum_f<KP, NT>(dd, gam, first, sTot, sFirst, cg, rs, lane, w);
       // gamma of this lane's dh rows from the wave totals (same order of sums as gam)
 #pragma unroll
       for (int j = 0; j < NTK; ++j) {
@@ -955,7 +1123,9 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int ii = mi * 16 + 4 * (lane >> 4) + rr;
-        dst[ii * PA + jj] = from_f32<bf16>(jj <= ii ? at[rr] * p.scale : 0.f);
+        float a = at[rr] * p.scale;
+        if constexpr (SG) a *= exp2_hw(jj <= ii ? sG[ii] - sG[jj] : 0.f);   // A, dA decayed
+        dst[ii * PA + jj] = from_f32<bf16>(jj <= ii ? a : 0.f);
       }
     }
     // dq pre: fr do h^T (h fragments from HBM); dk pre: v dh'^T
@@ -988,9 +1158,20 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       }
       hdp[t] += __shfl_xor(hdp[t], 16);
       hdp[t] += __shfl_xor(hdp[t], 32);
-      const float fr = sFr[hk];
+      if constexpr (SG) {   // row factors: scale 2^{G_i} on do h^T, 2^{gamma - G_j} on v dh^T
 #pragma unroll
-      for (int i = 0; i < RT; ++i) aq[t][i] *= fr;
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const float gr = sG[(rt0 + i) * 16 + 4 * (lane >> 4) + rr];
+            aq[t][i][rr] *= p.scale * exp2_hw(gr);
+            ak[t][i][rr] *= exp2_hw(gam_s - gr);
+          }
+      } else {
+        const float fr = sFr[hk];
+#pragma unroll
+        for (int i = 0; i < RT; ++i) aq[t][i] *= fr;
+      }
       // sum over this wave's rows of kg (.) ak: kg read in the accumulator layout (rows
       // 4 (lane >> 4) + 0..3 of column lane & 15 of each 16 x 16 tile) by transposed reads
       dkc[t] = 0.f;
@@ -1044,11 +1225,12 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
       for (int i = 0; i < JT; ++i) {
         const int jt = jt0 + i;
-        // dv^T = dh'^T kg^T + do^T A
+        // dv^T = dh'^T kg^T + do^T A (scalar gates: (dh^T k^T) 2^{gamma - G_j} + do^T A)
         f32x4 avt = zero4();
 #pragma unroll
         for (int kk = 0; kk < KP / 32; ++kk)
           mma(avt, fh[kk], ld_frag(sKg + (jt * 16 + (lane & 15)) * PKP + (lane >> 4) * 8 + kk * 32));
+        if constexpr (SG) avt *= exp2_hw(gam_s - sG[jt * 16 + (lane & 15)]);
 #pragma unroll
         for (int kk = 0; kk < HC / 32; ++kk)
           mma(avt, fd[kk], ld_frag_t(sA + kk * 32 * PA + jt * 16, PA, lane));
@@ -1060,29 +1242,34 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       }
     }
     // dh <- 2^gamma dh + (scale q 2^{g~})^T do = fr * (dh fe / scale + qg^T do)
+    // (scalar gates: 2^gamma dh + q2^T do, q2 = scale q 2^{G})
 #pragma unroll
     for (int j = 0; j < NTK; ++j) {
-      const float d = sFe[(kt0 + j) * 16 + (lane & 15)] / p.scale;
+      const float d = SG ? sFe[(kt0 + j) * 16 + (lane & 15)]
+                         : sFe[(kt0 + j) * 16 + (lane & 15)] / p.scale;
 #pragma unroll
       for (int i = 0; i < NTV; ++i) acc[i][j] *= d;
     }
+    const bf16* sQd = SG ? sQ2 : sQg;
 #pragma unroll
     for (int kk = 0; kk < HC; kk += 32) {
       Frag<bf16> x[NTV], y[NTK];
 #pragma unroll
       for (int i = 0; i < NTV; ++i) x[i] = ld_frag_t(sDo + kk * PVP + (vt0 + i) * 16, PVP, lane);
 #pragma unroll
-      for (int j = 0; j < NTK; ++j) y[j] = ld_frag_t(sQg + kk * PKP + (kt0 + j) * 16, PKP, lane);
+      for (int j = 0; j < NTK; ++j) y[j] = ld_frag_t(sQd + kk * PKP + (kt0 + j) * 16, PKP, lane);
 #pragma unroll
       for (int i = 0; i < NTV; ++i)
 #pragma unroll
         for (int j = 0; j < NTK; ++j) mma(acc[i][j], x[i], y[j]);
     }
+    if constexpr (!SG) {
 #pragma unroll
-    for (int j = 0; j < NTK; ++j) {
-      const float f = sFr[(kt0 + j) * 16 + (lane & 15)];
+      for (int j = 0; j < NTK; ++j) {
+        const float f = sFr[(kt0 + j) * 16 + (lane & 15)];
 #pragma unroll
-      for (int i = 0; i < NTV; ++i) acc[i][j] *= f;
+        for (int i = 0; i < NTV; ++i) acc[i][j] *= f;
+      }
     }
     __syncthreads();   // every tile read is done: the exchange aliases them
 
@@ -1118,8 +1305,10 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         pr[j][e] = q8[e] * xq[e] - k8[e] * xk[e];
-        xq[e] *= exp2_hw(dd[j][e]);
-        xk[e] *= exp2_hw(-dd[j][e]);
+        if constexpr (!SG) {   // scalar gates: the factors are in already
+          xq[e] *= exp2_hw(dd[j][e]);
+          xk[e] *= exp2_hw(-dd[j][e]);
+        }
       }
       if (row < len && colA) {
         const long b0 = (long)t0 * rsK + (long)hh * K;
@@ -1128,51 +1317,54 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         st16(dk + b0, a, pack8(xk));
       }
     }
-    // reverse cumsum over rows: in-thread, then across the wave's row segments
+    // dg (uniform branch: absent for scalar gates without a gate gradient)
+    if (p.dg) {
+      // reverse cumsum over rows: in-thread, then across the wave's row segments
 #pragma unroll
-    for (int j = RPT - 2; j >= 0; --j)
+      for (int j = RPT - 2; j >= 0; --j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pr[j][e] += pr[j + 1][e];
-    float x[8];
+        for (int e = 0; e < 8; ++e) pr[j][e] += pr[j + 1][e];
+      float x[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = pr[0][e];
+      for (int e = 0; e < 8; ++e) x[e] = pr[0][e];
 #pragma unroll
-    for (int d = M::NCG; d < 64; d <<= 1) {
+      for (int d = M::NCG; d < 64; d <<= 1) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float y = __shfl_down(x[e], d);
-        if (lane + d < 64) x[e] += y;
+        for (int e = 0; e < 8; ++e) {
+          const float y = __shfl_down(x[e], d);
+          if (lane + d < 64) x[e] += y;
+        }
       }
-    }
-    if (lane < M::NCG) st_f8(sSuf + w * KP + cg * 8, x);
-    __syncthreads();
-    {
-      float off[8], t8[8], u8[8];
+      if (lane < M::NCG) st_f8(sSuf + w * KP + cg * 8, x);
+      __syncthreads();
+      {
+        float off[8], t8[8], u8[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) off[e] = x[e] - pr[0][e];   // later segments of the wave
-      for (int ww = w + 1; ww < NW; ++ww) {   // later waves (w is wave-uniform)
-        ld_f8(sSuf + ww * KP + cg * 8, t8);
+        for (int e = 0; e < 8; ++e) off[e] = x[e] - pr[0][e];   // later segments of the wave
+        for (int ww = w + 1; ww < NW; ++ww) {   // later waves (w is wave-uniform)
+          ld_f8(sSuf + ww * KP + cg * 8, t8);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) off[e] += t8[e];
-      }
-      ld_f8(sHd + cg * 8, u8);
+          for (int e = 0; e < 8; ++e) off[e] += t8[e];
+        }
+        ld_f8(sHd + cg * 8, u8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) off[e] += u8[e];
+        for (int e = 0; e < 8; ++e) off[e] += u8[e];
 #pragma unroll
-      for (int gi = 0; gi < Lay::NRG; ++gi) {
-        ld_f8(sDkc + gi * KP + cg * 8, t8);
+        for (int gi = 0; gi < Lay::NRG; ++gi) {
+          ld_f8(sDkc + gi * KP + cg * 8, t8);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) off[e] += t8[e];
-      }
+          for (int e = 0; e < 8; ++e) off[e] += t8[e];
+        }
 #pragma unroll
-      for (int j = 0; j < RPT; ++j) {
-        const int row = rs * RPT + j;
-        if (row < len && colA) {
-          float o8[8];
+        for (int j = 0; j < RPT; ++j) {
+          const int row = rs * RPT + j;
+          if (row < len && colA) {
+            float o8[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) o8[e] = pr[j][e] + off[e];
-          st16(dg + (long)t0 * rsK + (long)hh * K, ((uint32_t)row * (uint32_t)rsK + cg * 8) * 2u,
-               pack8(o8));
+            for (int e = 0; e < 8; ++e) o8[e] = pr[j][e] + off[e];
+            st16(dg + (long)t0 * rsK + (long)hh * K,
+                 ((uint32_t)row * (uint32_t)rsK + cg * 8) * 2u, pack8(o8));
+          }
         }
       }
     }
@@ -1228,8 +1420,12 @@ long head_seg_ws_bytes(int N, int NS, int H, int K, int V) {
 template <int KP, int VP, bool REV>
 static hipError_t launch_head_scan(const HeadScanArgs& p, hipStream_t st, long blocks) {
   constexpr int NT = HNT;
-  hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV, NT>), dim3((unsigned)blocks), dim3(NT), 0,
-                     st, p);
+  if (p.g)
+    hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV, NT, false>), dim3((unsigned)blocks),
+                       dim3(NT), 0, st, p);
+  else
+    hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV, NT, true>), dim3((unsigned)blocks),
+                       dim3(NT), 0, st, p);
   return hipGetLastError();
 }
 
@@ -1287,19 +1483,25 @@ hipError_t run_head_scan(const HeadScanArgs& p0, bool reverse, hipStream_t st) {
   return head_scan_launch(p, reverse, st, 3, 0, p.NS);
 }
 
-template <int KP, int VP>
-static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
-  using Lay = HFLayout<KP, VP>;
-  const long blocks = (long)p.si.N * p.NS * p.H * ((p.V + VP - 1) / VP);
-  if (blocks == 0) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP>,
+template <int KP, int VP, bool SG>
+static hipError_t launch_head_fwd_sg(const HeadFwdArgs& p, hipStream_t st, long blocks) {
+  using Lay = HFLayout<KP, VP, SG>;
+  hipError_t e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP, SG>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
   if (e != hipSuccess) return e;
   ktimer_mark(KT_HEAD_FWD, false, st);
-  hipLaunchKernelGGL((head_fwd_kernel<KP, VP>), dim3((unsigned)blocks), dim3(HNT), Lay::bytes,
-                     st, p);
+  hipLaunchKernelGGL((head_fwd_kernel<KP, VP, SG>), dim3((unsigned)blocks), dim3(HNT),
+                     Lay::bytes, st, p);
   ktimer_mark(KT_HEAD_FWD, true, st);
   return hipGetLastError();
+}
+
+template <int KP, int VP>
+static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
+  const long blocks = (long)p.si.N * p.NS * p.H * ((p.V + VP - 1) / VP);
+  if (blocks == 0) return hipSuccess;
+  return p.g ? launch_head_fwd_sg<KP, VP, false>(p, st, blocks)
+             : launch_head_fwd_sg<KP, VP, true>(p, st, blocks);
 }
 
 hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
@@ -1308,6 +1510,8 @@ hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
     s.a = p.k;
     s.b = p.v;
     s.g = p.g;
+    s.gs = p.gs;
+    s.gs_ts = p.gs_ts;
     s.s_init = p.h0;
     s.s_all = nullptr;
     s.s_final = nullptr;
@@ -1330,20 +1534,26 @@ hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   return v64 ? launch_head_fwd<128, 64>(p, st) : launch_head_fwd<128, 128>(p, st);
 }
 
-template <int KP, int VP>
-static hipError_t launch_head_bwd(const HeadBwdArgs& p, hipStream_t st) {
+template <int KP, int VP, bool SG>
+static hipError_t launch_head_bwd_sg(const HeadBwdArgs& p, hipStream_t st, long blocks) {
   constexpr int NT = HNT;
-  using Lay = HBLayout<KP, VP, NT / 64>;
-  const long blocks = (long)p.si.N * p.NS * p.H;
-  if (blocks == 0) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute((const void*)head_bwd_kernel<KP, VP, NT>,
+  using Lay = HBLayout<KP, VP, NT / 64, SG>;
+  hipError_t e = hipFuncSetAttribute((const void*)head_bwd_kernel<KP, VP, NT, SG>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
   if (e != hipSuccess) return e;
   ktimer_mark(KT_HEAD_BWD, false, st);
-  hipLaunchKernelGGL((head_bwd_kernel<KP, VP, NT>), dim3((unsigned)blocks), dim3(NT), Lay::bytes,
-                     st, p);
+  hipLaunchKernelGGL((head_bwd_kernel<KP, VP, NT, SG>), dim3((unsigned)blocks), dim3(NT),
+                     Lay::bytes, st, p);
   ktimer_mark(KT_HEAD_BWD, true, st);
   return hipGetLastError();
+}
+
+template <int KP, int VP>
+static hipError_t launch_head_bwd(const HeadBwdArgs& p, hipStream_t st) {
+  const long blocks = (long)p.si.N * p.NS * p.H;
+  if (blocks == 0) return hipSuccess;
+  return p.g ? launch_head_bwd_sg<KP, VP, false>(p, st, blocks)
+             : launch_head_bwd_sg<KP, VP, true>(p, st, blocks);
 }
 
 hipError_t run_head_bwd(const HeadBwdArgs& p, hipStream_t st) {
@@ -1352,6 +1562,8 @@ hipError_t run_head_bwd(const HeadBwdArgs& p, hipStream_t st) {
     s.a = p.q;
     s.b = p.dout;
     s.g = p.g;
+    s.gs = p.gs;
+    s.gs_ts = p.gs_ts;
     s.s_init = p.dht;
     s.seg_state = p.seg_state;
     s.seg_gam = p.seg_gam;

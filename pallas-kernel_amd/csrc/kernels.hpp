@@ -189,8 +189,13 @@ int head_vtiles(int K, int V);   // V tiles (blocks per segment and head)
 void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL, int VT);
 long head_seg_ws_bytes(int N, int NS, int H, int K, int V);
 
+// Full-head kernels. Gates: g ([T, H, K] bf16, raw) or, with g == nullptr, the scalar
+// gates of simple GLA: gate(t, h) = gs[t * gs_ts + h] for every key column (float; gs_ts = H
+// for per-token gates, 0 for a per-head constant).
 struct HeadScanArgs {
   const void *a, *b, *g;  // forward: k, v ; reverse: q, do
+  const float* gs;
+  long gs_ts;
   const float* s_init;    // forward: h0 ; reverse: dht (nullable)
   void* s_all;            // per-chunk states [NC, H, K, V] bf16 (nullable)
   float* s_final;         // forward: ht ; reverse: dh0 (nullable)
@@ -206,6 +211,8 @@ hipError_t run_head_scan(const HeadScanArgs& p, bool reverse, hipStream_t st);
 
 struct HeadFwdArgs {
   const void *q, *k, *v, *g;
+  const float* gs;
+  long gs_ts;
   const float* h0;        // nullable
   void* o;
   void* h_out;            // [NC, H, K, V] bf16 (nullable)
@@ -221,9 +228,11 @@ hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st);
 
 struct HeadBwdArgs {
   const void *q, *k, *v, *g, *dout;
+  const float* gs;
+  long gs_ts;
   const void* h;          // [NC, H, K, V] bf16 forward states (chunk start)
   const float* dht;       // nullable
-  void *dq, *dk, *dv, *dg;
+  void *dq, *dk, *dv, *dg;  // dg nullable with scalar gates
   float* dh0;             // nullable
   float* seg_state;       // NS > 1 only
   float* seg_gam;

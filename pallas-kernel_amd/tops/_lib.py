@@ -50,6 +50,10 @@ _SIGS = {
     "tops_gla_fused_recurrent_bwd": [_P] * 16 + [_F, _I, _I64, _I64, _I64, _I64, _I64, _P,
                                                  _I64, _I, _P],
     "tops_gla_full_head": [_I64, _I64, _I, _I, _I],
+    "tops_gla_simple_chunk_fwd": [_P] * 4 + [_I64] + [_P] * 5 + [_I64, _F] + [_I64] * 5 +
+                                 [_I, _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_simple_chunk_bwd": [_P] * 4 + [_I64] + [_P] * 11 + [_I64, _F] + [_I64] * 5 +
+                                 [_I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_rmsnorm_gated_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _F, _I, _P],
     "tops_gla_rmsnorm_gated_bwd": [_P] * 9 + [_I64, _I64, _I64, _I, _P],
     "tops_gla_rmsnorm_ws_bytes": [_I64, _I64],

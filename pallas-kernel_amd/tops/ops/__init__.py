@@ -1,1 +1,1 @@
-"""Operator packages (``tops.ops.gla``)."""
+"""Operator packages (``tops.ops.gla``, ``tops.ops.simple_gla``, ``tops.ops.common``)."""

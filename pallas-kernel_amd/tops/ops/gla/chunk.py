@@ -97,11 +97,25 @@ def _shape_check(q, k=None, v=None, g=None, h0=None, N=None, name="initial_state
 
 
 def _gates(g, g_gamma, q):
+    """The per-element gate tensor: g, or g_gamma broadcast (kept in float32, as the
+    reference computes its ramp ``g_gamma * pos`` in float32, ``chunk.py:1134-1143``), or
+    zeros."""
     if g is not None:
         return g
     if g_gamma is not None:
-        return g_gamma.to(q.dtype).expand(q.shape)
+        return g_gamma.to(torch.float32).expand(q.shape)
     return torch.zeros_like(q)
+
+
+def _per_head(g_gamma, H):
+    """g_gamma as a float32 ``[H]`` vector when it is constant over batch, time and key
+    columns (the scalar-gate kernels' per-head form), else None."""
+    if g_gamma.dim() > 4:
+        return None
+    shape = [1] * (4 - g_gamma.dim()) + list(g_gamma.shape)
+    if shape[0] != 1 or shape[1] != 1 or shape[3] != 1 or shape[2] not in (1, H):
+        return None
+    return g_gamma.reshape(shape[2]).to(torch.float32).expand(H)
 
 
 # ---------------------------------------------------------------------------
@@ -160,6 +174,89 @@ class _ChunkGLAFunction(torch.autograd.Function):
         return dq, dk, dv, dg, dh0, None, None, None, None
 
 
+class _ScalarGateGLAFunction(torch.autograd.Function):
+    """GLA with scalar gates on the full-head kernels (``tops_gla_simple_chunk_fwd / _bwd``):
+    the log-decay of token t and head h is ``gs[t, h]`` (gs ``[B * T, H]``) or ``gs[h]`` (gs
+    ``[H]``) for every key column. Differentiable w.r.t. q, k, v, gs and h0."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, gs, h0, scale, output_final_state, cu_list):
+        B, T, H, K = q.shape
+        V = v.shape[-1]
+        C = 64
+        dev = check_device(q, k, v, gs, h0)
+        seq = SeqLayout(B, T, C, cu_list, dev)
+        ts = 0 if gs.dim() == 1 else H
+        o = torch.empty_like(v)
+        ht = (torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev)
+              if output_final_state else None)
+        keep = any(ctx.needs_input_grad[:5])
+        h_ws = torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev) if keep else None
+        ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list is not None, q.dtype, dev)
+        call("tops_gla_simple_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(gs), ts, ptr(h0), ptr(o),
+             ptr(ht), ptr(h_ws), ptr(ws), nws, scale, B, T, H, K, V, C, *seq.args(),
+             dtype_code(q.dtype), stream_of(dev))
+        ctx.save_for_backward(q, k, v, gs, h0, h_ws)
+        ctx.meta = (scale, cu_list)
+        return o, ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        q, k, v, gs, h0, h_ws = ctx.saved_tensors
+        scale, cu_list = ctx.meta
+        B, T, H, K = q.shape
+        V = v.shape[-1]
+        C = 64
+        dev = q.device
+        seq = SeqLayout(B, T, C, cu_list, dev)
+        ts = 0 if gs.dim() == 1 else H
+        do = torch.zeros_like(v) if do is None else _c(do, v.dtype)
+        dht = None if dht is None else _c(dht, torch.float32)
+        dq, dk, dv = (torch.empty_like(x) for x in (q, k, v))
+        want_dg = ctx.needs_input_grad[3]
+        dg = torch.empty_like(q) if want_dg else None
+        need_dh0 = h0 is not None and ctx.needs_input_grad[4]
+        dh0 = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if need_dh0 else None
+        ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list is not None, q.dtype, dev)
+        call("tops_gla_simple_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(gs), ts, ptr(h0),
+             ptr(h_ws), ptr(do), ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None,
+             ptr(ws), nws, scale, B, T, H, K, V, C, *seq.args(), dtype_code(q.dtype),
+             stream_of(dev))
+        dgs = None
+        if want_dg:   # a scalar gate's gradient sums its key columns' gradients
+            d = dg.to(torch.float32).sum(-1)
+            dgs = d.reshape(B * T, H) if gs.dim() == 2 else d.sum((0, 1))
+        return dq, dk, dv, dgs, dh0, None, None, None
+
+
+def scalar_gate_gla(q, k, v, gs, initial_state, scale, output_final_state, cu_list):
+    """GLA whose log-decay is the same for every key column: ``gs`` float32 ``[B, T, H]``
+    (per-token raw gates) or ``[H]`` (a per-head constant). bf16 inputs of full-head shapes
+    run the scalar-gate chunk kernels; anything else the recurrent kernel on the gate
+    broadcast over K, in float32 (exact for any decay strength, as the scalar-gate kernels
+    are). Returns (o in the compute dtype, ht or None)."""
+    from .fused_recurrent import fused_recurrent_gla
+
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    cdt = _compute_dtype(q, k, v)
+    q, k, v = _c(q, cdt), _c(k, cdt), _c(v, cdt)
+    h0 = _c(initial_state, torch.float32)
+    grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (q, k, v, gs, h0))
+    if _full_head(K, V, 64, cdt, grad, q, k, v, h0):
+        gflat = gs.reshape(B * T, H) if gs.dim() == 3 else gs
+        return _ScalarGateGLAFunction.apply(q, k, v, _c(gflat, torch.float32), h0, float(scale),
+                                            bool(output_final_state), cu_list)
+    f32 = torch.float32
+    g = (gs[..., None] if gs.dim() == 3 else gs[None, None, :, None]).to(f32)
+    g = g.expand(B, T, H, K).contiguous()
+    o, ht = fused_recurrent_gla(q.to(f32), k.to(f32), v.to(f32), gk=g, scale=float(scale),
+                                initial_state=h0, output_final_state=bool(output_final_state),
+                                cu_seqlens=cu_list)
+    return o, ht
+
+
 def chunk_gla(q, k, v, g=None, g_gamma=None, scale=None, initial_state=None,
               output_final_state=False, cu_seqlens=None, chunk_size=16):
     """Chunked GLA forward (differentiable). Reference: ``tops/ops/gla/chunk.py:1187-1251``.
@@ -177,13 +274,18 @@ def chunk_gla(q, k, v, g=None, g_gamma=None, scale=None, initial_state=None,
     V = v.shape[-1]
     assert k.shape == (B, T, H, K), f"Expected k shape {(B, T, H, K)}, got {tuple(k.shape)}"
     assert v.shape[:3] == (B, T, H), f"Expected v shape {(B, T, H, V)}, got {tuple(v.shape)}"
-    g = _gates(g, g_gamma, q)
-    assert g.shape == (B, T, H, K), f"Expected g shape {(B, T, H, K)}, got {tuple(g.shape)}"
     cu_list = None if cu_seqlens is None else _lib.to_list(cu_seqlens)
     N = B if cu_list is None else len(cu_list) - 1
     if initial_state is not None:
         assert initial_state.shape == (N, H, K, V), \
             f"Expected initial_state shape {(N, H, K, V)}, got {tuple(initial_state.shape)}"
+    gh = _per_head(g_gamma, H) if g is None and g_gamma is not None else None
+    if gh is not None:   # a per-head constant decay: the scalar-gate kernels, gate in float32
+        o, ht = scalar_gate_gla(q, k, v, gh, initial_state, _default_scale(scale, K),
+                                output_final_state, cu_list)
+        return o.to(dtype), (ht if output_final_state else None)
+    g = _gates(g, g_gamma, q)
+    assert g.shape == (B, T, H, K), f"Expected g shape {(B, T, H, K)}, got {tuple(g.shape)}"
     cdt = _compute_dtype(q, k, v, g)
     o, ht = _ChunkGLAFunction.apply(_c(q, cdt), _c(k, cdt), _c(v, cdt), _c(g, cdt),
                                     _c(initial_state, torch.float32),

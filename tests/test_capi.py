@@ -32,7 +32,7 @@ def _declared():
 
 def test_header_lists_entry_points():
     decl = _declared()
-    assert len(decl) == 28, decl
+    assert len(decl) == 30, decl
     assert set(decl) == set(_lib.EXPORTED)
 
 
@@ -176,3 +176,21 @@ def test_segment_workspace_query():
     st2, gm2 = 4 * 2 * 16 * 256 * 128 * 4, 4 * 2 * 16 * 256 * 4
     assert q(4, 8192, 16, 256, 128, 64, 0, 1) == st2 + (gm2 + 255) // 256 * 256
     assert q(4, 8192, 16, 320, 128, 64, 0, 1) == 0      # K > 256: other kernels
+
+
+def test_simple_chunk_validation():
+    buf = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    fwd = lambda gs, ts, dtype, K=128: [buf, buf, buf, gs, ts, NULL, buf, NULL, NULL, NULL, 0,  # noqa: E731
+                                        1.0, 1, 64, 2, K, 128, 64, NULL, NULL, 1, 1, dtype, NULL]
+    rc, msg = _rc("tops_gla_simple_chunk_fwd", *fwd(NULL, 0, 1))
+    assert rc == 1 and "gs must not be NULL" in msg
+    rc, msg = _rc("tops_gla_simple_chunk_fwd", *fwd(buf, 3, 1))
+    assert rc == 1 and "gs_ts must be 0 or H" in msg
+    rc, msg = _rc("tops_gla_simple_chunk_fwd", *fwd(buf, 2, 0))   # float32: not full-head
+    assert rc == 2 and "full-head" in msg
+    bwd = lambda K, V: [buf, buf, buf, buf, 0, NULL, buf, buf, NULL, buf, buf, buf, NULL, NULL,  # noqa: E731
+                        NULL, NULL, 0, 1.0, 1, 64, 2, K, V, 64, NULL, NULL, 1, 1, 1, NULL]
+    rc, msg = _rc("tops_gla_simple_chunk_bwd", *bwd(128, 256))   # the fused backward: V <= 128
+    assert rc == 2 and "full-head" in msg
+    rc, msg = _rc("tops_gla_simple_chunk_bwd", *(bwd(128, 128)[:6] + [NULL] + bwd(128, 128)[7:]))
+    assert rc == 1 and "h_ws is required" in msg

@@ -469,3 +469,121 @@ def test_layer_norm_gate_and_conv_closed_forms():
     np.testing.assert_allclose(yv[:, 3:].numpy(), L.short_conv(xx[:1, 3:], w, b, None).numpy(),
                                atol=1e-12)
     assert torch.allclose(L.short_conv(xx, w, b, "silu"), F.silu(yy))
+
+
+# ---------------------------------------------------------------------------
+# simple GLA (scalar gates)
+# ---------------------------------------------------------------------------
+
+SG = orc.simple_gla
+
+
+def _sg_inputs(B, T, H, K, V, seed, h0=False, N=None):
+    r = RNG(seed)
+    q = r.standard_normal((B, T, H, K))
+    k = r.standard_normal((B, T, H, K))
+    v = r.standard_normal((B, T, H, V))
+    g_raw = _logsig(r.standard_normal((B, T, H))) / 4      # per-token scalar gates
+    gamma = -np.abs(r.standard_normal(H)) * 0.3              # per-head constant
+    N = B if N is None else N
+    s0 = r.standard_normal((N, H, K, V)) if h0 else None
+    return q, k, v, g_raw, gamma, s0
+
+
+def test_simple_naive_is_broadcast_gla_and_linear_attention():
+    B, T, H, K, V = 2, 11, 3, 4, 5
+    q, k, v, g_raw, gamma, s0 = _sg_inputs(B, T, H, K, V, 1, h0=True)
+    gk = np.repeat(g_raw[..., None], K, -1) + gamma[None, None, :, None]
+    o, S = SG.simple_gla_naive(q, k, v, g=np.repeat(g_raw[..., None], K, -1),
+                               g_gamma=np.broadcast_to(gamma[None, None, :, None], q.shape),
+                               initial_state=s0, output_final_state=True)
+    o2, S2 = orc.naive_recurrent_gla(q, k, v, gk, None, s0, True)
+    np.testing.assert_allclose(o, o2, rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(S, S2, rtol=1e-13, atol=1e-13)
+    # no gate, no h0: causal linear attention, every (t, s) pair
+    o0, _ = SG.simple_gla_naive(q, k, v, scale=0.3)
+    ref = np.zeros_like(o0)
+    for b in range(B):
+        for t in range(T):
+            for s in range(t + 1):
+                ref[b, t] += 0.3 * np.einsum("hk,hk->h", q[b, t], k[b, s])[:, None] * v[b, s]
+    np.testing.assert_allclose(o0, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_simple_intra_bruteforce():
+    B, T, H, K, C = 1, 16, 2, 3, 8
+    q, k, _, _, gamma, _ = _sg_inputs(B, T, H, K, 1, 2)
+    A = SG.chunk_simple_gla_fwd_intra(q, k, gamma, 0.5, C)
+    for n in range(T // C):
+        for i in range(C):
+            for j in range(C):
+                for h in range(H):
+                    a = 0.5 * np.dot(q[0, n * C + i, h], k[0, n * C + j, h]) * \
+                        np.exp(gamma[h] * (i - j))
+                    assert abs(A[0, n * C + i, h, j] - a) < 1e-12
+
+
+SG_CASES = [
+    dict(B=2, T=64, H=2, K=4, V=6, C=16, gate="g_gamma"),
+    dict(B=1, T=96, H=3, K=5, V=4, C=32, gate="g"),
+    dict(B=2, T=64, H=2, K=4, V=4, C=64, gate="both", h0=True),
+    dict(B=1, T=48, H=2, K=3, V=5, C=16, gate="none", h0=True, scale=0.2),
+    dict(B=2, T=64, H=2, K=4, V=4, C=16, gate="both", cu=[0, 32, 80, 128], h0=True),
+]
+
+
+@pytest.mark.parametrize("cfg", SG_CASES, ids=[str(i) for i in range(len(SG_CASES))])
+def test_chunk_simple_gla_equals_naive(cfg):
+    B, T, H, K, V, C = (cfg[x] for x in ("B", "T", "H", "K", "V", "C"))
+    cu = cfg.get("cu")
+    N = len(cu) - 1 if cu else B
+    q, k, v, g_raw, gamma, s0 = _sg_inputs(B, T, H, K, V, 3, cfg.get("h0", False), N)
+    gate = cfg["gate"]
+    use_g = gate in ("g", "both")
+    use_gamma = gate in ("g_gamma", "both")
+    g_cum = SG.scalar_cumsum(g_raw.reshape(1, B * T, H) if cu else g_raw, C, cu)
+    g_cum = g_cum.reshape(B, T, H)
+    sc = cfg.get("scale")
+    o, ht = SG.chunk_simple_gla_fwd(q, k, v, g=g_cum if use_g else None,
+                                    g_gamma=gamma if use_gamma else None, scale=sc, h0=s0,
+                                    use_ht=True, cu_seqlens=cu, chunk_size=C)
+    gk = np.zeros((B, T, H, K))
+    if use_g:
+        gk += g_raw[..., None]
+    if use_gamma:
+        gk += gamma[None, None, :, None]
+    flat = (lambda x: x.reshape(1, B * T, *x.shape[2:])) if cu else (lambda x: x)
+    o2, S2 = orc.naive_recurrent_gla(flat(q), flat(k), flat(v), flat(gk), sc, s0, True, cu)
+    np.testing.assert_allclose(o, o2.reshape(o.shape), rtol=1e-11, atol=1e-11)
+    np.testing.assert_allclose(ht, S2, rtol=1e-11, atol=1e-11)
+
+
+def test_chunk_simple_gla_fwd_ref_equals_naive_with_padding():
+    """Odd T: the reference pads with zero rows whose gate still decays the final state."""
+    B, T, H, K, V, C = 2, 40, 2, 4, 3, 16
+    q, k, v, _, gamma, s0 = _sg_inputs(B, T, H, K, V, 4, h0=True)
+    ht, o = SG.chunk_simple_gla_fwd_ref(q, k, v, gamma, 0.4, s0, True, C)
+    gk = np.broadcast_to(gamma[None, None, :, None], (B, T, H, K))
+    o2, S2 = orc.naive_recurrent_gla(q, k, v, gk, 0.4, s0, True)
+    np.testing.assert_allclose(o, o2, rtol=1e-11, atol=1e-11)
+    Tp = 48   # the padded rows decay the state by gamma per row
+    np.testing.assert_allclose(ht, S2 * np.exp(gamma * (Tp - T))[None, :, None, None],
+                               rtol=1e-11, atol=1e-11)
+
+
+@pytest.mark.parametrize("h0,dht", [(False, False), (True, False), (True, True)])
+def test_chunk_simple_gla_bwd_equals_autograd(h0, dht):
+    B, T, H, K, V, C = 2, 48, 2, 4, 3, 16
+    q, k, v, _, gamma, s0 = _sg_inputs(B, T, H, K, V, 5, h0=h0)
+    r = RNG(6)
+    do = r.standard_normal((B, T, H, V))
+    dh = r.standard_normal((B, H, K, V)) if dht else None
+    dq, dk, dv, dh0 = SG.chunk_simple_gla_bwd(q, k, v, gamma, 0.3, s0, do, dh, C)
+    gk = np.ascontiguousarray(np.broadcast_to(gamma[None, None, :, None], (B, T, H, K)))
+    gq, gk_, gv, _, _, gh0 = _autograd(q, k, v, gk, None, 0.3, s0, do, dh, None)
+    for name, a, b in [("dq", dq, gq), ("dk", dk, gk_), ("dv", dv, gv)]:
+        np.testing.assert_allclose(a, b, rtol=1e-9, atol=1e-9, err_msg=name)
+    if h0:
+        np.testing.assert_allclose(dh0, gh0, rtol=1e-9, atol=1e-9)
+    else:
+        assert dh0 is None
