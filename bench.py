@@ -60,9 +60,13 @@ def _inputs(device):
     do = r.standard_normal((B, T, H, V), dtype=f)
     dht = r.standard_normal((B, H, K, V), dtype=f) * 0.1
     g = (-np.logaddexp(0, -graw) / 16).astype(f)
+    # --op simple_gla: a per-head constant log-decay (logsigmoid(randn(H)), drawn last so the
+    # main workload's inputs are unchanged)
+    gamma = (-np.logaddexp(0, -r.standard_normal(H, dtype=f))).astype(f)
     bf = lambda x: torch.from_numpy(x).to(device).to(torch.bfloat16)  # noqa: E731
     fp = lambda x: torch.from_numpy(x).to(device)  # noqa: E731
-    return dict(q=bf(q), k=bf(k), v=bf(v), g=bf(g), h0=fp(h0), do=bf(do), dht=fp(dht))
+    return dict(q=bf(q), k=bf(k), v=bf(v), g=bf(g), h0=fp(h0), do=bf(do), dht=fp(dht),
+                gamma=fp(gamma))
 
 
 def _copy_calibration(device, mib=512, reps=3):
@@ -78,7 +82,7 @@ def _copy_calibration(device, mib=512, reps=3):
     torch.cuda.synchronize(device)
 
 
-def _kernel_profile(x, reps=10):
+def _kernel_profile(x, reps=10, op="chunk_gla"):
     """Per-launch duration of the step's dominant kernels, each launched through the C ABI.
 
     kernels: the fused full-head forward / backward kernels, timed with the library's HIP
@@ -105,8 +109,19 @@ def _kernel_profile(x, reps=10):
     ws, nws = _lib.seg_workspace(B, T, H, K, V, C, False, torch.bfloat16, dev)
     tok = B * T * H
     hbytes = seq.NC * H * K * V * BF
+    gs = x["gamma"]
     # (entry point, kernel name, timing slot, algorithmic bytes of the kernel per launch)
     runs = [
+        ("simple_chunk_fwd",
+         lambda: call("tops_gla_simple_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(gs), 0, ptr(h0),
+                      ptr(o), ptr(ht), ptr(h), ptr(ws), nws, sc, *lay),
+         "head_fwd_kernel", 0, tok * (2 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes),
+        ("simple_chunk_bwd",
+         lambda: call("tops_gla_simple_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(gs), 0, ptr(h0),
+                      ptr(h), ptr(do), ptr(dht), ptr(dq), ptr(dk), ptr(dv), None, ptr(dh0),
+                      None, ptr(ws), nws, sc, *lay),
+         "head_bwd_kernel", 1, tok * (4 * K + 3 * V) * BF + STATE_BYTES * 2 + hbytes),
+    ] if op == "simple_gla" else [
         ("chunk_fwd",
          lambda: call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(o),
                       ptr(ht), ptr(h), ptr(ws), nws, sc, *lay),
@@ -204,6 +219,10 @@ def main():
     ap.add_argument("--profile-reps", type=int, default=10)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 512 MiB device copy (counter calibration)")
+    ap.add_argument("--op", choices=("chunk_gla", "simple_gla"), default="chunk_gla",
+                    help="simple_gla: the same shape with a per-head constant log-decay "
+                         "(chunk_gla(g_gamma=...), the scalar-gate kernels); not the headline "
+                         "metric, no CPU baseline")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the GLA path shards over batch and "
@@ -223,6 +242,14 @@ def main():
                             chunk_size=C)
         return torch.autograd.grad((o, ht), (lq, lk, lv, lg, lh0), (x["do"], x["dht"]))
 
+    if a.op == "simple_gla":
+        gg = x["gamma"].reshape(H, 1)
+
+        def step():  # noqa: F811
+            o, ht = G.chunk_gla(lq, lk, lv, g_gamma=gg, initial_state=lh0,
+                                output_final_state=True, chunk_size=C)
+            return torch.autograd.grad((o, ht), (lq, lk, lv, lh0), (x["do"], x["dht"]))
+
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize(dev)
@@ -236,8 +263,10 @@ def main():
     ms = e0.elapsed_time(e1) / a.steps
     tokens_s = B * T / (ms * 1e-3)
 
+    simple = a.op == "simple_gla"
     out = {
-        "metric": METRIC,
+        "metric": METRIC if not simple else
+        "chunk_gla g_gamma (simple GLA) fwd+bwd tokens/s, B4 T8192 H16 K=V=128",
         "value": round(tokens_s, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -249,25 +278,29 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "chunk_gla fwd+bwd (BASELINE configs[3])", "B": B, "T": T,
+        "config": {"workload": "chunk_gla fwd+bwd (BASELINE configs[3])" if not simple else
+                   "chunk_gla fwd+bwd, per-head g_gamma, BASELINE configs[3] shape",
+                   "B": B, "T": T,
                    "H": H, "K": K, "V": V, "chunk_size": C, "h0": True, "dht": True,
                    "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
         "tflops": round(FLOPS_STEP / (ms * 1e-3) / 1e12, 2),
         "mfma_frac": round(FLOPS_STEP / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
     }
+    if simple:   # the flop count of the per-element form does not describe this op
+        del out["tflops"], out["mfma_frac"]
     if not a.no_kernel_profile:
-        prof, stages = _kernel_profile(x, max(1, a.profile_reps))
+        prof, stages = _kernel_profile(x, max(1, a.profile_reps), a.op)
         dom = max(prof, key=lambda n: prof[n]["ms"])
         d = prof[dom]
         out["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": d["gbs"],
                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
-                           "traffic": _measured_traffic(dom)}
+                           "traffic": None if simple else _measured_traffic(dom)}
         out["kernels"] = prof
         out["stages"] = stages
     if a.calibrate_copy:
         _copy_calibration(dev)
-    if not a.no_cpu_baseline:
+    if not a.no_cpu_baseline and not simple:
         out["cpu_baseline"] = _cpu_baseline(a.cpu_heads)
     print(json.dumps(out), flush=True)
 
