@@ -63,6 +63,19 @@ struct HTilesN {
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// acc + sum of the products of 8 bf16 pairs (v_dot2c_f32_bf16: fp32 accumulation)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot8_bf16(uint4 a, uint4 b, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.x),
+                                        __builtin_bit_cast(bf16x2_t, b.x), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.y),
+                                        __builtin_bit_cast(bf16x2_t, b.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.z),
+                                        __builtin_bit_cast(bf16x2_t, b.z), acc, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.w),
+                                         __builtin_bit_cast(bf16x2_t, b.w), acc, false);
+}
+
 __device__ __forceinline__ void unpack8(const uint4& u, float (&x)[8]) {
   x[0] = bf16_lo(u.x); x[1] = bf16_hi(u.x);
   x[2] = bf16_lo(u.y); x[3] = bf16_hi(u.y);
@@ -838,9 +851,10 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 // h (state entering the chunk) comes from the forward's per-chunk states; its MFMA
 // fragments are read straight from HBM (16 bytes per lane).
 // Waves: dq/dk own KTW k tiles x RT row tiles, dv^T VTW v tiles x JT row tiles, dh as in
-// the scans. A chunk's inputs are fetched when the chunk starts: this kernel has no
-// registers left to hold the next chunk in flight, and spilling them costs far more than
-// the exposed load latency (the block's 8 waves and the other blocks keep HBM busy).
+// the scans. The next chunk's gates (needed first, by the cumsum) are fetched during the
+// epilogue; its q, k, v, do and h when it starts (the cumsum runs under those loads). There
+// are no registers to hold more of the next chunk in flight: prefetching q and k as well
+// measured slower (spills).
 // ---------------------------------------------------------------------------
 // SG (scalar gates): q2 = scale q 2^{G_i} for the dh update and G (one float per row).
 template <int KP, int VP, int NW, bool SG = false>
@@ -934,6 +948,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   const int nsteps = sg.ce - sg.cb;
   const long rsK = (long)H * K, rsV = (long)H * V;
   const long KV = (long)K * V;
+  const float inv_scale = 1.f / p.scale;   // uniform
 
   const int cg = tid % M::NCG, rs = tid / M::NCG;
   const int vg = tid % MV::NCG, vrs = tid / MV::NCG;
@@ -957,16 +972,26 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
     t0 = sg.bos + ci * HC;
     len = min(HC, sg.eos - t0);
   };
-  auto issue_main = [&](int step) {
+  auto issue_qk = [&](int step) {
     int t0, len, ci;
     chunk_of(step, t0, len, ci);
-    const long oa = (long)t0 * rsK + (long)hh * K, ov = (long)t0 * rsV + (long)hh * V;
+    const long oa = (long)t0 * rsK + (long)hh * K;
     hload<RPT>(Rq, q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<RPT>(Rk, k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+  };
+  auto issue_qkg = [&](int step) {
+    int t0, len, ci;
+    chunk_of(step, t0, len, ci);
+    const long oa = (long)t0 * rsK + (long)hh * K;
     if constexpr (SG)
       Rs = p.gs[(long)(t0 + min(lane, len - 1)) * p.gs_ts + hh];
     else
       hload<RPT>(Rg, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+  };
+  auto issue_vd = [&](int step) {
+    int t0, len, ci;
+    chunk_of(step, t0, len, ci);
+    const long ov = (long)t0 * rsV + (long)hh * V;
     hload<VRPT>(Rv, v + ov, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
     hload<VRPT>(Rd, dout + ov, (uint32_t)rsV, vrs * VRPT, len, vg * 8, V);
   };
@@ -984,10 +1009,12 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   };
 
 
+  if (nsteps > 0) issue_qkg(0);
   for (int step = 0; step < nsteps; ++step) {
     int t0, len, ci;
     chunk_of(step, t0, len, ci);
-    issue_main(step);
+    issue_qk(step);
+    issue_vd(step);
     issue_h(step);
 
     // ---- (1) cumsum, gating; dh' = fe (.) dh to LDS ----
@@ -1142,13 +1169,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         Frag<bf16> yh;
         yh.d = mask16(Rh[t][f], (hk < K && f * 32 + 8 * (lane >> 4) < V) ? ~0u : 0u);
         const Frag<bf16> ydh = ld_frag(sDh + hk * PVP + f * 32 + 8 * (lane >> 4));
-        {
-          float a8[8], b8[8];
-          unpack8(yh.d, a8);
-          unpack8(ydh.d, b8);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) hdp[t] += a8[e] * b8[e];
-        }
+        hdp[t] = dot8_bf16(yh.d, ydh.d, hdp[t]);
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
           const int ro = (rt0 + i) * 16 + (lane & 15);
@@ -1246,7 +1267,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
     for (int j = 0; j < NTK; ++j) {
       const float d = SG ? sFe[(kt0 + j) * 16 + (lane & 15)]
-                         : sFe[(kt0 + j) * 16 + (lane & 15)] / p.scale;
+                         : sFe[(kt0 + j) * 16 + (lane & 15)] * inv_scale;
 #pragma unroll
       for (int i = 0; i < NTV; ++i) acc[i][j] *= d;
     }
@@ -1286,10 +1307,14 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
           XK[ro * PX + hk] = ak[t][i][rr];
         }
       }
-      if (w < NKG && lane < 16) sHd[hk] = hdp[t] * (sFr[hk] / p.scale);   // 2^r sum h dh'
+      if (w < NKG && lane < 16) sHd[hk] = hdp[t] * (sFr[hk] * inv_scale);   // 2^r sum h dh'
       if (lane < 16) sDkc[(w / NKG) * KP + hk] = dkc[t];
     }
     __syncthreads();
+
+    // the next chunk's q, k and gates (needed first: cumsum and gating): their registers
+    // are free from here on, and the loads run under the epilogue
+    if (step + 1 < nsteps) issue_qkg(step + 1);
 
     // ---- (5) epilogue: dq, dk, dg rows ----
     float pr[RPT][8];
