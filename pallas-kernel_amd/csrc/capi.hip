@@ -119,18 +119,25 @@ bool use_head(int dtype, int chunk, int64_t K, int64_t V, bool g_is_cumsum,
 // Sequence segmentation of the full-head kernels when the caller's workspace holds it
 // (state part first, then the decays); otherwise NS = 1.
 void seg_setup(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void* ws,
-               int64_t ws_bytes, int& NS, int& SL, float*& st, float*& gm) {
+               int64_t ws_bytes, int& NS, int& SL, float*& st, float*& gm,
+               void** gate = nullptr) {
   tops::head_seg_plan(si.N, (int)H, si.T, si.C, si.cu != nullptr, NS, SL,
                       tops::head_vtiles((int)K, (int)V));
   const long need = tops::head_seg_ws_bytes(si.N, NS, (int)H, (int)K, (int)V);
   st = gm = nullptr;
-  if (NS <= 1 || ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 255u) != 0) {
+  if (gate) *gate = nullptr;
+  const bool usable = ws != nullptr && ((uintptr_t)ws & 255u) == 0;
+  if (NS <= 1 || !usable || ws_bytes < need) {
     NS = 1;
     SL = 0;
-    return;
+  } else {
+    st = (float*)ws;
+    gm = (float*)((char*)ws + (long)si.N * NS * H * K * V * 4);
   }
-  st = (float*)ws;
-  gm = (float*)((char*)ws + (long)si.N * NS * H * K * V * 4);
+  // the wide forward's per-chunk gating workspace follows the segment part
+  const long gbytes = si.cu ? 0 : tops::head_gate_ws_bytes(si.N, si.T, (int)H, (int)K, (int)V);
+  const long seg = NS > 1 ? need : 0;
+  if (gate && gbytes > 0 && usable && ws_bytes >= seg + gbytes) *gate = (char*)ws + seg;
 }
 
 }  // namespace
@@ -193,7 +200,9 @@ int64_t tops_gla_chunk_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int6
   int NS, SL;
   tops::head_seg_plan((int)B, (int)H, (int)T, chunk_size, varlen != 0, NS, SL,
                       tops::head_vtiles((int)K, (int)V));
-  return tops::head_seg_ws_bytes((int)B, NS, (int)H, (int)K, (int)V);
+  const long seg = NS > 1 ? tops::head_seg_ws_bytes((int)B, NS, (int)H, (int)K, (int)V) : 0;
+  const long gate = varlen ? 0 : tops::head_gate_ws_bytes((int)B, (int)T, (int)H, (int)K, (int)V);
+  return seg + gate;
 }
 
 int tops_gla_chunk_local_cumsum(const void* g, void* out, int64_t B, int64_t T, int64_t H,
@@ -383,7 +392,8 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
     f.o = o;
     f.h_out = h_ws;
     f.ht = ht;
-    seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, f.NS, f.SL, f.seg_state, f.seg_gam);
+    seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, f.NS, f.SL, f.seg_state, f.seg_gam,
+              &f.gate_ws);
     f.scale = scale;
     f.H = (int)H;
     f.K = (int)K;

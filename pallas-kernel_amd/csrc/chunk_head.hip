@@ -531,6 +531,116 @@ __global__ __launch_bounds__(256) void head_combine_kernel(float* __restrict__ s
 }
 
 // ---------------------------------------------------------------------------
+// Per-chunk gating of wide heads (K = 256, several V tiles per head). Every V tile's block of
+// the fused forward needs the same gated tiles, intra matrix and column factors of a chunk;
+// this kernel makes them once per (chunk, head) into a caller workspace, and the forward's
+// PRE build reads them instead of gating for itself. Workspace entry of chunk c, head h at
+// (c * H + h) * GW bytes: qg bf16 [64][K], kg bf16 [64][K], A bf16 [64][64] (scaled, causal),
+// factors f32 [3][K]: scale 2^r, 2^r, 2^{gamma - r}.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr long gate_ws_entry(int K) {
+  return 2L * HC * K * 2 + (long)HC * HC * 2 + 3L * K * 4;
+}
+
+template <int KP>
+struct GPLayout {
+  static constexpr int PKP = pitch_of<bf16>(KP);
+  static constexpr int qg = 0;
+  static constexpr int kg = qg + HC * PKP * 2;
+  static constexpr int tot = kg + HC * PKP * 2;
+  static constexpr int first = tot + HNW * KP * 4;
+  static constexpr int bytes = first + KP * 4;
+};
+
+template <int KP>
+__global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
+  using M = HMap<KP>;
+  using Lay = GPLayout<KP>;
+  constexpr int RPT = M::RPT, PKP = Lay::PKP;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
+  bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
+  float* sTot = reinterpret_cast<float*>(smem + Lay::tot);
+  float* sFirst = reinterpret_cast<float*>(smem + Lay::first);
+  const int H = p.H, K = p.K;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hh = blockIdx.x % H, ci = blockIdx.x / H, seq = blockIdx.y;
+  int bos, eos, c0, nc;
+  seq_range(p.si, seq, bos, eos, c0, nc);
+  if (ci >= nc) return;   // uniform
+  const int t0 = bos + ci * HC, len = min(HC, eos - t0);
+  const long rsK = (long)H * K;
+  const int cg = tid % M::NCG, rs = tid / M::NCG;
+  const bool colA = cg * 8 < K;
+  const long oa = (long)t0 * rsK + (long)hh * K;
+  uint4 Rq[RPT], Rk[RPT], Rg[RPT];
+  hload<RPT>(Rq, (const bf16*)p.q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+  hload<RPT>(Rk, (const bf16*)p.k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+  hload<RPT>(Rg, (const bf16*)p.g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+  uint4 gm[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) gm[j] = mask16(Rg[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
+  float gt[RPT][8], gam[8], first[8];
+  head_cumsum<KP>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+  unsigned char* ent = (unsigned char*)p.gate_ws + ((long)(c0 + ci) * H + hh) * gate_ws_entry(K);
+  bf16* gq = (bf16*)ent;
+  bf16* gk = gq + HC * K;
+  bf16* gA = gk + HC * K;
+  float* gf = (float*)(gA + HC * HC);
+  float r[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = 0.5f * (first[e] + gam[e]);
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int row = rs * RPT + j;
+    const uint32_t m = (colA && row < len) ? ~0u : 0u;
+    float xq[8], xk[8];
+    unpack8(mask16(Rq[j], m), xq);
+    unpack8(mask16(Rk[j], m), xk);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = gt[j][e] - r[e];
+      xq[e] *= exp2_hw(d);
+      xk[e] *= exp2_hw(-d);
+    }
+    const uint4 pq = pack8(xq), pk = pack8(xk);
+    *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pq;
+    *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pk;
+    if (colA) {
+      *reinterpret_cast<uint4*>(gq + row * K + cg * 8) = pq;
+      *reinterpret_cast<uint4*>(gk + row * K + cg * 8) = pk;
+    }
+  }
+  if (rs == 0 && colA) {
+    float f0[8], f1[8], f2[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      f1[e] = exp2_hw(r[e]);
+      f0[e] = p.scale * f1[e];
+      f2[e] = exp2_hw(gam[e] - r[e]);
+    }
+    st_f8(gf + cg * 8, f0);
+    st_f8(gf + K + cg * 8, f1);
+    st_f8(gf + 2 * K + cg * 8, f2);
+  }
+  __syncthreads();
+  // the 16 tiles of A (the upper ones as zeros), two per wave
+  for (int t = w; t < 16; t += HNW) {
+    const int mi = t >> 2, ni = t & 3;
+    f32x4 at = zero4();
+    if (ni <= mi)
+      mma_tile<bf16>(at, sQg + mi * 16 * PKP, PKP, sKg + ni * 16 * PKP, PKP, KP, lane);
+    const int jj = ni * 16 + (lane & 15);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int ii = mi * 16 + 4 * (lane >> 4) + rr;
+      gA[ii * HC + jj] = from_f32<bf16>(jj <= ii ? at[rr] * p.scale : 0.f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Fused forward: per chunk (base-2 gates, r = (g~_first + gamma) / 2 per column)
 //   qg = q 2^{g~-r}, kg = k 2^{r-g~}, kd = kg 2^{gamma-r}, A = scale tril(qg kg^T),
 //   o = A v + qg (scale 2^r h), h <- 2^{gamma} h + kd^T v.
@@ -561,7 +671,7 @@ struct HFLayout {
   static constexpr int bytes = grow + (SG ? HC * 4 : 0);
 };
 
-template <int KP, int VP, bool SG>
+template <int KP, int VP, bool SG, bool PRE = false>
 __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   using M = HMap<KP>;
   using MV = HMap<VP>;
@@ -571,8 +681,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   constexpr int PKP = Lay::PKP, PVP = Lay::PVP, PA = Lay::PA;
   constexpr int NTV = TL::NTV, NTK = TL::NTK;
   // chunks of inputs in flight: two register sets, one for the wide head (K = 256), whose
-  // rows take twice the registers
+  // rows take twice the registers (and whose loop body is only inlined once)
   constexpr int PF = KP > 128 ? 1 : 2;
+  static_assert(!PRE || (!SG && !Lay::KD), "PRE: wide heads with per-element gates");
   static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
@@ -614,9 +725,12 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   const int vg = tid % MV::NCG, vrs = tid / MV::NCG;
   const bool colA = cg * 8 < K, colB = vg * 8 < Vw;
 
-  // zero A once (its upper triangle is never written)
+  // zero A once (its upper triangle is never written); PRE: the column factors past K too
   for (int i = tid; i < HC * PA / 8; i += HNT)
     reinterpret_cast<uint4*>(sA)[i] = make_uint4(0, 0, 0, 0);
+  if constexpr (PRE) {
+    for (int i = tid; i < KP; i += HNT) sRs[i] = sPre[i] = sPost[i] = 0.f;
+  }
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
   f32x4 acc[NTV][NTK];
@@ -629,20 +743,33 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   struct Regs {
     uint4 q[RPT], k[RPT], g[RPT], v[VRPT];
     float gs;   // SG: the gate of row `lane`
+    uint4 a, f;  // PRE: 16 bytes of A, 16 bytes of the factors
   };
   auto issue = [&](int step, Regs& R) {
     const int st = min(step, nsteps - 1);
     const int t0 = sg.bos + (sg.cb + st) * HC;
     const int len = min(HC, sg.eos - t0);
     const long oa = (long)t0 * rsK + (long)hh * K;
-    hload<RPT>(R.q, q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
-    hload<RPT>(R.k, k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
-    if constexpr (SG)
-      R.gs = p.gs[(long)(t0 + min(lane, len - 1)) * p.gs_ts + hh];
-    else
-      hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
-    hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V + cv, (uint32_t)rsV, vrs * VRPT, len,
-                vg * 8, Vw);
+    if constexpr (PRE) {
+      const unsigned char* ent = (const unsigned char*)p.gate_ws +
+                                 ((long)(sg.c0 + sg.cb + st) * H + hh) * gate_ws_entry(K);
+      const bf16* gq = (const bf16*)ent;
+      hload<RPT>(R.q, gq, (uint32_t)K, rs * RPT, HC, cg * 8, K);
+      hload<RPT>(R.k, gq + HC * K, (uint32_t)K, rs * RPT, HC, cg * 8, K);
+      R.a = ld16(gq + 2 * HC * K, (uint32_t)tid * 16u);   // 64 x 64 bf16 = 512 x 16 bytes
+      R.f = ld16(gq + 2 * HC * K + HC * HC, (uint32_t)min(tid, 3 * K / 4 - 1) * 16u);
+      hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V + cv, (uint32_t)rsV, vrs * VRPT, len,
+                  vg * 8, Vw);
+    } else {
+      hload<RPT>(R.q, q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+      hload<RPT>(R.k, k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+      if constexpr (SG)
+        R.gs = p.gs[(long)(t0 + min(lane, len - 1)) * p.gs_ts + hh];
+      else
+        hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+      hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V + cv, (uint32_t)rsV, vrs * VRPT, len,
+                  vg * 8, Vw);
+    }
   };
 
   auto body = [&](int step, Regs& R) {
@@ -652,7 +779,27 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 
     // ---- (1) cumsum, gating ----
     float Gl = 0.f, gam_s = 0.f;   // SG: G of row `lane`, the chunk's total (base 2)
-    if constexpr (SG) {
+    if constexpr (PRE) {   // gated tiles, A and factors as made by head_gate_kernel
+      __syncthreads();   // the previous chunk's reads of the tiles are done
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {   // (rows past the chunk are zeros in the workspace)
+        const int row = rs * RPT + j;
+        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = mask16(R.q[j], colA ? ~0u : 0u);
+        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = mask16(R.k[j], colA ? ~0u : 0u);
+      }
+#pragma unroll
+      for (int j = 0; j < VRPT; ++j) {
+        const int row = vrs * VRPT + j;
+        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) =
+            mask16(R.v[j], (colB && row < len) ? ~0u : 0u);
+      }
+      *reinterpret_cast<uint4*>(sA + (tid >> 3) * PA + (tid & 7) * 8) = R.a;
+      if (tid < 3 * K / 4) {   // factors: scale 2^r, 2^r, 2^{gamma-r} (K floats each)
+        const int i4 = tid * 4, which = i4 / K, col = i4 % K;
+        const int off = which == 0 ? Lay::rsc : which == 1 ? Lay::pre : Lay::post;
+        *reinterpret_cast<uint4*>(smem + off + col * 4) = R.f;
+      }
+    } else if constexpr (SG) {
       // scalar gates: A's decay 2^{G_i - G_j} is applied after q k^T, the inter term's 2^{G_i}
       // after q h', and the update runs on v 2^{gamma - G_j}; every factor is <= 1 for
       // decaying gates, whatever their size
@@ -748,7 +895,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     __syncthreads();
 
     // ---- (2) A (lower tiles), h_n to HBM, h' = scale 2^r h into LDS ----
-    for (int t = w; t < 10; t += HNW) {
+    for (int t = w; t < (PRE ? 0 : 10); t += HNW) {
       const int mi = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
       const int ni = t - mi * (mi + 1) / 2;
       f32x4 at = zero4();
@@ -1435,6 +1582,14 @@ void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL, in
   }
 }
 
+// Per-chunk gating workspace of the wide forward: K = 256 heads split into three or more V
+// tiles (each tile's block would otherwise gate the same chunk again); fixed-length only.
+long head_gate_ws_bytes(int N, int T, int H, int K, int V) {
+  if (head_kp(K) != 256 || head_vtiles(K, V) < 3 || N <= 0 || T <= 0) return 0;
+  const long nt = (T + HC - 1) / HC;
+  return (long)N * nt * H * gate_ws_entry(K);
+}
+
 long head_seg_ws_bytes(int N, int NS, int H, int K, int V) {
   if (NS <= 1) return 0;
   const long st = (long)N * NS * H * K * V * 4;
@@ -1525,6 +1680,27 @@ template <int KP, int VP>
 static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   const long blocks = (long)p.si.N * p.NS * p.H * ((p.V + VP - 1) / VP);
   if (blocks == 0) return hipSuccess;
+  if constexpr (KP == 256) {
+    if (p.g && p.gate_ws) {   // per-chunk gating once, then the V tiles' blocks
+      using GL = GPLayout<KP>;
+      hipError_t e = hipFuncSetAttribute((const void*)head_gate_kernel<KP>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, GL::bytes);
+      if (e != hipSuccess) return e;
+      const int nt = (p.si.T + HC - 1) / HC;
+      hipLaunchKernelGGL((head_gate_kernel<KP>), dim3((unsigned)(nt * p.H), (unsigned)p.si.N),
+                         dim3(HNT), GL::bytes, st, p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      using Lay = HFLayout<KP, VP, false>;
+      e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP, false, true>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
+      if (e != hipSuccess) return e;
+      ktimer_mark(KT_HEAD_FWD, false, st);
+      hipLaunchKernelGGL((head_fwd_kernel<KP, VP, false, true>), dim3((unsigned)blocks),
+                         dim3(HNT), Lay::bytes, st, p);
+      ktimer_mark(KT_HEAD_FWD, true, st);
+      return hipGetLastError();
+    }
+  }
   return p.g ? launch_head_fwd_sg<KP, VP, false>(p, st, blocks)
              : launch_head_fwd_sg<KP, VP, true>(p, st, blocks);
 }

@@ -188,6 +188,7 @@ bool head_bwd_supported(int K, int V);                                     // + 
 int head_vtiles(int K, int V);   // V tiles (blocks per segment and head)
 void head_seg_plan(int N, int H, int T, int C, bool varlen, int& NS, int& SL, int VT);
 long head_seg_ws_bytes(int N, int NS, int H, int K, int V);
+long head_gate_ws_bytes(int N, int T, int H, int K, int V);   // 0 unless it pays
 
 // Full-head kernels. Gates: g ([T, H, K] bf16, raw) or, with g == nullptr, the scalar
 // gates of simple GLA: gate(t, h) = gs[t * gs_ts + h] for every key column (float; gs_ts = H
@@ -216,6 +217,7 @@ struct HeadFwdArgs {
   const float* h0;        // nullable
   void* o;
   void* h_out;            // [NC, H, K, V] bf16 (nullable)
+  void* gate_ws;          // per-chunk gating workspace of wide heads (nullable; fixed length)
   float* ht;              // nullable
   float* seg_state;       // NS > 1 only
   float* seg_gam;
