@@ -39,12 +39,12 @@ constexpr int HNT = 512;  // threads per block
 constexpr int HNW = HNT / 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int KP, int NT = HNT>
+template <int KP, int NT = HNT, int CR = HC>
 struct HMap {
   static constexpr int NCG = KP / 8;     // 8-column groups
   static constexpr int NRS = NT / NCG;   // row segments
-  static constexpr int RPT = HC / NRS;   // rows per thread
-  static_assert(RPT >= 1 && NRS * RPT == HC, "thread mapping");
+  static constexpr int RPT = CR / NRS;   // rows per thread (CR rows per tile)
+  static_assert(RPT >= 1 && NRS * RPT == CR, "thread mapping");
 };
 
 // State / output tile split over the 8 waves: v tiles by halves, k tiles by quarters.
@@ -139,17 +139,18 @@ __device__ __forceinline__ Seg seg_of(const SeqInfo& si, int seq, int s, int NS,
   return r;
 }
 
-// Base-2 chunk-local cumsum of an [HC x KP] gate tile held as RPT rows x 8 columns per
-// thread: gt holds the raw gates (already masked) on entry and g~ log2 e on return; gam =
-// its last row, first = its row 0. sTot [NT/64][KP], sFirst [KP]. One barrier.
-template <int KP, int NT>
-using GateRows = float[HMap<KP, NT>::RPT][8];
+// Base-2 chunk-local cumsum of a [CR x KP] gate tile (CR = HC rows unless stated) held as
+// RPT rows x 8 columns per thread: gt holds the raw gates (already masked) on entry and
+// g~ log2 e on return; gam = its last row, first = its row 0. sTot [NT/64][KP],
+// sFirst [KP]. One barrier.
+template <int KP, int NT, int CR = HC>
+using GateRows = float[HMap<KP, NT, CR>::RPT][8];
 
-template <int KP, int NT = HNT>
-__device__ __forceinline__ void head_cumsum_f(GateRows<KP, NT>& gt, float (&gam)[8],
+template <int KP, int NT = HNT, int CR = HC>
+__device__ __forceinline__ void head_cumsum_f(GateRows<KP, NT, CR>& gt, float (&gam)[8],
                                               float (&first)[8], float* sTot, float* sFirst,
                                               int cg, int rs, int lane, int w) {
-  using M = HMap<KP, NT>;
+  using M = HMap<KP, NT, CR>;
 #pragma unroll
   for (int j = 0; j < M::RPT; ++j) {
 #pragma unroll
@@ -195,14 +196,14 @@ __device__ __forceinline__ void head_cumsum_f(GateRows<KP, NT>& gt, float (&gam)
 }
 
 // The same from the raw bf16 tile (16 bytes = 8 columns per row).
-template <int KP, int NT = HNT>
-__device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP, NT>::RPT],
-                                            float (&gt)[HMap<KP, NT>::RPT][8], float (&gam)[8],
-                                            float (&first)[8], float* sTot, float* sFirst,
-                                            int cg, int rs, int lane, int w) {
+template <int KP, int NT = HNT, int CR = HC>
+__device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP, NT, CR>::RPT],
+                                            float (&gt)[HMap<KP, NT, CR>::RPT][8],
+                                            float (&gam)[8], float (&first)[8], float* sTot,
+                                            float* sFirst, int cg, int rs, int lane, int w) {
 #pragma unroll
-  for (int j = 0; j < HMap<KP, NT>::RPT; ++j) unpack8(graw[j], gt[j]);
-  head_cumsum_f<KP, NT>(gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+  for (int j = 0; j < HMap<KP, NT, CR>::RPT; ++j) unpack8(graw[j], gt[j]);
+  head_cumsum_f<KP, NT, CR>(gt, gam, first, sTot, sFirst, cg, rs, lane, w);
 }
 
 // Scalar gates (simple GLA, g_gamma): one float per row and head, the same for every key
@@ -293,11 +294,11 @@ __device__ __forceinline__ void store_state_bf16(const f32x4 (&acc)[NTV][NTK], b
     }
 }
 
-// acc = acc * decay[k] + X^T Y over the chunk: X = b [c][v] (sB), Y = a [c][k] (sA), both
-// read with transposed fragments.
+// acc = acc * decay[k] + X^T Y over the chunk's CR rows: X = b [c][v] (sB), Y = a [c][k]
+// (sA), both read with transposed fragments.
 // With `post`, the result is then scaled by post[k] (the update then reads
 // acc = post (.) (acc * decay + X^T Y)).
-template <int NTV, int NTK>
+template <int NTV, int NTK, int CR = HC>
 __device__ __forceinline__ void state_update(f32x4 (&acc)[NTV][NTK], const bf16* sB, int PB,
                                              const bf16* sA, int PA, const float* decay,
                                              int vt0, int kt0, int lane,
@@ -309,7 +310,7 @@ __device__ __forceinline__ void state_update(f32x4 (&acc)[NTV][NTK], const bf16*
     for (int i = 0; i < NTV; ++i) acc[i][j] *= d;
   }
 #pragma unroll
-  for (int kk = 0; kk < HC; kk += 32) {
+  for (int kk = 0; kk < CR; kk += 32) {
     Frag<bf16> x[NTV], y[NTK];
 #pragma unroll
     for (int i = 0; i < NTV; ++i) x[i] = ld_frag_t(sB + kk * PB + (vt0 + i) * 16, PB, lane);
@@ -341,19 +342,38 @@ __host__ __device__ constexpr int head_vp(int KP, int V) {
 // ---------------------------------------------------------------------------
 // State scan: forward h (a = k, b = v) or reverse dh (a = q, b = do)
 // ---------------------------------------------------------------------------
-template <int KP, int VP, bool REV, int NT, bool SG>
+// LDS of head_scan_kernel: the gated a tile and the b tile of CR rows, cumsum scratch.
+template <int KP, int VP, int NT, int CR>
+struct HSLayout {
+  static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP);
+  static constexpr int a = 0;
+  static constexpr int b = a + CR * PKP * 2;
+  static constexpr int tot = b + CR * PVP * 2;
+  static constexpr int first = tot + (NT / 64) * KP * 4;
+  static constexpr int gam = first + KP * 4;
+  static constexpr int bytes = gam + KP * 4;
+};
+
+// CR = HC: one step per chunk (every pass). CR = 2 HC (pass 1 only, which needs the
+// segment's final state and total decay but no per-chunk state): one step per pair of
+// chunks, a 128-row tile with its own cumsum; the recurrence is the same row by row, so the
+// final state is unchanged, and every factor stays <= 1.
+template <int KP, int VP, bool REV, int NT, bool SG, int CR = HC>
 __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
-  using MA = HMap<KP, NT>;
-  using MB = HMap<VP, NT>;
+  using MA = HMap<KP, NT, CR>;
+  using MB = HMap<VP, NT, CR>;
   using TL = HTilesN<KP, VP, NT / 64>;
+  using Lay = HSLayout<KP, VP, NT, CR>;
+  static_assert(CR == HC || CR == 2 * HC, "chunk rows");
   constexpr int RPT = MA::RPT, VRPT = MB::RPT;
-  constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP);
+  constexpr int PKP = Lay::PKP, PVP = Lay::PVP;
   constexpr int NTV = TL::NTV, NTK = TL::NTK;
-  __shared__ __attribute__((aligned(16))) bf16 sA[HC * PKP];
-  __shared__ __attribute__((aligned(16))) bf16 sB[HC * PVP];
-  __shared__ __attribute__((aligned(16))) float sTot[(NT / 64) * KP];
-  __shared__ __attribute__((aligned(16))) float sFirst[KP];
-  __shared__ __attribute__((aligned(16))) float sGam[KP];
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  bf16* sA = reinterpret_cast<bf16*>(smem + Lay::a);
+  bf16* sB = reinterpret_cast<bf16*>(smem + Lay::b);
+  float* sTot = reinterpret_cast<float*>(smem + Lay::tot);
+  float* sFirst = reinterpret_cast<float*>(smem + Lay::first);
+  float* sGam = reinterpret_cast<float*>(smem + Lay::gam);
 
   const bf16* __restrict__ a = (const bf16*)p.a;
   const bf16* __restrict__ b = (const bf16*)p.b;
@@ -370,7 +390,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   const int nsl = p.ns_launch;
   const int s = p.s_begin + (L / H) % nsl;
   const Seg sg = seg_of(p.si, (L / H) / nsl, s, p.NS, p.SL);
-  const int nsteps = sg.ce - sg.cb;
+  const int nsteps = CR == HC ? sg.ce - sg.cb : (sg.ce - sg.cb + 1) / 2;
   const bool first_seg = REV ? (s == p.NS - 1) : (s == 0);
   const bool last_seg = REV ? (s == 0) : (s == p.NS - 1);
   const long rsK = (long)H * K, rsV = (long)H * V;
@@ -395,11 +415,25 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     uint4 a[RPT], g[RPT], b[VRPT];
     float gs[RPT];
   };
+  // rows [t0, t0 + len) of step `step`; ci = its first chunk. Pairs of chunks (CR = 2 HC)
+  // are taken in flow order, so an odd count leaves the segment's last chunk in flow order
+  // on its own; len never crosses the segment's end.
+  auto span = [&](int step, int& t0, int& len, int& ci) {
+    if constexpr (CR == HC) {
+      ci = REV ? (sg.ce - 1 - step) : (sg.cb + step);
+      t0 = sg.bos + ci * HC;
+      len = min(HC, sg.eos - t0);
+    } else {
+      const int lo = REV ? max(sg.cb, sg.ce - 2 * step - 2) : sg.cb + 2 * step;
+      const int hi = REV ? sg.ce - 2 * step : min(sg.ce, lo + 2);
+      ci = lo;
+      t0 = sg.bos + lo * HC;
+      len = min(sg.eos, sg.bos + hi * HC) - t0;
+    }
+  };
   auto issue = [&](int step, Regs& R) {
-    const int st = min(step, nsteps - 1);
-    const int ci = REV ? (sg.ce - 1 - st) : (sg.cb + st);
-    const int t0 = sg.bos + ci * HC;
-    const int len = min(HC, sg.eos - t0);
+    int t0, len, ci;
+    span(min(step, nsteps - 1), t0, len, ci);
     const long oa = (long)t0 * rsK + (long)hh * K;
     hload<RPT>(R.a, a + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     if constexpr (SG)
@@ -415,9 +449,8 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   for (int e = 0; e < 8; ++e) gsum[e] = 0.f;
 
   auto body = [&](int step, Regs& R) {
-    const int ci = REV ? (sg.ce - 1 - step) : (sg.cb + step);
-    const int t0 = sg.bos + ci * HC;
-    const int len = min(HC, sg.eos - t0);
+    int t0, len, ci;
+    span(step, t0, len, ci);
     float gt[RPT][8], gam[8], first[8];
     if constexpr (SG) {
 #pragma unroll
@@ -426,13 +459,13 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) gt[j][e] = x;
       }
-      head_cumsum_f<KP, NT>(gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+      head_cumsum_f<KP, NT, CR>(gt, gam, first, sTot, sFirst, cg, rs, lane, w);
     } else {
       uint4 gm[RPT];
 #pragma unroll
       for (int j = 0; j < RPT; ++j)
         gm[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
-      head_cumsum<KP, NT>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+      head_cumsum<KP, NT, CR>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
     }
     (void)first;
 #pragma unroll
@@ -462,10 +495,12 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     }
     issue(step + 2, R);
     __syncthreads();
-    if (s_all)   // state entering the chunk (forward) / leaving it (reverse)
-      store_state_bf16<NTV, NTK>(acc, s_all + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K, Vw,
-                                 vt0, kt0, lane, V);
-    state_update<NTV, NTK>(acc, sB, PVP, sA, PKP, sGam, vt0, kt0, lane);
+    if constexpr (CR == HC) {
+      if (s_all)   // state entering the chunk (forward) / leaving it (reverse)
+        store_state_bf16<NTV, NTK>(acc, s_all + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K,
+                                   Vw, vt0, kt0, lane, V);
+    }
+    state_update<NTV, NTK, CR>(acc, sB, PVP, sA, PKP, sGam, vt0, kt0, lane);
   };
 
   if (nsteps > 0) {
@@ -1597,16 +1632,31 @@ long head_seg_ws_bytes(int N, int NS, int H, int K, int V) {
   return st + (gm + 255) / 256 * 256;
 }
 
+template <int KP, int VP, bool REV, bool SG, int CR>
+static hipError_t launch_head_scan_cr(const HeadScanArgs& p, hipStream_t st, long blocks) {
+  constexpr int NT = HNT;
+  using Lay = HSLayout<KP, VP, NT, CR>;
+  static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
+  const void* fn = (const void*)head_scan_kernel<KP, VP, REV, NT, SG, CR>;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     Lay::bytes);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV, NT, SG, CR>), dim3((unsigned)blocks),
+                     dim3(NT), Lay::bytes, st, p);
+  return hipGetLastError();
+}
+
+// Pass 1 of heads up to 128 wide steps over pairs of chunks (half the serial steps and
+// barriers); the passes that store per-chunk states, and K = 256, step chunk by chunk.
 template <int KP, int VP, bool REV>
 static hipError_t launch_head_scan(const HeadScanArgs& p, hipStream_t st, long blocks) {
-  constexpr int NT = HNT;
-  if (p.g)
-    hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV, NT, false>), dim3((unsigned)blocks),
-                       dim3(NT), 0, st, p);
-  else
-    hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV, NT, true>), dim3((unsigned)blocks),
-                       dim3(NT), 0, st, p);
-  return hipGetLastError();
+  if constexpr (KP <= 128) {
+    if (p.pass == 1)
+      return p.g ? launch_head_scan_cr<KP, VP, REV, false, 2 * HC>(p, st, blocks)
+                 : launch_head_scan_cr<KP, VP, REV, true, 2 * HC>(p, st, blocks);
+  }
+  return p.g ? launch_head_scan_cr<KP, VP, REV, false, HC>(p, st, blocks)
+             : launch_head_scan_cr<KP, VP, REV, true, HC>(p, st, blocks);
 }
 
 template <bool REV>

@@ -332,13 +332,18 @@ def test_north_star_shape_slices():
         check("dh0", to_np(th0.grad[b:b + 1, h:h + 1]), ref[4], "bf16")
 
 
-def test_segmented_scans_match_sequential():
-    """The segment-parallel scans (local states, combine, all segments at once) give the
-    sequential scan's results: tops_gla_chunk_fwd / _bwd with and without the workspace."""
+@pytest.mark.parametrize("B,T,H", [(2, 4096, 4), (1, 2412, 2), (1, 2284, 2)],
+                         ids=["even", "short-last", "odd"])
+def test_segmented_scans_match_sequential(B, T, H):
+    """The segment-parallel scans (local states over chunk pairs, combine, all segments at
+    once) give the sequential scan's results: tops_gla_chunk_fwd / _bwd with and without the
+    workspace. 2412 tokens: 38 chunks (the last partial) in segments of 10, 10, 10, 8 (a
+    short last segment); 2284 tokens: 36 chunks (the last partial) in 4 segments of 9, so
+    every segment's pairs end with a single chunk."""
     from tops import _lib
     from tops._lib import SeqLayout, call, ptr, stream_of
 
-    B, T, H, K, V, C = 2, 4096, 4, 128, 128, 64
+    K, V, C = 128, 128, 64
     q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, 821, gate_div=16.0, h0=True, dht=True,
                                           dtype="bf16")
     d = lambda x: to_dev(x, "bf16")  # noqa: E731
