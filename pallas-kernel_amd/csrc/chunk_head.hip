@@ -811,6 +811,11 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     const int ci = sg.cb + step;
     const int t0 = sg.bos + ci * HC;
     const int len = min(HC, sg.eos - t0);
+    // h_n to HBM first: the vector memory path is idle here (the next chunk's loads are
+    // issued at the end of the gating, and stores queued behind them wait for them)
+    if (hout)
+      store_state_bf16<NTV, NTK>(acc, hout + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K, Vw,
+                                 vt0, kt0, lane, V);
 
     // ---- (1) cumsum, gating ----
     float Gl = 0.f, gam_s = 0.f;   // SG: G of row `lane`, the chunk's total (base 2)
@@ -929,7 +934,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     issue(step + PF, R);
     __syncthreads();
 
-    // ---- (2) A (lower tiles), h_n to HBM, h' = scale 2^r h into LDS ----
+    // ---- (2) A (lower tiles), h' = scale 2^r h into LDS ----
     for (int t = w; t < (PRE ? 0 : 10); t += HNW) {
       const int mi = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
       const int ni = t - mi * (mi + 1) / 2;
@@ -944,9 +949,6 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
         sA[ii * PA + jj] = from_f32<bf16>(jj <= ii ? a : 0.f);
       }
     }
-    if (hout)
-      store_state_bf16<NTV, NTK>(acc, hout + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K, Vw,
-                                 vt0, kt0, lane, V);
 #pragma unroll
     for (int j = 0; j < NTK; ++j) {
       const int kk = (kt0 + j) * 16 + (lane & 15);
