@@ -139,6 +139,31 @@ __device__ __forceinline__ Seg seg_of(const SeqInfo& si, int seq, int s, int NS,
   return r;
 }
 
+// Scans over the four 16-lane rows of a wave, lane l of every row holding the same column
+// (8-column groups of a 128-wide tile): v_permlane16_swap gives each lane its pair partner
+// (rows 0 / 1, 2 / 3), v_permlane32_swap the other half's pair sum; no LDS, no lane indices.
+// Returned: x_0 + .. + x_r (rows4_prefix) or x_r + .. + x_3 (rows4_suffix) for row r.
+__device__ __forceinline__ float rows4_prefix(float x, int lane) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  const float pair = __uint_as_float(p[0]) + __uint_as_float(p[1]);   // x_{2i} + x_{2i+1}
+  float y = (lane & 16) ? pair : x;
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(pair), __float_as_uint(pair),
+                                                  false, false);
+  if (lane & 32) y += __uint_as_float(q[0]);   // rows 2, 3: + the pair sum of rows 0, 1
+  return y;
+}
+__device__ __forceinline__ float rows4_suffix(float x, int lane) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  const float pair = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  float y = (lane & 16) ? x : pair;
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(pair), __float_as_uint(pair),
+                                                  false, false);
+  if (!(lane & 32)) y += __uint_as_float(q[1]);   // rows 0, 1: + the pair sum of rows 2, 3
+  return y;
+}
+
 // Base-2 chunk-local cumsum of a [CR x KP] gate tile (CR = HC rows unless stated) held as
 // RPT rows x 8 columns per thread: gt holds the raw gates (already masked) on entry and
 // g~ log2 e on return; gam = its last row, first = its row 0. sTot [NT/64][KP],
@@ -159,12 +184,17 @@ __device__ __forceinline__ void head_cumsum_f(GateRows<KP, NT, CR>& gt, float (&
   float x[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = gt[M::RPT - 1][e];
+  if constexpr (M::NCG == 16) {
 #pragma unroll
-  for (int d = M::NCG; d < 64; d <<= 1) {
+    for (int e = 0; e < 8; ++e) x[e] = rows4_prefix(x[e], lane);
+  } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float y = __shfl_up(x[e], d);
-      if (lane >= d) x[e] += y;
+    for (int d = M::NCG; d < 64; d <<= 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = __shfl_up(x[e], d);
+        if (lane >= d) x[e] += y;
+      }
     }
   }
   if (lane >= 64 - M::NCG) st_f8(sTot + w * KP + cg * 8, x);   // wave total
@@ -1536,12 +1566,17 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       float x[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = pr[0][e];
+      if constexpr (M::NCG == 16) {
 #pragma unroll
-      for (int d = M::NCG; d < 64; d <<= 1) {
+        for (int e = 0; e < 8; ++e) x[e] = rows4_suffix(x[e], lane);
+      } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float y = __shfl_down(x[e], d);
-          if (lane + d < 64) x[e] += y;
+        for (int d = M::NCG; d < 64; d <<= 1) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float y = __shfl_down(x[e], d);
+            if (lane + d < 64) x[e] += y;
+          }
         }
       }
       if (lane < M::NCG) st_f8(sSuf + w * KP + cg * 8, x);
