@@ -7,17 +7,20 @@ already resident in HBM (the benchmark's input recipe: numpy default_rng(seed=4)
 q, k, v, g_raw, h0, do, dht; g = logsigmoid(g_raw) / 16; h0, dht ~ N(0, 0.1^2)).
 
 Prints ONE JSON line with the driver's fields plus
-  roofline     : the dominant kernel of a step (largest share of its time), timed with
-                 HIP events the library records on the launch stream (torch's current
-                 stream) right around that kernel, against the HBM roofline with its
+  roofline     : the dominant kernel of a step (largest share of its time), timed in the
+                 timed steps themselves with HIP events the library records on the launch
+                 stream (torch's current stream) right around every launch of that kernel
+                 (average over the timed steps), against the HBM roofline with its
                  algorithmic bytes per launch, and the copy-calibrated rocprofv3
                  FETCH_SIZE + WRITE_SIZE bytes per launch (profiles/hbm_traffic.json);
   cpu_baseline : the numpy oracle (float32, one thread) on a bounded sample of the same
                  workload (1 batch row, all 16 heads, full T), scaled to tokens/s of
                  the whole workload;
-  kernels      : the fused forward / backward kernels: average duration, achieved GB/s;
-  stages       : the chunk_fwd / chunk_bwd entry points (segment local states + combine
-                 + fused kernel) and the part before the fused kernel.
+  kernels      : the fused forward / backward kernels in the timed steps: average
+                 duration, achieved GB/s;
+  stages       : the chunk_fwd / chunk_bwd entry points called on their own, back to back
+                 (segment local states + combine + fused kernel), and the part before the
+                 fused kernel (timed the same way).
 """
 
 from __future__ import annotations
@@ -82,13 +85,24 @@ def _copy_calibration(device, mib=512, reps=3):
     torch.cuda.synchronize(device)
 
 
-def _kernel_profile(x, reps=10, op="chunk_gla"):
-    """Per-launch duration of the step's dominant kernels, each launched through the C ABI.
+def _kernel_bytes(op="chunk_gla"):
+    """Algorithmic HBM bytes per launch of the fused forward / backward kernels: every input
+    read once and every output written once (tok = B*T*H token-heads; h / dh per chunk bf16;
+    h0 / ht or dht / dh0 fp32)."""
+    tok = B * T * H
+    hbytes = (T // C) * B * H * K * V * BF
+    if op == "simple_gla":   # scalar gates: no [.., K] gate tensor in or out
+        return {"head_fwd_kernel": tok * (2 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes,
+                "head_bwd_kernel": tok * (4 * K + 3 * V) * BF + STATE_BYTES * 2 + hbytes}
+    return {"head_fwd_kernel": tok * (3 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes,
+            "head_bwd_kernel": tok * (6 * K + 3 * V) * BF + STATE_BYTES * 2 + hbytes}
 
-    kernels: the fused full-head forward / backward kernels, timed with the library's HIP
-    events recorded on the launch stream right around each kernel (tops_gla_kernel_ms);
-    stages: the whole entry points (segment local states + combine + fused kernel), timed
-    with torch events on the same stream."""
+
+def _kernel_profile(x, reps=10, op="chunk_gla"):
+    """The step's two entry points called on their own through the C ABI, back to back:
+    whole entry point (segment local states + combine + fused kernel) timed with torch
+    events on the launch stream, the fused kernel with the library's HIP events around it
+    (tops_gla_kernel_ms), their difference = the segment preparation."""
     import torch
 
     from tops import _lib
@@ -107,34 +121,32 @@ def _kernel_profile(x, reps=10, op="chunk_gla"):
     q, k, v, g, h0, do, dht = (x[n] for n in ("q", "k", "v", "g", "h0", "do", "dht"))
     lay = (B, T, H, K, V, C, *seq.args(), bf, st)
     ws, nws = _lib.seg_workspace(B, T, H, K, V, C, False, torch.bfloat16, dev)
-    tok = B * T * H
-    hbytes = seq.NC * H * K * V * BF
     gs = x["gamma"]
-    # (entry point, kernel name, timing slot, algorithmic bytes of the kernel per launch)
+    # (entry point, kernel name, timing slot)
     runs = [
         ("simple_chunk_fwd",
          lambda: call("tops_gla_simple_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(gs), 0, ptr(h0),
                       ptr(o), ptr(ht), ptr(h), ptr(ws), nws, sc, *lay),
-         "head_fwd_kernel", 0, tok * (2 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes),
+         "head_fwd_kernel", 0),
         ("simple_chunk_bwd",
          lambda: call("tops_gla_simple_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(gs), 0, ptr(h0),
                       ptr(h), ptr(do), ptr(dht), ptr(dq), ptr(dk), ptr(dv), None, ptr(dh0),
                       None, ptr(ws), nws, sc, *lay),
-         "head_bwd_kernel", 1, tok * (4 * K + 3 * V) * BF + STATE_BYTES * 2 + hbytes),
+         "head_bwd_kernel", 1),
     ] if op == "simple_gla" else [
         ("chunk_fwd",
          lambda: call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(o),
                       ptr(ht), ptr(h), ptr(ws), nws, sc, *lay),
-         "head_fwd_kernel", 0, tok * (3 * K + 2 * V) * BF + STATE_BYTES * 2 + hbytes),
+         "head_fwd_kernel", 0),
         ("chunk_bwd",
          lambda: call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(h),
                       ptr(do), ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None,
                       ptr(dh), ptr(ws), nws, sc, *lay),
-         "head_bwd_kernel", 1, tok * (6 * K + 3 * V) * BF + STATE_BYTES * 2 + hbytes),
+         "head_bwd_kernel", 1),
     ]
-    kernels, stages = {}, {}
+    stages = {}
     cur = torch.cuda.current_stream(dev)
-    for entry, fn, kname, slot, nbytes in runs:
+    for entry, fn, kname, slot in runs:
         fn()  # warm (the forward also produces the states the backward reads)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(cur)
@@ -144,16 +156,12 @@ def _kernel_profile(x, reps=10, op="chunk_gla"):
         torch.cuda.synchronize(dev)
         ems = e0.elapsed_time(e1) / reps
         call("tops_gla_kernel_timing", 1)
-        kms = 0.0
         for _ in range(reps):
             fn()
-            kms += float(lib.tops_gla_kernel_ms(slot))
+        kms = float(lib.tops_gla_kernel_ms(slot))
         call("tops_gla_kernel_timing", 0)
-        kms /= reps
-        kernels[kname] = dict(ms=round(kms, 4), bytes=int(nbytes),
-                              gbs=round(nbytes / (kms * 1e-3) / 1e9, 1))
         stages[entry] = dict(ms=round(ems, 4), segment_prep_ms=round(ems - kms, 4))
-    return kernels, stages
+    return stages
 
 
 def _measured_traffic(kernel):
@@ -232,6 +240,7 @@ def main():
     import torch
 
     import tops.ops.gla as G
+    from tops import _lib
 
     dev = torch.device("cuda:0")
     x = _inputs(dev)
@@ -255,12 +264,23 @@ def main():
     torch.cuda.synchronize(dev)
     cur = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    timing = not a.no_kernel_profile
+    if timing:   # HIP events around every fused-kernel launch of the timed steps
+        _lib.call("tops_gla_kernel_timing", 1)
     e0.record(cur)
     for _ in range(a.steps):
         step()
     e1.record(cur)
     torch.cuda.synchronize(dev)
     ms = e0.elapsed_time(e1) / a.steps
+    kernels = {}
+    if timing:
+        lib = _lib.load()
+        for slot, (kname, nbytes) in enumerate(_kernel_bytes(a.op).items()):
+            kms = float(lib.tops_gla_kernel_ms(slot))
+            kernels[kname] = dict(ms=round(kms, 4), bytes=int(nbytes),
+                                  gbs=round(nbytes / (kms * 1e-3) / 1e9, 1))
+        _lib.call("tops_gla_kernel_timing", 0)
     tokens_s = B * T / (ms * 1e-3)
 
     simple = a.op == "simple_gla"
@@ -288,8 +308,9 @@ def main():
     }
     if simple:   # the flop count of the per-element form does not describe this op
         del out["tflops"], out["mfma_frac"]
-    if not a.no_kernel_profile:
-        prof, stages = _kernel_profile(x, max(1, a.profile_reps), a.op)
+    if timing:
+        prof = kernels
+        stages = _kernel_profile(x, max(1, a.profile_reps), a.op)
         dom = max(prof, key=lambda n: prof[n]["ms"])
         d = prof[dom]
         out["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": d["gbs"],

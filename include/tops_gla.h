@@ -326,10 +326,11 @@ int64_t tops_gla_short_conv_ws_bytes(int64_t B, int64_t T, int64_t D, int W, int
 
 /*
  * Measurement hook (no counterpart in the reference): with timing enabled, HIP events are
- * recorded on the launch stream around the fused full-head forward (which = 0) and
- * backward (which = 1) kernels of tops_gla_chunk_fwd / tops_gla_chunk_bwd.
- * tops_gla_kernel_ms waits for the last such launch and returns its duration in ms (-1 if
- * there is none). Process-wide state, for profiling runs only.
+ * recorded on the launch stream around every launch of the fused full-head forward
+ * (which = 0) and backward (which = 1) kernels (tops_gla_chunk_fwd / _bwd and the
+ * scalar-gate entry points). tops_gla_kernel_ms waits for the last such launch and returns
+ * the average duration in ms of the launches recorded since timing was enabled (the last
+ * 256 of them; -1 if there is none). Process-wide state, for profiling runs only.
  */
 int tops_gla_kernel_timing(int enable);
 float tops_gla_kernel_ms(int which);

@@ -144,16 +144,19 @@ void seg_setup(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void* w
 
 namespace tops {
 
-// Measurement hook state (process-wide; for profiling runs, not for concurrent callers).
+// Measurement hook state (process-wide; for profiling runs, not for concurrent callers):
+// a ring of KT_RING event pairs per kernel, one pair per launch while timing is on.
+constexpr int KT_RING = 256;
 static bool g_kt_on = false;
 static bool g_kt_made = false;
-static bool g_kt_done[KT_COUNT] = {};
-static hipEvent_t g_kt_ev[KT_COUNT][2];
+static long g_kt_n[KT_COUNT] = {};            // launches recorded since timing was enabled
+static hipEvent_t g_kt_ev[KT_COUNT][KT_RING][2];
 
 void ktimer_mark(int which, bool stop, hipStream_t st) {
   if (!g_kt_on) return;
-  if (hipEventRecord(g_kt_ev[which][stop ? 1 : 0], st) == hipSuccess && stop)
-    g_kt_done[which] = true;
+  const long n = g_kt_n[which];
+  if (hipEventRecord(g_kt_ev[which][n % KT_RING][stop ? 1 : 0], st) == hipSuccess && stop)
+    g_kt_n[which] = n + 1;
 }
 
 }  // namespace tops
@@ -163,23 +166,33 @@ extern "C" {
 int tops_gla_kernel_timing(int enable) {
   if (enable && !tops::g_kt_made) {
     for (int i = 0; i < tops::KT_COUNT; ++i)
-      for (int j = 0; j < 2; ++j)
-        if (hipEventCreate(&tops::g_kt_ev[i][j]) != hipSuccess)
-          return fail(TOPS_GLA_EHIP, "hipEventCreate failed");
+      for (int r = 0; r < tops::KT_RING; ++r)
+        for (int j = 0; j < 2; ++j)
+          if (hipEventCreate(&tops::g_kt_ev[i][r][j]) != hipSuccess)
+            return fail(TOPS_GLA_EHIP, "hipEventCreate failed");
     tops::g_kt_made = true;
   }
   tops::g_kt_on = enable != 0;
-  for (int i = 0; i < tops::KT_COUNT; ++i) tops::g_kt_done[i] = false;
+  if (enable)
+    for (int i = 0; i < tops::KT_COUNT; ++i) tops::g_kt_n[i] = 0;
   return ok();
 }
 
 float tops_gla_kernel_ms(int which) {
-  if (which < 0 || which >= tops::KT_COUNT || !tops::g_kt_done[which]) return -1.f;
-  float ms = -1.f;
-  if (hipEventSynchronize(tops::g_kt_ev[which][1]) != hipSuccess) return -1.f;
-  if (hipEventElapsedTime(&ms, tops::g_kt_ev[which][0], tops::g_kt_ev[which][1]) != hipSuccess)
+  if (which < 0 || which >= tops::KT_COUNT || tops::g_kt_n[which] == 0) return -1.f;
+  const long n = tops::g_kt_n[which];
+  const long m = n < tops::KT_RING ? n : tops::KT_RING;
+  if (hipEventSynchronize(tops::g_kt_ev[which][(n - 1) % tops::KT_RING][1]) != hipSuccess)
     return -1.f;
-  return ms;
+  double sum = 0.0;
+  for (long i = n - m; i < n; ++i) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, tops::g_kt_ev[which][i % tops::KT_RING][0],
+                            tops::g_kt_ev[which][i % tops::KT_RING][1]) != hipSuccess)
+      return -1.f;
+    sum += ms;
+  }
+  return (float)(sum / m);
 }
 
 
