@@ -19,7 +19,7 @@ Prints ONE JSON line with the driver's fields plus
   kernels      : the fused forward / backward kernels in the timed steps: average
                  duration, achieved GB/s;
   stages       : the chunk_fwd / chunk_bwd entry points called on their own, back to back
-                 (segment local states + combine + fused kernel), and the part before the
+                 (segment local states + fused kernel), and the part before the
                  fused kernel (timed the same way).
 """
 
@@ -100,7 +100,7 @@ def _kernel_bytes(op="chunk_gla"):
 
 def _kernel_profile(x, reps=10, op="chunk_gla"):
     """The step's two entry points called on their own through the C ABI, back to back:
-    whole entry point (segment local states + combine + fused kernel) timed with torch
+    whole entry point (segment local states + fused kernel) timed with torch
     events on the launch stream, the fused kernel with the library's HIP events around it
     (tops_gla_kernel_ms), their difference = the segment preparation."""
     import torch

@@ -23,10 +23,11 @@
 // Sequence segments: with NS > 1 the chunks of a sequence are split into NS segments of SL
 // chunks. Pass 1 (head_scan_kernel, pass 1) computes every segment's local final state
 // (from a zero state; the first segment in flow order starts from the given initial state)
-// and the segment's total log2 decay; head_combine_kernel turns them into the state
-// entering every segment; pass 3 (head_scan_kernel pass 3, or head_fwd_kernel) then walks
-// all segments in parallel from those states. State composition over a segment is exact:
-// h_out = 2^{Gamma} h_in + L with Gamma the summed (base-2) gates of the segment.
+// and the segment's total log2 decay; then every segment's block (head_scan_kernel pass 3,
+// head_fwd_kernel, head_bwd_kernel) folds the local states of the segments before it in
+// flow order into its entry state (load_entry_state) and walks its chunks, all segments in
+// parallel. State composition over a segment is exact: h_out = 2^{Gamma} h_in + L with
+// Gamma the summed (base-2) gates of the segment.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -291,6 +292,35 @@ __device__ __forceinline__ void load_state(f32x4 (&acc)[NTV][NTK], const float* 
     }
 }
 
+// Entry state of segment s of a segmented scan, folded from the pass-1 local states L_u and
+// segment decays Gamma_u (base 2) in the workspace, in the order the scan runs: forward
+// L_0, then H <- 2^{Gamma_u} H + L_u for u = 1 .. s-1; reverse L_{NS-1}, then u = NS-2 ..
+// s+1. Slot u of (sequence, head) is st + ((seq NS + u) H + h) K ld (+ cv: a V tile's
+// first column), its decays gm + ((seq NS + u) H + h) K.
+template <int NTV, int NTK, bool REV>
+__device__ __forceinline__ void load_entry_state(f32x4 (&acc)[NTV][NTK], const float* st,
+                                                 const float* gm, int seq, int s, int NS,
+                                                 int H, int hh, int K, int Vw, int cv, int ld,
+                                                 int vt0, int kt0, int lane) {
+  const long KV = (long)K * ld;
+  auto slot = [&](int u) { return st + ((long)(seq * NS + u) * H + hh) * KV + cv; };
+  const int u0 = REV ? NS - 1 : 0;
+  load_state<NTV, NTK>(acc, slot(u0), K, Vw, vt0, kt0, lane, ld);
+  for (int u = REV ? u0 - 1 : 1; REV ? u > s : u < s; u += REV ? -1 : 1) {
+    f32x4 x[NTV][NTK];
+    load_state<NTV, NTK>(x, slot(u), K, Vw, vt0, kt0, lane, ld);
+#pragma unroll
+    for (int j = 0; j < NTK; ++j) {
+      const int kk = (kt0 + j) * 16 + (lane & 15);
+      const float g = kk < K ? exp2_hw(gm[((long)(seq * NS + u) * H + hh) * K + kk]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < NTV; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][j][e] = g * acc[i][j][e] + x[i][j][e];
+    }
+  }
+}
+
 template <int NTV, int NTK>
 __device__ __forceinline__ void store_state_f32(const f32x4 (&acc)[NTV][NTK], float* dst,
                                                 int K, int V, int vt0, int kt0, int lane,
@@ -433,12 +463,15 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
   f32x4 acc[NTV][NTK];
   {
-    const float* init = nullptr;
-    if (first_seg)
-      init = p.s_init ? p.s_init + ((long)sg.seq * H + hh) * KV + cv : nullptr;
-    else if (p.pass == 3)
-      init = p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV + cv;
-    load_state<NTV, NTK>(acc, init, K, Vw, vt0, kt0, lane, V);
+    if (!first_seg && p.pass == 3)
+      load_entry_state<NTV, NTK, REV>(acc, p.seg_state, p.seg_gam, sg.seq, s, p.NS, H, hh, K,
+                                      Vw, cv, V, vt0, kt0, lane);
+    else
+      load_state<NTV, NTK>(acc,
+                           first_seg && p.s_init
+                               ? p.s_init + ((long)sg.seq * H + hh) * KV + cv
+                               : nullptr,
+                           K, Vw, vt0, kt0, lane, V);
   }
 
   struct Regs {
@@ -555,43 +588,6 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   } else if (last_seg && p.s_final) {
     store_state_f32<NTV, NTK>(acc, p.s_final + ((long)sg.seq * H + hh) * KV + cv, K, Vw, vt0,
                               kt0, lane, V);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Segment combine: seg_state[s] <- state entering segment s (flow order), from the local
-// states L_s (pass 1) and the base-2 segment decays Gamma_s.
-//   forward: H_1 = L_0, H_{s+1} = 2^{Gamma_s} H_s + L_s
-//   reverse: D_{NS-2} = L_{NS-1}, D_{s-1} = 2^{Gamma_s} D_s + L_s
-// One thread per (sequence, head, k, v) element.
-// ---------------------------------------------------------------------------
-template <bool REV>
-__global__ __launch_bounds__(256) void head_combine_kernel(float* __restrict__ st,
-                                                           const float* __restrict__ gm, int N,
-                                                           int NS, int H, int K, int V) {
-  const long KV = (long)K * V;
-  const long total = (long)N * H * KV;
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
-  const long kv = i % KV;
-  const int hh = (int)((i / KV) % H), seq = (int)(i / (KV * H));
-  const int kk = (int)(kv / V);
-  auto at = [&](int s) -> long { return ((long)(seq * NS + s) * H + hh) * KV + kv; };
-  auto gam = [&](int s) -> float { return gm[((long)(seq * NS + s) * H + hh) * K + kk]; };
-  if (!REV) {
-    float h = st[at(0)];
-    for (int s = 1; s < NS; ++s) {
-      const float l = s < NS - 1 ? st[at(s)] : 0.f;
-      st[at(s)] = h;
-      if (s < NS - 1) h = exp2_hw(gam(s)) * h + l;
-    }
-  } else {
-    float d = st[at(NS - 1)];
-    for (int s = NS - 2; s >= 0; --s) {
-      const float l = s > 0 ? st[at(s)] : 0.f;
-      st[at(s)] = d;
-      if (s > 0) d = exp2_hw(gam(s)) * d + l;
-    }
   }
 }
 
@@ -800,9 +796,12 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
   f32x4 acc[NTV][NTK];
   {
-    const float* init = s == 0 ? (p.h0 ? p.h0 + ((long)sg.seq * H + hh) * KV + cv : nullptr)
-                               : p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV + cv;
-    load_state<NTV, NTK>(acc, init, K, Vw, vt0, kt0, lane, V);
+    if (s > 0)
+      load_entry_state<NTV, NTK, false>(acc, p.seg_state, p.seg_gam, sg.seq, s, p.NS, H, hh, K,
+                                        Vw, cv, V, vt0, kt0, lane);
+    else
+      load_state<NTV, NTK>(acc, p.h0 ? p.h0 + ((long)sg.seq * H + hh) * KV + cv : nullptr, K,
+                           Vw, vt0, kt0, lane, V);
   }
 
   struct Regs {
@@ -1173,10 +1172,12 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
   f32x4 acc[NTV][NTK];   // dh[v][k]
   {
-    const float* init = s == p.NS - 1
-                            ? (p.dht ? p.dht + ((long)sg.seq * H + hh) * KV : nullptr)
-                            : p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV;
-    load_state<NTV, NTK>(acc, init, K, V, vt0, kt0, lane);
+    if (s < p.NS - 1)
+      load_entry_state<NTV, NTK, true>(acc, p.seg_state, p.seg_gam, sg.seq, s, p.NS, H, hh, K, V,
+                                       0, V, vt0, kt0, lane);
+    else
+      load_state<NTV, NTK>(acc, p.dht ? p.dht + ((long)sg.seq * H + hh) * KV : nullptr, K, V,
+                           vt0, kt0, lane);
   }
 
   uint4 Rq[RPT], Rk[RPT], Rg[RPT], Rv[VRPT], Rd[VRPT], Rh[KTW][NHF];
@@ -1722,25 +1723,12 @@ static hipError_t head_scan_launch(HeadScanArgs p, bool reverse, hipStream_t st,
   return reverse ? head_scan_kp<true>(p, st, blocks) : head_scan_kp<false>(p, st, blocks);
 }
 
-static hipError_t head_combine(const HeadScanArgs& p, bool reverse, hipStream_t st) {
-  const long total = (long)p.si.N * p.H * p.K * p.V;
-  const unsigned blocks = (unsigned)((total + 255) / 256);
-  if (reverse)
-    hipLaunchKernelGGL((head_combine_kernel<true>), dim3(blocks), dim3(256), 0, st,
-                       p.seg_state, p.seg_gam, p.si.N, p.NS, p.H, p.K, p.V);
-  else
-    hipLaunchKernelGGL((head_combine_kernel<false>), dim3(blocks), dim3(256), 0, st,
-                       p.seg_state, p.seg_gam, p.si.N, p.NS, p.H, p.K, p.V);
-  return hipGetLastError();
-}
-
-// Segment passes 1 and 2 (no-op when NS == 1).
+// Segment pass 1 (no-op when NS == 1): the local states; every segment's block folds its
+// own entry state from them (load_entry_state).
 static hipError_t head_prepare_segments(const HeadScanArgs& p, bool reverse, hipStream_t st) {
   if (p.NS <= 1) return hipSuccess;
   // pass 1 skips the last segment in flow order (its local state is never needed)
-  hipError_t e = head_scan_launch(p, reverse, st, 1, reverse ? 1 : 0, p.NS - 1);
-  if (e != hipSuccess) return e;
-  return head_combine(p, reverse, st);
+  return head_scan_launch(p, reverse, st, 1, reverse ? 1 : 0, p.NS - 1);
 }
 
 hipError_t run_head_scan(const HeadScanArgs& p0, bool reverse, hipStream_t st) {
