@@ -64,6 +64,15 @@ struct HTilesN {
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A loop-invariant per-lane offset kept out of loop-invariant code motion: hoisted out of a
+// chunk loop, such offsets become long-lived registers (64-bit per-lane pointers for global
+// accesses) that the fused backward cannot hold, and spill; recomputed in the loop they cost
+// an integer op or two.
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // acc + sum of the products of 8 bf16 pairs (v_dot2c_f32_bf16: fp32 accumulation)
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float dot8_bf16(uint4 a, uint4 b, float acc) {
@@ -154,7 +163,7 @@ __device__ __forceinline__ float rows4_prefix(float x, int lane) {
   if (lane & 32) y += __uint_as_float(q[0]);   // rows 2, 3: + the pair sum of rows 0, 1
   return y;
 }
-__device__ __forceinline__ float rows4_suffix(float x, int lane) {
+__device__ __forceinline__ float rows4_suffix(float x, int lane, float* total = nullptr) {
   const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
   const float pair = __uint_as_float(p[0]) + __uint_as_float(p[1]);
@@ -162,6 +171,7 @@ __device__ __forceinline__ float rows4_suffix(float x, int lane) {
   const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(pair), __float_as_uint(pair),
                                                   false, false);
   if (!(lane & 32)) y += __uint_as_float(q[1]);   // rows 0, 1: + the pair sum of rows 2, 3
+  if (total) *total = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // x_0 + .. + x_3
   return y;
 }
 
@@ -1079,12 +1089,11 @@ struct HBLayout {
   // row groups of the dq / dk tiles (waves sharing a k tile)
   static constexpr int NKT = KP / 16, KTW = NKT > NW ? NKT / NW : 1, NRG = NW / (NKT / KTW);
   static constexpr int tot = 0;                    // [NW][KP] cumsum wave totals
-  static constexpr int suf = tot + NW * KP * 4;    // [NW][KP] dg suffix wave totals
-  static constexpr int first = suf + NW * KP * 4;
+  static constexpr int suf = tot + NW * KP * 4;    // [NRG][KP] dg row-group totals
+  static constexpr int first = suf + NRG * KP * 4;
   static constexpr int fr = first + KP * 4;        // scale 2^r
   static constexpr int fe = fr + KP * 4;           // 2^{gamma-r}
-  static constexpr int hd = fe + KP * 4;           // 2^gamma sum_v h dh
-  static constexpr int dkc = hd + KP * 4;          // [NRG][KP] sum_rows kg (v dh'^T)
+  static constexpr int dkc = fe + KP * 4;          // [NRG][KP] sum_rows kg (v dh'^T)
   static constexpr int qg = dkc + NRG * KP * 4;
   static constexpr int kg = qg + HC * PKP * 2;
   static constexpr int v = kg + HC * PKP * 2;
@@ -1095,11 +1104,13 @@ struct HBLayout {
   static constexpr int q2 = da + HC * PA * 2;      // SG only
   static constexpr int grow = q2 + (SG ? HC * PKP * 2 : 0);
   static constexpr int end_tiles = grow + (SG ? HC * 4 : 0);
-  // exchange [HC][PX] x 2 from v on (qg, kg stay intact for the epilogue); it may reach
-  // A / dA, which are therefore rewritten in full (zero upper tiles) every chunk
+  // exchange [HC][PX] x 3 (dq, dk pre-factors, dg) from v on (qg, kg stay intact for the
+  // epilogue); it may reach A / dA, which are therefore rewritten in full (zero upper tiles)
+  // every chunk
   static constexpr int xq = v;
   static constexpr int xk = xq + HC * PX * 4;
-  static constexpr int end_x = xk + HC * PX * 4;
+  static constexpr int xg = xk + HC * PX * 4;
+  static constexpr int end_x = xg + HC * PX * 4;
   static constexpr int bytes = end_tiles > end_x ? end_tiles : end_x;
 };
 
@@ -1127,7 +1138,6 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   float* sFirst = reinterpret_cast<float*>(smem + Lay::first);
   float* sFr = reinterpret_cast<float*>(smem + Lay::fr);
   float* sFe = reinterpret_cast<float*>(smem + Lay::fe);
-  float* sHd = reinterpret_cast<float*>(smem + Lay::hd);
   float* sDkc = reinterpret_cast<float*>(smem + Lay::dkc);
   bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
   bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
@@ -1138,6 +1148,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   bf16* sdA = reinterpret_cast<bf16*>(smem + Lay::da);
   float* XQ = reinterpret_cast<float*>(smem + Lay::xq);
   float* XK = reinterpret_cast<float*>(smem + Lay::xk);
+  float* XG = reinterpret_cast<float*>(smem + Lay::xg);
   bf16* sQ2 = reinterpret_cast<bf16*>(smem + Lay::q2);
   float* sG = reinterpret_cast<float*>(smem + Lay::grow);
 
@@ -1231,6 +1242,10 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
     issue_qk(step);
     issue_vd(step);
     issue_h(step);
+    // lane / thread indices for the per-lane offsets of the dv, dq, dk, dg stores and of the
+    // transposed kg / qg reads: taken through opaque() every chunk so that those offsets are
+    // recomputed in the loop (hoisted, they are long-lived registers the kernel cannot hold)
+    const int ln = (int)opaque((uint32_t)lane), tl = (int)opaque((uint32_t)tid);
 
     // ---- (1) cumsum, gating; dh' = fe (.) dh to LDS ----
     float dd[RPT][8];   // g~ - r (base 2)
@@ -1413,8 +1428,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       dkc[t] = 0.f;
 #pragma unroll
       for (int i = 0; i < RT; ++i) {
-        const bf16* pk = sKg + ((rt0 + i) * 16 + 4 * (lane >> 4) + ((lane & 15) >> 2)) * PKP +
-                         (kq0 + t) * 16 + 4 * (lane & 3);
+        const bf16* pk = sKg + ((rt0 + i) * 16 + 4 * (ln >> 4) + ((ln & 15) >> 2)) * PKP +
+                         (kq0 + t) * 16 + 4 * (ln & 3);
         const s4_t kv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) s4_t*)(pk));
 #pragma unroll
@@ -1472,9 +1487,11 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
           mma(avt, fd[kk], ld_frag_t(sA + kk * 32 * PA + jt * 16, PA, lane));
         const int jj = jt * 16 + (lane & 15);
         const int vv = vd * 16 + 4 * (lane >> 4);
-        if (jj < len && vv < V)
-          st8(dv + (long)t0 * rsV + (long)hh * V, ((uint32_t)jj * (uint32_t)rsV + vv) * 2u,
+        if (jj < len && vv < V) {
+          const int jl = jt * 16 + (ln & 15), vl = vd * 16 + 4 * (ln >> 4);
+          st8(dv + (long)t0 * rsV + (long)hh * V, ((uint32_t)jl * (uint32_t)rsV + vl) * 2u,
               make_uint2(pack2_bf16(avt[0], avt[1]), pack2_bf16(avt[2], avt[3])));
+        }
       }
     }
     // dh <- 2^gamma dh + (scale q 2^{g~})^T do = fr * (dh fe / scale + qg^T do)
@@ -1509,7 +1526,13 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
     }
     __syncthreads();   // every tile read is done: the exchange aliases them
 
-    // ---- (4) exchange dq / dk pre-factors ----
+    // ---- (4) exchange dq / dk pre-factors; dg in the accumulator layout ----
+    // dg = revcumsum_rows(qg (.) xq - kg (.) xk) + 2^r sum_v h dh' + sum_rows kg (.) dk_inter,
+    // xq / xk the pre-factors (q dq - k dk with the gate factors cancelled). A wave holds RT
+    // row tiles of its k tile: the rows of its row group (all 64 when NRG = 1), so the reverse
+    // cumsum runs in registers: in-lane over a tile's 4 rows, rows4_suffix over the lane
+    // groups, a running total over the tiles; later row groups (NRG > 1) and their dk sums
+    // are added in the epilogue.
 #pragma unroll
     for (int t = 0; t < KTW; ++t) {
       const int hk = (kq0 + t) * 16 + (lane & 15);
@@ -1522,8 +1545,37 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
           XK[ro * PX + hk] = ak[t][i][rr];
         }
       }
-      if (w < NKG && lane < 16) sHd[hk] = hdp[t] * (sFr[hk] * inv_scale);   // 2^r sum h dh'
-      if (lane < 16) sDkc[(w / NKG) * KP + hk] = dkc[t];
+      if (p.dg) {   // uniform: absent for scalar gates without a gate gradient
+        const float hd = hdp[t] * (sFr[hk] * inv_scale);   // 2^r sum_v h dh'
+        float carry = Lay::NRG == 1 ? hd + dkc[t] : hd;
+#pragma unroll
+        for (int i = RT - 1; i >= 0; --i) {
+          const int r0 = (rt0 + i) * 16 + 4 * (lane >> 4);
+          const int off = ((rt0 + i) * 16 + 4 * (ln >> 4) + ((ln & 15) >> 2)) * PKP +
+                          (kq0 + t) * 16 + 4 * (ln & 3);
+          const s4_t qv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s4_t*)(sQg + off));
+          const s4_t kv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s4_t*)(sKg + off));
+          float x[4];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            x[rr] = __uint_as_float((uint32_t)(uint16_t)qv[rr] << 16) * aq[t][i][rr] -
+                    __uint_as_float((uint32_t)(uint16_t)kv[rr] << 16) * ak[t][i][rr];
+          x[2] += x[3];
+          x[1] += x[2];
+          x[0] += x[1];
+          float tot;
+          const float later = rows4_suffix(x[0], lane, &tot) - x[0] + carry;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) XG[(r0 + rr) * PX + hk] = x[rr] + later;
+          carry += tot;
+        }
+        if (Lay::NRG > 1 && lane < 16) {
+          sSuf[(w / NKG) * KP + hk] = carry - hd;   // the row group's total
+          sDkc[(w / NKG) * KP + hk] = dkc[t];
+        }
+      }
     }
     __syncthreads();
 
@@ -1532,85 +1584,48 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
     if (step + 1 < nsteps) issue_qkg(step + 1);
 
     // ---- (5) epilogue: dq, dk, dg rows ----
-    float pr[RPT][8];
+    // (the next chunk's first barrier, in its gating, comes before anything overwrites the
+    // exchange)
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
       const int row = rs * RPT + j;
-      // q dq - k dk = qg xq - kg xk (xq, xk before their gate factors)
-      float xq[8], xk[8], q8[8], k8[8];
+      float xq[8], xk[8];
       ld_f8(XQ + row * PX + cg * 8, xq);
       ld_f8(XK + row * PX + cg * 8, xk);
-      unpack8(*reinterpret_cast<const uint4*>(sQg + row * PKP + cg * 8), q8);
-      unpack8(*reinterpret_cast<const uint4*>(sKg + row * PKP + cg * 8), k8);
+      if constexpr (!SG) {   // scalar gates: the factors are in already
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pr[j][e] = q8[e] * xq[e] - k8[e] * xk[e];
-        if constexpr (!SG) {   // scalar gates: the factors are in already
+        for (int e = 0; e < 8; ++e) {
           xq[e] *= exp2_hw(dd[j][e]);
           xk[e] *= exp2_hw(-dd[j][e]);
         }
       }
-      if (row < len && colA) {
-        const long b0 = (long)t0 * rsK + (long)hh * K;
-        const uint32_t a = ((uint32_t)row * (uint32_t)rsK + cg * 8) * 2u;
+      const bool st_ok = row < len && colA;
+      const long b0 = (long)t0 * rsK + (long)hh * K;
+      const uint32_t a =
+          ((uint32_t)((tl / M::NCG) * RPT + j) * (uint32_t)rsK + (tl % M::NCG) * 8) * 2u;
+      if (st_ok) {
         st16(dq + b0, a, pack8(xq));
         st16(dk + b0, a, pack8(xk));
       }
-    }
-    // dg (uniform branch: absent for scalar gates without a gate gradient)
-    if (p.dg) {
-      // reverse cumsum over rows: in-thread, then across the wave's row segments
+      if (p.dg) {
+        float xg[8];
+        ld_f8(XG + row * PX + cg * 8, xg);
+        if constexpr (Lay::NRG > 1) {   // later row groups' totals; every group's dk sum
+          const int rg = row / (RT * 16);
+          float t8[8];
 #pragma unroll
-      for (int j = RPT - 2; j >= 0; --j)
+          for (int gi = 0; gi < Lay::NRG; ++gi) {
+            ld_f8(sDkc + gi * KP + cg * 8, t8);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pr[j][e] += pr[j + 1][e];
-      float x[8];
+            for (int e = 0; e < 8; ++e) xg[e] += t8[e];
+            if (gi > rg) {
+              ld_f8(sSuf + gi * KP + cg * 8, t8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = pr[0][e];
-      if constexpr (M::NCG == 16) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = rows4_suffix(x[e], lane);
-      } else {
-#pragma unroll
-        for (int d = M::NCG; d < 64; d <<= 1) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float y = __shfl_down(x[e], d);
-            if (lane + d < 64) x[e] += y;
+              for (int e = 0; e < 8; ++e) xg[e] += t8[e];
+            }
           }
         }
-      }
-      if (lane < M::NCG) st_f8(sSuf + w * KP + cg * 8, x);
-      __syncthreads();
-      {
-        float off[8], t8[8], u8[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) off[e] = x[e] - pr[0][e];   // later segments of the wave
-        for (int ww = w + 1; ww < NW; ++ww) {   // later waves (w is wave-uniform)
-          ld_f8(sSuf + ww * KP + cg * 8, t8);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) off[e] += t8[e];
-        }
-        ld_f8(sHd + cg * 8, u8);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) off[e] += u8[e];
-#pragma unroll
-        for (int gi = 0; gi < Lay::NRG; ++gi) {
-          ld_f8(sDkc + gi * KP + cg * 8, t8);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) off[e] += t8[e];
-        }
-#pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-          const int row = rs * RPT + j;
-          if (row < len && colA) {
-            float o8[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o8[e] = pr[j][e] + off[e];
-            st16(dg + (long)t0 * rsK + (long)hh * K,
-                 ((uint32_t)row * (uint32_t)rsK + cg * 8) * 2u, pack8(o8));
-          }
-        }
+        if (st_ok) st16(dg + b0, a, pack8(xg));
       }
     }
   }
