@@ -178,6 +178,14 @@ def test_segment_workspace_query():
     assert q(4, 8192, 16, 320, 128, 64, 0, 1) == 0      # K > 256: other kernels
 
 
+def test_kernel_timer_without_launches():
+    # host-only: with no timed launch recorded the timer reports -1 (no HIP call is made)
+    lib = _lib.load()
+    assert lib.tops_gla_kernel_ms(0) == -1.0
+    assert lib.tops_gla_kernel_ms(1) == -1.0
+    assert lib.tops_gla_kernel_ms(7) == -1.0
+
+
 def test_simple_chunk_validation():
     buf = ctypes.c_void_p(256)  # never dereferenced: validation fails first
     fwd = lambda gs, ts, dtype, K=128: [buf, buf, buf, gs, ts, NULL, buf, NULL, NULL, NULL, 0,  # noqa: E731
