@@ -495,7 +495,8 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     return fail(TOPS_GLA_EINVAL, "dh_ws must not be NULL off the fused full-head backward");
   int NS = 1, SL = 0;
   float *seg_st = nullptr, *seg_gm = nullptr;
-  if (head) seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, NS, SL, seg_st, seg_gm);
+  void* gate = nullptr;   // per-chunk gating of wide heads (when the workspace holds it)
+  if (head) seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, NS, SL, seg_st, seg_gm, &gate);
   auto head_scan = [&](bool rev, const void* a, const void* b, const float* s_init, void* s_all,
                        float* s_final, float sc) {
     tops::HeadScanArgs s = {};
@@ -570,6 +571,20 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     // wide heads: the full-head reverse scan stores dh for the per-chunk gradient kernels
     rc = hip_status(head_scan(true, q, dout, dht, dh_ws, dh0, scale), "chunk_bwd (dh scan)");
     if (rc) return rc;
+    if (gate) {   // gated k, A and the column factors once per (chunk, head), for dv
+      tops::HeadFwdArgs a = {};
+      a.q = q;
+      a.k = k;
+      a.g = g;
+      a.gate_ws = gate;
+      a.scale = scale;
+      a.H = (int)H;
+      a.K = (int)K;
+      a.V = (int)V;
+      a.si = si;
+      rc = hip_status(tops::run_head_gate(a, st), "chunk_bwd (gating)");
+      if (rc) return rc;
+    }
   } else {
     tops::ScanArgs d;
     d.a = q;
@@ -588,7 +603,7 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     rc = hip_status(tops::run_state_scan(d, true, dtype, st), "chunk_bwd (dh scan)");
     if (rc) return rc;
   }
-  tops::BwdArgs p;
+  tops::BwdArgs p = {};
   p.q = q;
   p.k = k;
   p.v = v;
@@ -600,6 +615,7 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   p.dk = dk;
   p.dv = dv;
   p.dg = dg;
+  p.gate_ws = head && !head_bwd ? gate : nullptr;
   p.scale = scale;
   p.H = (int)H;
   p.K = (int)K;
@@ -753,7 +769,7 @@ int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const v
                     h == nullptr || dout == nullptr || dh == nullptr || dq == nullptr ||
                     dk == nullptr || dg == nullptr))
     return fail(TOPS_GLA_EINVAL, "no argument of chunk_bwd_dqkg may be NULL");
-  tops::BwdArgs p;
+  tops::BwdArgs p = {};
   p.q = q;
   p.k = k;
   p.v = v;
@@ -787,7 +803,7 @@ int tops_gla_chunk_bwd_dv(const void* q, const void* k, const void* g, const voi
   if (B * T > 0 && (q == nullptr || k == nullptr || g == nullptr || dout == nullptr ||
                     dh == nullptr || dv == nullptr))
     return fail(TOPS_GLA_EINVAL, "no argument of chunk_bwd_dv may be NULL");
-  tops::BwdArgs p;
+  tops::BwdArgs p = {};
   p.q = q;
   p.k = k;
   p.v = nullptr;

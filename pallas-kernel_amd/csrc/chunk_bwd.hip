@@ -14,7 +14,9 @@
 //   above except dv is local to a K tile (its contractions run over V and over the chunk).
 // chunk_bwd_dv_kernel:   one block per (chunk, head, 64-wide V tile), accumulating the
 //   K contractions of A and of k_d.dh over K tiles; it produces dv^T tiles so that each lane
-//   stores four consecutive values of a row.
+//   stores four consecutive values of a row. With the per-chunk gating workspace (PRE: wide
+//   bf16 heads, chunk 64) it reads kg, e^{gamma-r} and A from there instead: the gating and
+//   A would otherwise be recomputed by every V tile's block of a (chunk, head).
 // Tiles are staged in LDS row-major exactly as loaded (16-byte global loads); operands that
 // are needed transposed (kg^T, qg^T, dA^T, dh^T, do^T, A^T) are read with transposed MFMA
 // fragments. Element-wise work maps a thread to two adjacent columns x C/8 rows.
@@ -416,8 +418,9 @@ struct DvLayout {
   static constexpr int bytes = dh + SQ;
 };
 
-template <typename T, int C, bool VEC>
+template <typename T, int C, bool VEC, bool PRE = false>
 __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
+  static_assert(!PRE || C == 64, "the gating workspace holds chunks of 64");
   using Lay = DvLayout<T, C>;
   constexpr int CP = Lay::CP, P64 = Lay::P64, PCP = Lay::PCP;
   constexpr int EPP = 16 / (int)sizeof(T);
@@ -457,6 +460,12 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
   const int vb = vt * 64;
   const int cp = tid & 31, seg = tid >> 5;
   const int c_0 = 2 * cp, c_1 = c_0 + 1;
+  // PRE: this (chunk, head)'s gating entry: kg [64][K], A [64][64], factors [3][K]
+  const unsigned char* ent =
+      PRE ? (const unsigned char*)p.gate_ws + ((long)c * H + hh) * gate_ws_entry(K) : nullptr;
+  const T* gkg = reinterpret_cast<const T*>(ent) + 64 * K;
+  const T* gA = reinterpret_cast<const T*>(ent) + 2 * 64 * K;
+  const float* gpost = reinterpret_cast<const float*>(ent + 2L * 64 * K * 2 + 64 * 64 * 2) + 2 * K;
 
   // A[i][j] (lower tiles only) and dv^T[v][j], both accumulated over K tiles
   f32x4 Aacc[NA], Dacc[NO];
@@ -468,31 +477,40 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
   uint4 rq[PPT], rk[PPT], rg[PPT], rdh[HPT];
   for (int kt = 0; kt < KT; ++kt) {
     const int kb = kt * 64;
-    tile_load<T, C, VEC>(rq, q + baseK, rsK, len, kb, K, tid);
-    tile_load<T, C, VEC>(rk, k + baseK, rsK, len, kb, K, tid);
-    tile_load<T, C, VEC>(rg, g + baseK, rsK, len, kb, K, tid);
+    if constexpr (PRE) {
+      tile_load<T, C, VEC>(rk, gkg, K, C, kb, K, tid);   // rows past the chunk are zeros
+    } else {
+      tile_load<T, C, VEC>(rq, q + baseK, rsK, len, kb, K, tid);
+      tile_load<T, C, VEC>(rk, k + baseK, rsK, len, kb, K, tid);
+      tile_load<T, C, VEC>(rg, g + baseK, rsK, len, kb, K, tid);
+    }
     tile_load<T, 64, VEC>(rdh, dhs + (((long)c * H + hh) * K + kb) * V, V, min(64, K - kb), vb,
                           V, tid);
     if (kt > 0) __syncthreads();   // readers of the previous K tile are done
-    tile_store<T, C>(sQr, P64, rq, tid);
-    tile_store<T, C>(sKr, P64, rk, tid);
-    tile_store<T, C>(sGr, P64, rg, tid);
-    __syncthreads();
-    float d0[RPS], d1[RPS], gam0, gam1, r0, r1;
-    pair_cumsum<T, C>(sGr, P64, c_0, seg, sTot, sFirst, d0, d1, gam0, gam1, r0, r1);
+    if constexpr (PRE) {
+      tile_store<T, C>(sKg, P64, rk, tid);
+      if (tid < 64) sEg[tid] = kb + tid < K ? gpost[kb + tid] : 0.f;
+    } else {
+      tile_store<T, C>(sQr, P64, rq, tid);
+      tile_store<T, C>(sKr, P64, rk, tid);
+      tile_store<T, C>(sGr, P64, rg, tid);
+      __syncthreads();
+      float d0[RPS], d1[RPS], gam0, gam1, r0, r1;
+      pair_cumsum<T, C>(sGr, P64, c_0, seg, sTot, sFirst, d0, d1, gam0, gam1, r0, r1);
 #pragma unroll
-    for (int rr = 0; rr < RPS; ++rr) {
-      const int row = seg * RPS + rr;
-      float qa, qb, ka, kb2;
-      Pair<T>::ld(sQr + row * P64 + c_0, qa, qb);
-      Pair<T>::ld(sKr + row * P64 + c_0, ka, kb2);
-      const float e0 = gexp<T>(d0[rr]), e1 = gexp<T>(d1[rr]);
-      Pair<T>::st(sQg + row * P64 + c_0, qa * e0, qb * e1);
-      Pair<T>::st(sKg + row * P64 + c_0, ka / e0, kb2 / e1);
-    }
-    if (seg == 0) {
-      sEg[c_0] = gexp<T>(gam0 - r0);
-      sEg[c_1] = gexp<T>(gam1 - r1);
+      for (int rr = 0; rr < RPS; ++rr) {
+        const int row = seg * RPS + rr;
+        float qa, qb, ka, kb2;
+        Pair<T>::ld(sQr + row * P64 + c_0, qa, qb);
+        Pair<T>::ld(sKr + row * P64 + c_0, ka, kb2);
+        const float e0 = gexp<T>(d0[rr]), e1 = gexp<T>(d1[rr]);
+        Pair<T>::st(sQg + row * P64 + c_0, qa * e0, qb * e1);
+        Pair<T>::st(sKg + row * P64 + c_0, ka / e0, kb2 / e1);
+      }
+      if (seg == 0) {
+        sEg[c_0] = gexp<T>(gam0 - r0);
+        sEg[c_1] = gexp<T>(gam1 - r1);
+      }
     }
     __syncthreads();
     // dh' = dh scaled per K row by e^{gamma - r}, so that k_d . dh = kg . dh'
@@ -514,7 +532,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
 #pragma unroll
     for (int j = 0; j < NA; ++j) {   // A[i][j] += qg[i] . kg[j]
       const int t = w + 4 * j;
-      if (t < NT_A) {
+      if (!PRE && t < NT_A) {
         const int mi = t / NTM, ni = t % NTM;
         if (ni <= mi)
           mma_tile<T>(Aacc[j], sQg + mi * 16 * P64, P64, sKg + ni * 16 * P64, P64, 64, lane);
@@ -533,16 +551,22 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
   {
     uint4 rdo[PPT];
     tile_load<T, C, VEC>(rdo, dout + baseV, rsV, len, vb, V, tid);
-    for (int i = tid; i < CP * PCP; i += 256) sA[i] = zero_elem<T>();
-    if (CP > C)
-      for (int i = tid; i < (CP - C) * P64; i += 256) sDo[C * P64 + i] = zero_elem<T>();
-    __syncthreads();   // zero fill before the tile writes below
+    if constexpr (PRE) {   // A as made by the gating kernel (masked and scaled)
+      uint4 ra[PPT];
+      tile_load<T, C, VEC>(ra, gA, 64, C, 0, 64, tid);
+      tile_store<T, C>(sA, PCP, ra, tid);
+    } else {
+      for (int i = tid; i < CP * PCP; i += 256) sA[i] = zero_elem<T>();
+      if (CP > C)
+        for (int i = tid; i < (CP - C) * P64; i += 256) sDo[C * P64 + i] = zero_elem<T>();
+      __syncthreads();   // zero fill before the tile writes below
+    }
     tile_store<T, C>(sDo, P64, rdo, tid);
   }
 #pragma unroll
   for (int j = 0; j < NA; ++j) {
     const int t = w + 4 * j;
-    if (t < NT_A) {
+    if (!PRE && t < NT_A) {
       const int mi = t / NTM, ni = t % NTM;
       if (ni <= mi) {
         const int cc = ni * 16 + (lane & 15);
@@ -598,6 +622,17 @@ static hipError_t launch_bwd(const BwdArgs& p, hipStream_t st, int which) {
   }
   if (which & 2) {
     using Lay = DvLayout<T, C>;
+    if constexpr (C == 64 && sizeof(T) == 2) {
+      if (p.gate_ws) {
+        hipError_t e = hipFuncSetAttribute((const void*)chunk_bwd_dv_kernel<T, C, VEC, true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           Lay::bytes);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((chunk_bwd_dv_kernel<T, C, VEC, true>), dim3((unsigned)(nch * VT)),
+                           dim3(256), Lay::bytes, st, p);
+        return hipGetLastError();
+      }
+    }
     hipError_t e = hipFuncSetAttribute((const void*)chunk_bwd_dv_kernel<T, C, VEC>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
     if (e != hipSuccess) return e;

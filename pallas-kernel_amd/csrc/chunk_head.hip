@@ -609,9 +609,6 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 // (c * H + h) * GW bytes: qg bf16 [64][K], kg bf16 [64][K], A bf16 [64][64] (scaled, causal),
 // factors f32 [3][K]: scale 2^r, 2^r, 2^{gamma - r}.
 // ---------------------------------------------------------------------------
-__host__ __device__ constexpr long gate_ws_entry(int K) {
-  return 2L * HC * K * 2 + (long)HC * HC * 2 + 3L * K * 4;
-}
 
 template <int KP>
 struct GPLayout {
@@ -1766,20 +1763,27 @@ static hipError_t launch_head_fwd_sg(const HeadFwdArgs& p, hipStream_t st, long 
   return hipGetLastError();
 }
 
+hipError_t run_head_gate(const HeadFwdArgs& p, hipStream_t st) {
+  if (head_kp(p.K) != 256 || p.si.cu || !p.g || !p.gate_ws) return hipErrorInvalidValue;
+  const int nt = (p.si.T + HC - 1) / HC;
+  if ((long)nt * p.H * p.si.N == 0) return hipSuccess;
+  using GL = GPLayout<256>;
+  hipError_t e = hipFuncSetAttribute((const void*)head_gate_kernel<256>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, GL::bytes);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((head_gate_kernel<256>), dim3((unsigned)(nt * p.H), (unsigned)p.si.N),
+                     dim3(HNT), GL::bytes, st, p);
+  return hipGetLastError();
+}
+
 template <int KP, int VP>
 static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   const long blocks = (long)p.si.N * p.NS * p.H * ((p.V + VP - 1) / VP);
   if (blocks == 0) return hipSuccess;
   if constexpr (KP == 256) {
     if (p.g && p.gate_ws) {   // per-chunk gating once, then the V tiles' blocks
-      using GL = GPLayout<KP>;
-      hipError_t e = hipFuncSetAttribute((const void*)head_gate_kernel<KP>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, GL::bytes);
+      hipError_t e = run_head_gate(p, st);
       if (e != hipSuccess) return e;
-      const int nt = (p.si.T + HC - 1) / HC;
-      hipLaunchKernelGGL((head_gate_kernel<KP>), dim3((unsigned)(nt * p.H), (unsigned)p.si.N),
-                         dim3(HNT), GL::bytes, st, p);
-      if ((e = hipGetLastError()) != hipSuccess) return e;
       using Lay = HFLayout<KP, VP, false>;
       e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP, false, true>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);

@@ -61,11 +61,21 @@ struct BwdArgs {
   const void* h;        // [NC, H, K, V] forward states (chunk start)
   const void* dh;       // [NC, H, K, V] state gradients (chunk end)
   void *dq, *dk, *dv, *dg;
+  // per-chunk gating workspace (head_gate_kernel: bf16, chunk 64, fixed-length; nullable):
+  // the dv kernel then streams gated k, A and the column factors instead of recomputing
+  // them in every V tile's block
+  const void* gate_ws;
   float scale;
   int H, K, V;
   int vec;              // every base pointer 16-byte aligned and K, V multiples of 16 bytes
   SeqInfo si;
 };
+// Bytes of one (chunk, head) entry of the per-chunk gating workspace (chunk 64): qg, kg
+// [64][K] bf16, A [64][64] bf16 (masked, scaled), the column factors scale 2^r, 2^r,
+// 2^{gamma-r} [3][K] f32.
+__host__ __device__ constexpr long gate_ws_entry(int K) {
+  return 2L * 64 * K * 2 + 64L * 64 * 2 + 3L * K * 4;
+}
 // which: bit 0 = dq/dk/dg kernel, bit 1 = dv kernel
 hipError_t run_chunk_bwd(const BwdArgs& p, int dtype, hipStream_t st, int which = 3);
 
@@ -227,6 +237,8 @@ struct HeadFwdArgs {
   SeqInfo si;
 };
 hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st);
+// Per-chunk gating of wide heads (K = 256) into p.gate_ws (q, k, g, scale, H, K, si read).
+hipError_t run_head_gate(const HeadFwdArgs& p, hipStream_t st);
 
 struct HeadBwdArgs {
   const void *q, *k, *v, *g, *dout;
