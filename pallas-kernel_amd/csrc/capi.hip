@@ -497,6 +497,22 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   float *seg_st = nullptr, *seg_gm = nullptr;
   void* gate = nullptr;   // per-chunk gating of wide heads (when the workspace holds it)
   if (head) seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, NS, SL, seg_st, seg_gm, &gate);
+  if (head_bwd) gate = nullptr;
+  if (gate) {   // gated q, k, A and the column factors once per (chunk, head): the scans and
+                // the dv kernel stream them
+    tops::HeadFwdArgs a = {};
+    a.q = q;
+    a.k = k;
+    a.g = g;
+    a.gate_ws = gate;
+    a.scale = scale;
+    a.H = (int)H;
+    a.K = (int)K;
+    a.V = (int)V;
+    a.si = si;
+    rc = hip_status(tops::run_head_gate(a, st), "chunk_bwd (gating)");
+    if (rc) return rc;
+  }
   auto head_scan = [&](bool rev, const void* a, const void* b, const float* s_init, void* s_all,
                        float* s_final, float sc) {
     tops::HeadScanArgs s = {};
@@ -508,6 +524,7 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     s.s_final = s_final;
     s.seg_state = seg_st;
     s.seg_gam = seg_gm;
+    s.gate_ws = gate;
     s.NS = NS;
     s.SL = SL;
     s.scale = sc;
@@ -571,20 +588,6 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     // wide heads: the full-head reverse scan stores dh for the per-chunk gradient kernels
     rc = hip_status(head_scan(true, q, dout, dht, dh_ws, dh0, scale), "chunk_bwd (dh scan)");
     if (rc) return rc;
-    if (gate) {   // gated k, A and the column factors once per (chunk, head), for dv
-      tops::HeadFwdArgs a = {};
-      a.q = q;
-      a.k = k;
-      a.g = g;
-      a.gate_ws = gate;
-      a.scale = scale;
-      a.H = (int)H;
-      a.K = (int)K;
-      a.V = (int)V;
-      a.si = si;
-      rc = hip_status(tops::run_head_gate(a, st), "chunk_bwd (gating)");
-      if (rc) return rc;
-    }
   } else {
     tops::ScanArgs d;
     d.a = q;
@@ -615,7 +618,7 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   p.dk = dk;
   p.dv = dv;
   p.dg = dg;
-  p.gate_ws = head && !head_bwd ? gate : nullptr;
+  p.gate_ws = gate;
   p.scale = scale;
   p.H = (int)H;
   p.K = (int)K;

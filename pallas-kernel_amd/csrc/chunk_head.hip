@@ -428,8 +428,12 @@ struct HSLayout {
 // segment's final state and total decay but no per-chunk state): one step per pair of
 // chunks, a 128-row tile with its own cumsum; the recurrence is the same row by row, so the
 // final state is unchanged, and every factor stays <= 1.
-template <int KP, int VP, bool REV, int NT, bool SG, int CR = HC>
+// PRE (wide heads with the per-chunk gating workspace): the gated rows come from there --
+// qg (scale 2^r) for the reverse scan, kg (2^{gamma-r}) for the forward one -- with the
+// chunk decays, so a step has no cumsum and no per-element exp2.
+template <int KP, int VP, bool REV, int NT, bool SG, int CR = HC, bool PRE = false>
 __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
+  static_assert(!PRE || (!SG && CR == HC && HMap<KP, NT, CR>::RPT >= 4), "gated-tile scan");
   using MA = HMap<KP, NT, CR>;
   using MB = HMap<VP, NT, CR>;
   using TL = HTilesN<KP, VP, NT / 64>;
@@ -508,8 +512,24 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     int t0, len, ci;
     span(min(step, nsteps - 1), t0, len, ci);
     const long oa = (long)t0 * rsK + (long)hh * K;
-    hload<RPT>(R.a, a + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
-    if constexpr (SG)
+    if constexpr (PRE) {
+      // gated rows (zeros past the chunk); g[0..1] = this thread's 8 column factors
+      // (reverse: scale 2^r, forward: 2^{gamma-r}), g[2..3] = their chunk gate sums gamma
+      const unsigned char* ent =
+          (const unsigned char*)p.gate_ws + ((long)(sg.c0 + ci) * H + hh) * gate_ws_entry(K);
+      hload<RPT>(R.a, (const bf16*)ent + (REV ? 0 : HC * K), (uint32_t)K, rs * RPT, HC, cg * 8,
+                 K);
+      const float* fac = (const float*)(ent + 2L * HC * K * 2 + HC * HC * 2);
+      const uint32_t co = (uint32_t)min(cg * 8, K - 8) * 4u;
+      R.g[0] = ld16(fac + (REV ? 0 : 2 * K), co);
+      R.g[1] = ld16(fac + (REV ? 0 : 2 * K), co + 16u);
+      R.g[2] = ld16(fac + 3 * K, co);
+      R.g[3] = ld16(fac + 3 * K, co + 16u);
+    } else {
+      hload<RPT>(R.a, a + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
+    }
+    if constexpr (PRE) {
+    } else if constexpr (SG)
       sg_load<RPT>(R.gs, p.gs, p.gs_ts, t0, rs * RPT, len, hh);
     else
       hload<RPT>(R.g, g + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
@@ -525,7 +545,25 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     int t0, len, ci;
     span(step, t0, len, ci);
     float gt[RPT][8], gam[8], first[8];
-    if constexpr (SG) {
+    if constexpr (PRE) {
+      __syncthreads();   // the previous step's reads of the tiles are done
+      float fa[8], gs[8];
+      *reinterpret_cast<uint4*>(fa) = R.g[0];
+      *reinterpret_cast<uint4*>(fa + 4) = R.g[1];
+      *reinterpret_cast<uint4*>(gs) = R.g[2];
+      *reinterpret_cast<uint4*>(gs + 4) = R.g[3];
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const int row = rs * RPT + j;
+        float x[8];
+        unpack8(mask16(R.a[j], colA ? ~0u : 0u), x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= fa[e];
+        *reinterpret_cast<uint4*>(sA + row * PKP + cg * 8) = pack8(x);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gam[e] = gs[e];
+    } else if constexpr (SG) {
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
         const float x = (colA && rs * RPT + j < len) ? R.gs[j] : 0.f;
@@ -541,15 +579,17 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
       head_cumsum<KP, NT, CR>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
     }
     (void)first;
+    if constexpr (!PRE) {
 #pragma unroll
-    for (int j = 0; j < RPT; ++j) {
-      const int row = rs * RPT + j;
-      float x[8];
-      unpack8(mask16(R.a[j], (colA && row < len) ? ~0u : 0u), x);
+      for (int j = 0; j < RPT; ++j) {
+        const int row = rs * RPT + j;
+        float x[8];
+        unpack8(mask16(R.a[j], (colA && row < len) ? ~0u : 0u), x);
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        x[e] *= REV ? p.scale * exp2_hw(gt[j][e]) : exp2_hw(gam[e] - gt[j][e]);
-      *reinterpret_cast<uint4*>(sA + row * PKP + cg * 8) = pack8(x);
+        for (int e = 0; e < 8; ++e)
+          x[e] *= REV ? p.scale * exp2_hw(gt[j][e]) : exp2_hw(gam[e] - gt[j][e]);
+        *reinterpret_cast<uint4*>(sA + row * PKP + cg * 8) = pack8(x);
+      }
     }
 #pragma unroll
     for (int j = 0; j < VRPT; ++j) {
@@ -607,7 +647,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 // this kernel makes them once per (chunk, head) into a caller workspace, and the forward's
 // PRE build reads them instead of gating for itself. Workspace entry of chunk c, head h at
 // (c * H + h) * GW bytes: qg bf16 [64][K], kg bf16 [64][K], A bf16 [64][64] (scaled, causal),
-// factors f32 [3][K]: scale 2^r, 2^r, 2^{gamma - r}.
+// factors f32 [4][K]: scale 2^r, 2^r, 2^{gamma - r}, gamma (base 2).
 // ---------------------------------------------------------------------------
 
 template <int KP>
@@ -691,6 +731,7 @@ __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
     st_f8(gf + cg * 8, f0);
     st_f8(gf + K + cg * 8, f1);
     st_f8(gf + 2 * K + cg * 8, f2);
+    st_f8(gf + 3 * K + cg * 8, gam);
   }
   __syncthreads();
   // the 16 tiles of A (the upper ones as zeros), two per wave
@@ -1682,16 +1723,16 @@ long head_seg_ws_bytes(int N, int NS, int H, int K, int V) {
   return st + (gm + 255) / 256 * 256;
 }
 
-template <int KP, int VP, bool REV, bool SG, int CR>
+template <int KP, int VP, bool REV, bool SG, int CR, bool PRE = false>
 static hipError_t launch_head_scan_cr(const HeadScanArgs& p, hipStream_t st, long blocks) {
   constexpr int NT = HNT;
   using Lay = HSLayout<KP, VP, NT, CR>;
   static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
-  const void* fn = (const void*)head_scan_kernel<KP, VP, REV, NT, SG, CR>;
+  const void* fn = (const void*)head_scan_kernel<KP, VP, REV, NT, SG, CR, PRE>;
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      Lay::bytes);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV, NT, SG, CR>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((head_scan_kernel<KP, VP, REV, NT, SG, CR, PRE>), dim3((unsigned)blocks),
                      dim3(NT), Lay::bytes, st, p);
   return hipGetLastError();
 }
@@ -1704,6 +1745,8 @@ static hipError_t launch_head_scan(const HeadScanArgs& p, hipStream_t st, long b
     if (p.pass == 1)
       return p.g ? launch_head_scan_cr<KP, VP, REV, false, 2 * HC>(p, st, blocks)
                  : launch_head_scan_cr<KP, VP, REV, true, 2 * HC>(p, st, blocks);
+  } else {
+    if (p.g && p.gate_ws) return launch_head_scan_cr<KP, VP, REV, false, HC, true>(p, st, blocks);
   }
   return p.g ? launch_head_scan_cr<KP, VP, REV, false, HC>(p, st, blocks)
              : launch_head_scan_cr<KP, VP, REV, true, HC>(p, st, blocks);
@@ -1781,10 +1824,9 @@ static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   const long blocks = (long)p.si.N * p.NS * p.H * ((p.V + VP - 1) / VP);
   if (blocks == 0) return hipSuccess;
   if constexpr (KP == 256) {
-    if (p.g && p.gate_ws) {   // per-chunk gating once, then the V tiles' blocks
-      hipError_t e = run_head_gate(p, st);
-      if (e != hipSuccess) return e;
+    if (p.g && p.gate_ws) {   // the V tiles' blocks stream the per-chunk gating
       using Lay = HFLayout<KP, VP, false>;
+      hipError_t e;
       e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP, false, true>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
       if (e != hipSuccess) return e;
@@ -1800,8 +1842,16 @@ static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
 }
 
 hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
+  // wide heads with a gating workspace: gate every chunk once, first; the segment pass and
+  // the forward's V tiles stream it
+  const bool gated = head_kp(p.K) == 256 && p.g && p.gate_ws;
+  if (gated) {
+    hipError_t e = run_head_gate(p, st);
+    if (e != hipSuccess) return e;
+  }
   if (p.NS > 1) {
     HeadScanArgs s = {};
+    s.gate_ws = gated ? p.gate_ws : nullptr;
     s.a = p.k;
     s.b = p.v;
     s.g = p.g;

@@ -72,9 +72,9 @@ struct BwdArgs {
 };
 // Bytes of one (chunk, head) entry of the per-chunk gating workspace (chunk 64): qg, kg
 // [64][K] bf16, A [64][64] bf16 (masked, scaled), the column factors scale 2^r, 2^r,
-// 2^{gamma-r} [3][K] f32.
+// 2^{gamma-r} and the chunk's summed gates gamma (base 2) [4][K] f32.
 __host__ __device__ constexpr long gate_ws_entry(int K) {
-  return 2L * 64 * K * 2 + 64L * 64 * 2 + 3L * K * 4;
+  return 2L * 64 * K * 2 + 64L * 64 * 2 + 4L * K * 4;
 }
 // which: bit 0 = dq/dk/dg kernel, bit 1 = dv kernel
 hipError_t run_chunk_bwd(const BwdArgs& p, int dtype, hipStream_t st, int which = 3);
@@ -214,6 +214,9 @@ struct HeadScanArgs {
   float* seg_gam;
   int NS, SL;
   int pass, s_begin, ns_launch;   // set by the launcher
+  // per-chunk gating workspace of wide heads (nullable): the scans then stream qg (reverse)
+  // or kg (forward) and the column factors instead of gating in every V tile's block
+  const void* gate_ws;
   float scale;            // reverse only
   int H, K, V;
   SeqInfo si;
