@@ -402,7 +402,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dqkg_kernel(BwdArgs p) {
 // dv
 // ---------------------------------------------------------------------------
 
-template <typename T, int C>
+template <typename T, int C, bool PRE = false>
 struct DvLayout {
   static constexpr int CP = C < 32 ? 32 : C;
   static constexpr int P64 = pitch_of<T>(64), PCP = pitch_of<T>(CP);
@@ -410,18 +410,20 @@ struct DvLayout {
   static constexpr int TILE = ((CP * P64 * ES) + 15) / 16 * 16;
   static constexpr int SQ = ((64 * P64 * ES) + 15) / 16 * 16;
   static constexpr int AT = ((CP * PCP * ES) + 15) / 16 * 16;
-  // region R: raw q, k, g (per K tile), later A and do | qg, kg | dh' = e^{gamma-r} dh
+  // region R: raw q, k, g (per K tile), later A and do | qg, kg | dh' = e^{gamma-r} dh.
+  // PRE (no raw tiles, no qg): kg | dh' in the loop, A | do after it, over the same bytes.
   static constexpr int qr = 0, kr = TILE, gr = 2 * TILE;
   static constexpr int a = 0, do_ = AT;
-  static constexpr int R = (3 * TILE > AT + TILE) ? 3 * TILE : AT + TILE;
-  static constexpr int qg = R, kg = R + TILE, dh = R + 2 * TILE;
-  static constexpr int bytes = dh + SQ;
+  static constexpr int R = PRE ? 0 : (3 * TILE > AT + TILE) ? 3 * TILE : AT + TILE;
+  static constexpr int qg = R, kg = PRE ? 0 : R + TILE, dh = PRE ? TILE : R + 2 * TILE;
+  static constexpr int loop_end = dh + SQ, after_end = do_ + TILE;
+  static constexpr int bytes = loop_end > after_end ? loop_end : after_end;
 };
 
 template <typename T, int C, bool VEC, bool PRE = false>
 __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
   static_assert(!PRE || C == 64, "the gating workspace holds chunks of 64");
-  using Lay = DvLayout<T, C>;
+  using Lay = DvLayout<T, C, PRE>;
   constexpr int CP = Lay::CP, P64 = Lay::P64, PCP = Lay::PCP;
   constexpr int EPP = 16 / (int)sizeof(T);
   constexpr int PPT = pieces_per_thread<T, C>(), HPT = pieces_per_thread<T, 64>();
@@ -624,12 +626,13 @@ static hipError_t launch_bwd(const BwdArgs& p, hipStream_t st, int which) {
     using Lay = DvLayout<T, C>;
     if constexpr (C == 64 && sizeof(T) == 2) {
       if (p.gate_ws) {
+        using LP = DvLayout<T, C, true>;
         hipError_t e = hipFuncSetAttribute((const void*)chunk_bwd_dv_kernel<T, C, VEC, true>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           Lay::bytes);
+                                           LP::bytes);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL((chunk_bwd_dv_kernel<T, C, VEC, true>), dim3((unsigned)(nch * VT)),
-                           dim3(256), Lay::bytes, st, p);
+                           dim3(256), LP::bytes, st, p);
         return hipGetLastError();
       }
     }
