@@ -108,8 +108,10 @@ int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void
 /*
  * Bytes of the optional sequence-segment workspace (`seg_ws`) of tops_gla_chunk_fwd and
  * tops_gla_chunk_bwd for this problem (0: the call does not use one). With it the
- * inter-chunk scans of fixed-length sequences run as parallel segments (local states,
- * a combine, then all segments at once) instead of one chunk after another.
+ * inter-chunk scans of fixed-length sequences run as parallel segments (local states, then
+ * all segments at once, each folding its entry state from them) instead of one chunk after
+ * another; for wide heads (K = 256, three or more 64-column V tiles) it also holds the
+ * per-chunk gating that the scans, the forward and the dv kernel then stream.
  * No counterpart in the reference (its scans are sequential grid axes, chunk_h.py:252-271).
  */
 int64_t tops_gla_chunk_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,

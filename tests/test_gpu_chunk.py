@@ -335,8 +335,8 @@ def test_north_star_shape_slices():
 @pytest.mark.parametrize("B,T,H", [(2, 4096, 4), (1, 2412, 2), (1, 2284, 2)],
                          ids=["even", "short-last", "odd"])
 def test_segmented_scans_match_sequential(B, T, H):
-    """The segment-parallel scans (local states over chunk pairs, combine, all segments at
-    once) give the sequential scan's results: tops_gla_chunk_fwd / _bwd with and without the
+    """The segment-parallel scans (local states over chunk pairs, then all segments at once,
+    each folding its entry state) give the sequential scan's results: tops_gla_chunk_fwd / _bwd with and without the
     workspace. 2412 tokens: 38 chunks (the last partial) in segments of 10, 10, 10, 8 (a
     short last segment); 2284 tokens: 36 chunks (the last partial) in 4 segments of 9, so
     every segment's pairs end with a single chunk."""
