@@ -59,6 +59,10 @@ FWD_CASES = [
     # tile), segmented (1024 tokens -> 2 segments x 3 V tiles)
     dict(B=1, T=1024, H=2, K=256, V=160, seed=804, C=64, h0=True, gate_div=16.0),
     dict(B=1, T=300, H=2, K=200, V=72, seed=805, C=64, h0=True),
+    # K = 200 (a partial last 64-column K slice) with three V tiles: per-chunk gating
+    # workspace, partial last chunk; 1100 tokens -> two segments streaming it
+    dict(B=1, T=300, H=2, K=200, V=200, seed=806, C=64, h0=True, gate_div=4.0),
+    dict(B=1, T=1100, H=2, K=200, V=192, seed=807, C=64, h0=True, gate_div=16.0),
 ]
 
 
@@ -147,6 +151,10 @@ BWD_CASES = [
     dict(B=1, T=1024, H=2, K=128, V=64, seed=814, C=64, h0=True, dht=True, gate_div=4.0),
     # wide head: full-head forward and dh scan (V tiles, segments), per-chunk gradients
     dict(B=1, T=1024, H=2, K=256, V=192, seed=815, C=64, h0=True, dht=True, gate_div=16.0),
+    # K = 200, three V tiles: the scans and the dv kernel stream the per-chunk gating (a
+    # partial last K slice, a partial last chunk, two segments)
+    dict(B=1, T=1100, H=2, K=200, V=192, seed=816, C=64, h0=True, dht=True, gate_div=8.0),
+    dict(B=1, T=300, H=2, K=200, V=200, seed=817, C=64, dht=True, gate_div=4.0),
 ]
 
 
