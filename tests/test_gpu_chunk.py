@@ -63,6 +63,9 @@ FWD_CASES = [
     # workspace, partial last chunk; 1100 tokens -> two segments streaming it
     dict(B=1, T=300, H=2, K=200, V=200, seed=806, C=64, h0=True, gate_div=4.0),
     dict(B=1, T=1100, H=2, K=200, V=192, seed=807, C=64, h0=True, gate_div=16.0),
+    # varlen wide head: no gating workspace (fixed-length only), every tile gates for itself
+    dict(B=1, T=400, H=2, K=256, V=192, seed=808, C=64, h0=True, cu=[0, 70, 256, 400],
+         gate_div=8.0),
 ]
 
 
@@ -155,6 +158,9 @@ BWD_CASES = [
     # partial last K slice, a partial last chunk, two segments)
     dict(B=1, T=1100, H=2, K=200, V=192, seed=816, C=64, h0=True, dht=True, gate_div=8.0),
     dict(B=1, T=300, H=2, K=200, V=200, seed=817, C=64, dht=True, gate_div=4.0),
+    # varlen wide head (no gating workspace)
+    dict(B=1, T=400, H=2, K=256, V=192, seed=818, C=64, h0=True, dht=True, cu=[0, 70, 256, 400],
+         gate_div=8.0),
 ]
 
 
