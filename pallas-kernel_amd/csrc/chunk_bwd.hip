@@ -238,19 +238,23 @@ __global__ __launch_bounds__(256) void chunk_bwd_dqkg_kernel(BwdArgs p) {
 #pragma unroll
   for (int j = 0; j < NO; ++j) Mqx[j] = M2[j] = zero4();
   float hdp = 0.f;
+  // V tiles: the next tile's loads are issued before this tile's products (its registers
+  // are free once the tile is in LDS), so they arrive under the MFMA work
   for (int vt = 0; vt < VT; ++vt) {
     if (vt > 0) {
-      const int vb = vt * 64;
-      tile_load<T, C, VEC>(rdo, dout + baseV, rsV, len, vb, V, tid);
-      tile_load<T, C, VEC>(rv, v + baseV, rsV, len, vb, V, tid);
-      tile_load<T, 64, VEC>(rh, hrow, V, klen, vb, V, tid);
-      tile_load<T, 64, VEC>(rdh, dhrow, V, klen, vb, V, tid);
       __syncthreads();   // readers of the previous V tile are done
       tile_store<T, C>(sDo, P64, rdo, tid);
       tile_store<T, C>(sV, P64, rv, tid);
       tile_store<T, 64>(sH, P64, rh, tid);
       tile_store<T, 64>(sDh, P64, rdh, tid);
       __syncthreads();
+    }
+    if (vt + 1 < VT) {
+      const int vb = (vt + 1) * 64;
+      tile_load<T, C, VEC>(rdo, dout + baseV, rsV, len, vb, V, tid);
+      tile_load<T, C, VEC>(rv, v + baseV, rsV, len, vb, V, tid);
+      tile_load<T, 64, VEC>(rh, hrow, V, klen, vb, V, tid);
+      tile_load<T, 64, VEC>(rdh, dhrow, V, klen, vb, V, tid);
     }
 #pragma unroll
     for (int j = 0; j < NA; ++j) {   // dA[i][j] += do[i] . v[j]   (lower tiles)
@@ -477,10 +481,14 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
   for (int j = 0; j < NO; ++j) Dacc[j] = zero4();
 
   uint4 rq[PPT], rk[PPT], rg[PPT], rdh[HPT];
-  for (int kt = 0; kt < KT; ++kt) {
+  float reg = 0.f;   // PRE: the 2^{gamma-r} factor of column tid of the K tile
+  // K tiles: the next tile's loads are issued once this tile's registers are in LDS, so they
+  // arrive under the MFMA work
+  auto load_kt = [&](int kt) {
     const int kb = kt * 64;
     if constexpr (PRE) {
       tile_load<T, C, VEC>(rk, gkg, K, C, kb, K, tid);   // rows past the chunk are zeros
+      if (tid < 64) reg = kb + tid < K ? gpost[kb + tid] : 0.f;
     } else {
       tile_load<T, C, VEC>(rq, q + baseK, rsK, len, kb, K, tid);
       tile_load<T, C, VEC>(rk, k + baseK, rsK, len, kb, K, tid);
@@ -488,10 +496,13 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
     }
     tile_load<T, 64, VEC>(rdh, dhs + (((long)c * H + hh) * K + kb) * V, V, min(64, K - kb), vb,
                           V, tid);
+  };
+  if (KT > 0) load_kt(0);
+  for (int kt = 0; kt < KT; ++kt) {
     if (kt > 0) __syncthreads();   // readers of the previous K tile are done
     if constexpr (PRE) {
       tile_store<T, C>(sKg, P64, rk, tid);
-      if (tid < 64) sEg[tid] = kb + tid < K ? gpost[kb + tid] : 0.f;
+      if (tid < 64) sEg[tid] = reg;
     } else {
       tile_store<T, C>(sQr, P64, rq, tid);
       tile_store<T, C>(sKr, P64, rk, tid);
@@ -531,6 +542,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
       }
     }
     __syncthreads();
+    if (kt + 1 < KT) load_kt(kt + 1);
 #pragma unroll
     for (int j = 0; j < NA; ++j) {   // A[i][j] += qg[i] . kg[j]
       const int t = w + 4 * j;
