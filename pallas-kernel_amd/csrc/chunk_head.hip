@@ -247,6 +247,72 @@ __device__ __forceinline__ void head_cumsum(const uint4 (&graw)[HMap<KP, NT, CR>
   head_cumsum_f<KP, NT, CR>(gt, gam, first, sTot, sFirst, cg, rs, lane, w);
 }
 
+// One-sided cumsum of the state scans, which gate a row with one side of the cumsum only:
+// the reverse scan with the inclusive prefix g~_j, the forward one with the exclusive suffix
+// gam - g~_j (the sum of the rows after j). gt holds the raw gates on entry and that exponent
+// (base 2) on return; gam = the tile's total, valid in the row segment rs == total_rs<REV>
+// only (the last one for the prefix, the first one for the suffix). Every wave reads only
+// the wave totals on its side. sTot [NT/64][KP]; one barrier.
+template <int KP, int NT, bool REV>
+__host__ __device__ constexpr int total_rs() {
+  return REV ? HMap<KP, NT, HC>::NRS - 1 : 0;
+}
+template <int KP, int NT, int CR, bool REV>
+__device__ __forceinline__ void scan_cumsum_f(GateRows<KP, NT, CR>& gt, float (&gam)[8],
+                                              float* sTot, int cg, int lane, int w) {
+  using M = HMap<KP, NT, CR>;
+  constexpr int NW = NT / 64;
+#pragma unroll
+  for (int j = 0; j < M::RPT; ++j) {   // the thread's own rows: inclusive prefix
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gt[j][e] = gt[j][e] * kLog2e + (j ? gt[j - 1][e] : 0.f);
+  }
+  // over the wave's row segments: inclusive prefix (REV) / suffix of the thread sums
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = gt[M::RPT - 1][e];
+  if constexpr (M::NCG == 16) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = REV ? rows4_prefix(x[e], lane) : rows4_suffix(x[e], lane);
+  } else {
+#pragma unroll
+    for (int d = M::NCG; d < 64; d <<= 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (REV) {
+          const float y = __shfl_up(x[e], d);
+          if (lane >= d) x[e] += y;
+        } else {
+          const float y = __shfl_down(x[e], d);
+          if (lane + d < 64) x[e] += y;
+        }
+      }
+    }
+  }
+  // wave total: held by the last row segment (prefix) / the first one (suffix)
+  if (REV ? lane >= 64 - M::NCG : lane < M::NCG) st_f8(sTot + w * KP + cg * 8, x);
+  __syncthreads();
+  float off[8], t[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) off[e] = 0.f;
+  // the earlier (REV) / later waves' totals; w is wave-uniform: plain loops
+  for (int ww = REV ? 0 : w + 1; ww < (REV ? w : NW); ++ww) {
+    ld_f8(sTot + ww * KP + cg * 8, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) off[e] += t[e];
+  }
+  float own[8];   // the thread's own row sum
+#pragma unroll
+  for (int e = 0; e < 8; ++e) own[e] = gt[M::RPT - 1][e];
+#pragma unroll
+  for (int j = 0; j < M::RPT; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      gt[j][e] = REV ? gt[j][e] + (x[e] - own[e]) + off[e] : (x[e] - gt[j][e]) + off[e];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) gam[e] = REV ? gt[M::RPT - 1][e] : x[e] + off[e];
+}
+
 // Scalar gates (simple GLA, g_gamma): one float per row and head, the same for every key
 // column: gate(t, h) = gs[t * gs_ts + h] (gs_ts = 0: a per-head constant). Loads of rows
 // past the chunk are clamped to its last row; the caller masks them.
@@ -412,15 +478,15 @@ __host__ __device__ constexpr int head_vp(int KP, int V) {
 // ---------------------------------------------------------------------------
 // State scan: forward h (a = k, b = v) or reverse dh (a = q, b = do)
 // ---------------------------------------------------------------------------
-// LDS of head_scan_kernel: the gated a tile and the b tile of CR rows, cumsum scratch.
+// LDS of head_scan_kernel: the gated a tile and the b tile of CR rows, the wave totals of
+// the cumsum, the step's decays.
 template <int KP, int VP, int NT, int CR>
 struct HSLayout {
   static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP);
   static constexpr int a = 0;
   static constexpr int b = a + CR * PKP * 2;
   static constexpr int tot = b + CR * PVP * 2;
-  static constexpr int first = tot + (NT / 64) * KP * 4;
-  static constexpr int gam = first + KP * 4;
+  static constexpr int gam = tot + (NT / 64) * KP * 4;
   static constexpr int bytes = gam + KP * 4;
 };
 
@@ -446,7 +512,6 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   bf16* sA = reinterpret_cast<bf16*>(smem + Lay::a);
   bf16* sB = reinterpret_cast<bf16*>(smem + Lay::b);
   float* sTot = reinterpret_cast<float*>(smem + Lay::tot);
-  float* sFirst = reinterpret_cast<float*>(smem + Lay::first);
   float* sGam = reinterpret_cast<float*>(smem + Lay::gam);
 
   const bf16* __restrict__ a = (const bf16*)p.a;
@@ -473,6 +538,8 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   const int cg = tid % MA::NCG, rs = tid / MA::NCG;    // a / g mapping
   const int vg = tid % MB::NCG, vrs = tid / MB::NCG;   // b mapping
   const bool colA = cg * 8 < K, colB = vg * 8 < Vw;
+  // the row segment that holds the tile's total decay (every one with the gating workspace)
+  constexpr int TRS = PRE ? 0 : total_rs<KP, NT, REV>();
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
   f32x4 acc[NTV][NTK];
@@ -544,7 +611,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   auto body = [&](int step, Regs& R) {
     int t0, len, ci;
     span(step, t0, len, ci);
-    float gt[RPT][8], gam[8], first[8];
+    float gt[RPT][8], gam[8];
     if constexpr (PRE) {
       __syncthreads();   // the previous step's reads of the tiles are done
       float fa[8], gs[8];
@@ -570,15 +637,13 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) gt[j][e] = x;
       }
-      head_cumsum_f<KP, NT, CR>(gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+      scan_cumsum_f<KP, NT, CR, REV>(gt, gam, sTot, cg, lane, w);
     } else {
-      uint4 gm[RPT];
 #pragma unroll
       for (int j = 0; j < RPT; ++j)
-        gm[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
-      head_cumsum<KP, NT, CR>(gm, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+        unpack8(mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u), gt[j]);
+      scan_cumsum_f<KP, NT, CR, REV>(gt, gam, sTot, cg, lane, w);
     }
-    (void)first;
     if constexpr (!PRE) {
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
@@ -587,7 +652,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
         unpack8(mask16(R.a[j], (colA && row < len) ? ~0u : 0u), x);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          x[e] *= REV ? p.scale * exp2_hw(gt[j][e]) : exp2_hw(gam[e] - gt[j][e]);
+          x[e] *= REV ? p.scale * exp2_hw(gt[j][e]) : exp2_hw(gt[j][e]);
         *reinterpret_cast<uint4*>(sA + row * PKP + cg * 8) = pack8(x);
       }
     }
@@ -597,7 +662,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
       *reinterpret_cast<uint4*>(sB + row * PVP + vg * 8) =
           mask16(R.b[j], (colB && row < len) ? ~0u : 0u);
     }
-    if (rs == 0) {
+    if (rs == TRS) {
       float eg[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -633,7 +698,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   if (p.pass == 1) {
     store_state_f32<NTV, NTK>(acc, p.seg_state + ((long)(sg.seq * p.NS + s) * H + hh) * KV + cv,
                               K, Vw, vt0, kt0, lane, V);
-    if (vt == 0 && rs == 0 && colA)   // the decays are the same for every V tile
+    if (vt == 0 && rs == TRS && colA)   // the decays are the same for every V tile
       st_f8(p.seg_gam + ((long)(sg.seq * p.NS + s) * H + hh) * K + cg * 8, gsum);
   } else if (last_seg && p.s_final) {
     store_state_f32<NTV, NTK>(acc, p.s_final + ((long)sg.seq * H + hh) * KV + cv, K, Vw, vt0,
