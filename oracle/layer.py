@@ -14,6 +14,12 @@ Follows:
 
 Parameters come in as a dict of float64 tensors keyed by the torch module's parameter names
 (``q_proj.weight`` [out, in], ``gk_proj.1.bias``, ``q_conv1d.weight`` [D, 1, W], ...).
+
+Pinning (``tests/test_oracle.py``): ``recurrence`` against the pinned numpy
+``naive_recurrent_gla``; ``rms_norm``, ``gate_logsigmoid`` and ``short_conv`` by closed forms
+and brute-force taps. ``gla_layer`` is parity unpinned beyond those parts: its composition
+(projections, head split, reshapes) has no independent check, since the reference's layer
+tests compare against a torch layer that cannot be run here.
 """
 
 from __future__ import annotations
