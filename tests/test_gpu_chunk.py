@@ -115,6 +115,26 @@ def test_chunk_gla_fwd_bf16(cfg):
     check("ht", ht, hn, "bf16")
 
 
+def test_forward_same_with_and_without_grad():
+    """The full-head forward stores the per-chunk states (the backward's residual) only when a
+    gradient is wanted; o and the final state are bit-identical either way, segmented (1024
+    tokens: 2 segments) and not."""
+    G = _gla()
+    for T in (256, 1024):
+        q, k, v, g, s0, _, _ = make_inputs(2, T, 2, 128, 128, 611, gate_div=16.0, h0=True,
+                                           dtype="bf16")
+        x = [to_dev(a, "bf16") for a in (q, k, v, g)]
+        h0 = to_dev(s0, "state")
+        o0, h0n = G.chunk_gla(*x, initial_state=h0, output_final_state=True, chunk_size=64)
+        xg = [a.clone().requires_grad_() for a in x]
+        o1, h1n = G.chunk_gla(*xg, initial_state=h0, output_final_state=True, chunk_size=64)
+        torch.cuda.synchronize()
+        assert torch.equal(o0, o1.detach()), f"T={T}: o differs"
+        assert torch.equal(h0n, h1n.detach()), f"T={T}: final state differs"
+        o_ref, _ = orc.naive_recurrent_gla(q, k, v, g, initial_state=s0, output_final_state=True)
+        check("o", to_np(o0), o_ref, "bf16")
+
+
 def test_no_final_state_and_state_split():
     G = _gla()
     q, k, v, g, _, _, _ = make_inputs(1, 40, 2, 16, 32, 77)
