@@ -66,6 +66,10 @@ FWD_CASES = [
     # varlen wide head: no gating workspace (fixed-length only), every tile gates for itself
     dict(B=1, T=400, H=2, K=256, V=192, seed=808, C=64, h0=True, cu=[0, 70, 256, 400],
          gate_div=8.0),
+    # varlen on the main shape (full-head kernels, unsegmented): unaligned sequences, one of a
+    # single token
+    dict(B=1, T=700, H=2, K=128, V=128, seed=809, C=64, h0=True, cu=[0, 130, 131, 500, 700],
+         gate_div=8.0),
 ]
 
 
@@ -181,6 +185,9 @@ BWD_CASES = [
     # varlen wide head (no gating workspace)
     dict(B=1, T=400, H=2, K=256, V=192, seed=818, C=64, h0=True, dht=True, cu=[0, 70, 256, 400],
          gate_div=8.0),
+    # varlen on the main shape (full-head kernels): unaligned sequences, one of a single token
+    dict(B=1, T=700, H=2, K=128, V=128, seed=819, C=64, h0=True, dht=True,
+         cu=[0, 130, 131, 500, 700], gate_div=8.0),
 ]
 
 
