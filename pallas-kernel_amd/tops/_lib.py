@@ -194,8 +194,10 @@ class SeqLayout:
             return
         cu = to_list(cu_seqlens)
         assert self.B == 1, f"cu_seqlens requires B == 1, got B={self.B}"
-        assert len(cu) >= 2 and cu[0] == 0 and all(b >= a for a, b in zip(cu, cu[1:])), \
-            f"cu_seqlens must be non-decreasing from 0: {cu}"
+        # every sequence holds at least one token: the kernels read a sequence's last row, so
+        # an empty one is refused here rather than indexed
+        assert len(cu) >= 2 and cu[0] == 0 and all(b > a for a, b in zip(cu, cu[1:])), \
+            f"cu_seqlens must be strictly increasing from 0 (no empty sequences): {cu}"
         assert cu[-1] <= self.T, f"cu_seqlens[-1]={cu[-1]} exceeds T={self.T}"
         self.cu_list = cu
         self.N = len(cu) - 1

@@ -202,3 +202,13 @@ def test_simple_chunk_validation():
     assert rc == 2 and "full-head" in msg
     rc, msg = _rc("tops_gla_simple_chunk_bwd", *(bwd(128, 128)[:6] + [NULL] + bwd(128, 128)[7:]))
     assert rc == 1 and "h_ws is required" in msg
+
+
+def test_seq_layout_refuses_bad_cu_seqlens():
+    """cu_seqlens must start at 0, increase strictly (no empty sequence) and end within T;
+    refused on the host, before anything reaches the device."""
+    cpu = torch.device("cpu")
+    for cu, msg in (([0, 3, 3, 10], "no empty sequences"), ([1, 5, 10], "strictly increasing"),
+                    ([0, 6, 4, 10], "strictly increasing"), ([0, 4, 12], "exceeds T")):
+        with pytest.raises(AssertionError, match=msg):
+            _lib.SeqLayout(1, 10, 4, cu, cpu)
