@@ -16,6 +16,9 @@
  *    otherwise B must be 1, `cu_seqlens` is a device int32 array [N + 1] of token offsets
  *    and `chunk_offsets` a device int32 array [N + 1] with the prefix sums of
  *    ceil(len_i / chunk_size); `NC` is the total number of chunks (chunk_offsets[N]).
+ *    Every sequence holds at least one token (cu_seqlens strictly increasing, ending at most
+ *    at T): the library cannot read device offsets on the host, so this is the caller's
+ *    precondition (the Python layer checks it before the call).
  *    For fixed-length calls NC must equal B * ceil(T / chunk_size).
  *  - Per-chunk state buffers ([NC, H, K, V], element type `dtype`) are caller-provided
  *    workspaces; the library allocates nothing.
