@@ -15,11 +15,12 @@ Follows:
 Parameters come in as a dict of float64 tensors keyed by the torch module's parameter names
 (``q_proj.weight`` [out, in], ``gk_proj.1.bias``, ``q_conv1d.weight`` [D, 1, W], ...).
 
-Pinning (``tests/test_oracle.py``): ``recurrence`` against the pinned numpy
-``naive_recurrent_gla``; ``rms_norm``, ``gate_logsigmoid`` and ``short_conv`` by closed forms
-and brute-force taps. ``gla_layer`` is parity unpinned beyond those parts: its composition
-(projections, head split, reshapes) has no independent check, since the reference's layer
-tests compare against a torch layer that cannot be run here.
+Pinning: ``recurrence`` against the pinned numpy ``naive_recurrent_gla``; ``rms_norm``,
+``gate_logsigmoid`` and ``short_conv`` by closed forms and brute-force taps
+(``tests/test_oracle.py``); ``gla_layer`` (the composition: projections, GQA repeat, gate,
+norm and output gate, out-projection; output and every gradient) against fixtures written
+by the reference's own torch CPU layer, ``tests/src/layers/gla.py:53``, on twelve cases of
+the reference's layer-test table (``tests/test_layer_golden.py``, ``tests/golden/``).
 """
 
 from __future__ import annotations

@@ -1,10 +1,14 @@
 // extern "C" entry points declared in include/tops_gla.h: argument validation, sequence
-// layout, and kernel dispatch. Nothing here allocates or synchronizes.
+// layout, and kernel dispatch. No entry point allocates device memory or synchronizes (the
+// measurement hook at the end, a profiling aid, creates host-side HIP events once and its
+// reading call waits for its last event).
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <initializer_list>
+#include <mutex>
 
 #include "../../include/tops_gla.h"
 #include "common.hpp"
@@ -144,16 +148,20 @@ void seg_setup(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void* w
 
 namespace tops {
 
-// Measurement hook state (process-wide; for profiling runs, not for concurrent callers):
-// a ring of KT_RING event pairs per kernel, one pair per launch while timing is on.
+// Measurement hook state (process-wide, a profiling aid): a ring of KT_RING event pairs per
+// kernel, one pair per launch while timing is on. The flag is read without the lock (off: the
+// launch paths do nothing more); while it is on, marks, enabling and reading are serialized.
 constexpr int KT_RING = 256;
-static bool g_kt_on = false;
+static std::atomic<bool> g_kt_on{false};
+static std::mutex g_kt_mu;
 static bool g_kt_made = false;
 static long g_kt_n[KT_COUNT] = {};            // launches recorded since timing was enabled
 static hipEvent_t g_kt_ev[KT_COUNT][KT_RING][2];
 
 void ktimer_mark(int which, bool stop, hipStream_t st) {
-  if (!g_kt_on) return;
+  if (!g_kt_on.load(std::memory_order_relaxed)) return;
+  std::lock_guard<std::mutex> lk(g_kt_mu);
+  if (!g_kt_on.load(std::memory_order_relaxed)) return;
   const long n = g_kt_n[which];
   if (hipEventRecord(g_kt_ev[which][n % KT_RING][stop ? 1 : 0], st) == hipSuccess && stop)
     g_kt_n[which] = n + 1;
@@ -164,7 +172,8 @@ void ktimer_mark(int which, bool stop, hipStream_t st) {
 extern "C" {
 
 int tops_gla_kernel_timing(int enable) {
-  if (enable && !tops::g_kt_made) {
+  std::lock_guard<std::mutex> lk(tops::g_kt_mu);
+  if (enable && !tops::g_kt_made) {   // host-side event objects, created once
     for (int i = 0; i < tops::KT_COUNT; ++i)
       for (int r = 0; r < tops::KT_RING; ++r)
         for (int j = 0; j < 2; ++j)
@@ -172,13 +181,14 @@ int tops_gla_kernel_timing(int enable) {
             return fail(TOPS_GLA_EHIP, "hipEventCreate failed");
     tops::g_kt_made = true;
   }
-  tops::g_kt_on = enable != 0;
   if (enable)
     for (int i = 0; i < tops::KT_COUNT; ++i) tops::g_kt_n[i] = 0;
+  tops::g_kt_on.store(enable != 0);
   return ok();
 }
 
 float tops_gla_kernel_ms(int which) {
+  std::lock_guard<std::mutex> lk(tops::g_kt_mu);
   if (which < 0 || which >= tops::KT_COUNT || tops::g_kt_n[which] == 0) return -1.f;
   const long n = tops::g_kt_n[which];
   const long m = n < tops::KT_RING ? n : tops::KT_RING;
@@ -488,8 +498,9 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     return fail(TOPS_GLA_EINVAL, "h_ws is required when h is NULL");
   hipStream_t st = (hipStream_t)stream;
   // full-head scans for the state recompute; the fused backward for K, V <= 128
+  // the fused backward writes dq, dk, dv and dg with 16- and 8-byte vector stores
   const bool head = use_head(dtype, chunk_size, K, V, false, {q, k, v, g, h0, h, dout, dht,
-                                                              dh0, h_ws, dh_ws});
+                                                              dq, dk, dv, dg, dh0, h_ws, dh_ws});
   const bool head_bwd = head && tops::head_bwd_supported((int)K, (int)V);
   if (!head_bwd && dh_ws == nullptr && B * T > 0)
     return fail(TOPS_GLA_EINVAL, "dh_ws must not be NULL off the fused full-head backward");

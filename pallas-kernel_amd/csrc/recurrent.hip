@@ -524,7 +524,10 @@ hipError_t run_recurrent_fwd(const RecArgs& p, int dtype, int o_dtype, hipStream
   s.R = p.K;
   s.C = p.V;
   s.dir = p.reverse ? 1 : 0;
-  return run_scan(s, dtype, o_dtype, st);
+  ktimer_mark(KT_REC_FWD, false, st);
+  const hipError_t e = run_scan(s, dtype, o_dtype, st);
+  ktimer_mark(KT_REC_FWD, true, st);
+  return e;
 }
 
 hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st) {

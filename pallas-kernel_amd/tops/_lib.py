@@ -79,6 +79,20 @@ _RESTYPE = {"tops_gla_chunk_ws_bytes": ctypes.c_int64, "tops_gla_kernel_ms": cty
 
 EXPORTED = ["tops_gla_last_error", "tops_gla_version"] + list(_SIGS)
 
+
+class ArgumentError(ValueError, AssertionError):
+    """A refused argument. The reference reports these with ``assert`` (AssertionError); the
+    checks here guard device memory accesses, so they are real raises that ``python -O``
+    keeps, and the type is both a ValueError and an AssertionError so that callers written
+    against either keep working."""
+
+
+def require(cond, msg="invalid argument"):
+    """Raise ArgumentError(msg) unless cond."""
+    if not cond:
+        raise ArgumentError(msg)
+
+
 _lib = None
 _lock = threading.Lock()
 
@@ -193,12 +207,13 @@ class SeqLayout:
             self.cu_list = None
             return
         cu = to_list(cu_seqlens)
-        assert self.B == 1, f"cu_seqlens requires B == 1, got B={self.B}"
+        require(self.B == 1, f"cu_seqlens requires B == 1, got B={self.B}")
         # every sequence holds at least one token: the kernels read a sequence's last row, so
-        # an empty one is refused here rather than indexed
-        assert len(cu) >= 2 and cu[0] == 0 and all(b > a for a, b in zip(cu, cu[1:])), \
-            f"cu_seqlens must be strictly increasing from 0 (no empty sequences): {cu}"
-        assert cu[-1] <= self.T, f"cu_seqlens[-1]={cu[-1]} exceeds T={self.T}"
+        # an empty one is refused here rather than indexed (chunk_gla, fused_recurrent_gla and
+        # the simple-GLA entry points leave empty sequences out before they get here)
+        require(len(cu) >= 2 and cu[0] == 0 and all(b > a for a, b in zip(cu, cu[1:])),
+                f"cu_seqlens must be strictly increasing from 0 (no empty sequences): {cu}")
+        require(cu[-1] <= self.T, f"cu_seqlens[-1]={cu[-1]} exceeds T={self.T}")
         self.cu_list = cu
         self.N = len(cu) - 1
         nch = [(b - a + self.C - 1) // self.C for a, b in zip(cu, cu[1:])]
@@ -219,6 +234,37 @@ class SeqLayout:
     def args(self):
         """``cu_seqlens, chunk_offsets, N, NC`` as C arguments."""
         return (ptr(self.cu), ptr(self.chunk_cu), self.N, self.NC)
+
+
+def drop_empty(cu):
+    """Varlen layouts may hold empty sequences: the reference gives one zero chunks
+    (``chunk.py:751-793``) and its recurrence over zero tokens leaves the state as it was
+    (``naive.py:56-80``). The kernels read a sequence's last row, so the host leaves empty
+    sequences out: returns ``(cu without them, indices of the kept sequences)``, or
+    ``(cu, None)`` when every sequence holds a token."""
+    keep = [i for i in range(len(cu) - 1) if cu[i + 1] > cu[i]]
+    if len(keep) == len(cu) - 1:
+        return cu, None
+    return [cu[0]] + [cu[i + 1] for i in keep], keep
+
+
+def scatter_states(part, base, keep, shape, device):
+    """Final states of every sequence from those of the kept ones (``part``, may be None when
+    nothing was kept): an empty sequence's final state is its initial state (``base``, or
+    zeros). Differentiable w.r.t. both."""
+    full = (base.to(torch.float32) if base is not None
+            else torch.zeros(shape, dtype=torch.float32, device=device))
+    if part is None or not keep:
+        return full.clone()
+    idx = torch.tensor(keep, dtype=torch.long, device=device)
+    return full.index_copy(0, idx, part.to(torch.float32))
+
+
+def gather_states(x, keep):
+    """The rows of the kept sequences of a per-sequence state tensor (or None)."""
+    if x is None:
+        return None
+    return x.index_select(0, torch.tensor(keep, dtype=torch.long, device=x.device))
 
 
 def to_list(cu):

@@ -16,6 +16,7 @@ from typing import Any
 import torch
 import torch.nn.functional as F
 
+from .._lib import require
 from ..modules import FusedRMSNormGated, RMSNorm
 from ..modules._norm import GateLogSigmoidFn
 from ..modules.convolution import ShortConvolution
@@ -131,12 +132,12 @@ class GatedLinearAttention(torch.nn.Module):
         self.clamp_min = clamp_min
         self.layer_idx = layer_idx
 
-        assert mode in ["chunk", "fused_recurrent", "fused_chunk"], \
-            f"Not supported mode `{mode}`."
-        assert self.key_dim % num_heads == 0, \
-            f"key dim must be divisible by num_heads of {num_heads}"
-        assert self.value_dim % num_heads == 0, \
-            f"value dim must be divisible by num_heads of {num_heads}"
+        require(mode in ["chunk", "fused_recurrent", "fused_chunk"],
+                f"Not supported mode `{mode}`.")
+        require(self.key_dim % num_heads == 0,
+                f"key dim must be divisible by num_heads of {num_heads}")
+        require(self.value_dim % num_heads == 0,
+                f"value dim must be divisible by num_heads of {num_heads}")
         self.head_k_dim = self.key_dim // num_heads
         self.head_v_dim = self.value_dim // num_heads
 
@@ -171,8 +172,8 @@ class GatedLinearAttention(torch.nn.Module):
                 use_cache=False, output_attentions=False, **kwargs):
         """Reference: ``GatedLinearAttention.__call__``, ``tops/layers/gla.py:224-345``."""
         if attention_mask is not None:
-            assert attention_mask.dim() == 2, \
-                "Expected attention_mask as a 0-1 matrix with shape [batch_size, seq_len]."
+            require(attention_mask.dim() == 2,
+                    "Expected attention_mask as a 0-1 matrix with shape [batch_size, seq_len].")
         batch_size, q_len, _ = hidden_states.shape
         mode = "fused_recurrent" if q_len <= 64 else self.mode
 

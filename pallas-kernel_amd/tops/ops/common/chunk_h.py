@@ -14,7 +14,7 @@ from __future__ import annotations
 import torch
 
 from ... import _lib
-from ..._lib import SeqLayout, call, check_device, dtype_code, ptr, stream_of
+from ..._lib import SeqLayout, call, check_device, dtype_code, ptr, require, stream_of
 
 __all__ = ["chunk_fwd_h_kernel", "chunk_fwd_h_ref", "chunk_bwd_dh_kernel", "chunk_bwd_dh_ref"]
 
@@ -39,10 +39,10 @@ def _gate_cumsum(like, g, g_gamma, gk, C, cu):
 
 
 def _check(T, C, cu):
-    assert T % C == 0, "T mod chunk_size must equal to 0."
+    require(T % C == 0, "T mod chunk_size must equal to 0.")
     if cu is not None:
-        assert all(c % C == 0 for c in _lib.to_list(cu)), \
-            "cu_seqlens must be multiples of chunk_size"
+        require(all(c % C == 0 for c in _lib.to_list(cu)),
+                "cu_seqlens must be multiples of chunk_size")
 
 
 def _kernel_chunk(C):
@@ -81,7 +81,7 @@ def _fwd(k, v, gk, h0, output_final_state, cu, C, states_in_fp32):
     seq = SeqLayout(B, T, C, cu, dev)
     N = seq.N
     if h0 is not None:
-        assert tuple(h0.shape) == (N, H, K, V), f"Expected h0 shape {(N, H, K, V)}"
+        require(tuple(h0.shape) == (N, H, K, V), f"Expected h0 shape {(N, H, K, V)}")
     h = torch.empty(B, seq.NC // B, H, K, V, dtype=cdt, device=dev)
     ht = torch.empty(N, H, K, V, dtype=torch.float32, device=dev)
     call("tops_gla_chunk_fwd_h", ptr(kk), ptr(vv), ptr(gg), 1,
@@ -103,7 +103,7 @@ def _bwd(q, gk, do, dht, scale, cu, C, states_in_fp32, want_dh0):
     seq = SeqLayout(B, T, C, cu, dev)
     N = seq.N
     if dht is not None:
-        assert tuple(dht.shape) == (N, H, K, V), f"Expected dht shape {(N, H, K, V)}"
+        require(tuple(dht.shape) == (N, H, K, V), f"Expected dht shape {(N, H, K, V)}")
     dh = torch.empty(B, seq.NC // B, H, K, V, dtype=cdt, device=dev)
     dh0 = torch.empty(N, H, K, V, dtype=torch.float32, device=dev) if want_dh0 else None
     call("tops_gla_chunk_bwd_dh", ptr(qq), ptr(gg), 1, ptr(dd),
@@ -120,10 +120,10 @@ def chunk_fwd_h_kernel(k, v, *, g=None, g_gamma=None, gk=None, gv=None, h0=None,
     float32) and ht float32 ``[N, H, K, V]`` or None. ``interpret`` is accepted for API
     parity."""
     del interpret
-    assert gv is None, "gv is not supported by chunk_fwd_h"
+    require(gv is None, "gv is not supported by chunk_fwd_h")
     C = chunk_size
     S = C if split_size is None else split_size
-    assert S % C == 0, f"The `split_size` (got {S}) must be a multiple of `chunk_size` {C}"
+    require(S % C == 0, f"The `split_size` (got {S}) must be a multiple of `chunk_size` {C}")
     _check(k.shape[1], S, cu_seqlens)
     KC = _kernel_chunk(C)
     gc = _rechunk_cumsum(_gate_cumsum(k, g, g_gamma, gk, C, cu_seqlens), C, KC, cu_seqlens)
@@ -136,7 +136,7 @@ def chunk_fwd_h_ref(k, v, g=None, g_gamma=None, gk=None, gv=None, h0=None,
                     cu_seqlens_cpu=None, chunk_size=64):
     """Reference: ``tops/ops/common/chunk_h.py:277-396`` (same results on the HIP scan).
     Returns ``(h [B, NT, H, K, V], ht [N, H, K, V] float32 or None)``."""
-    assert gv is None, "gv is not supported by chunk_fwd_h"
+    require(gv is None, "gv is not supported by chunk_fwd_h")
     cu = cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens
     C = chunk_size
     _check(k.shape[1], C, cu)
@@ -157,7 +157,7 @@ def chunk_bwd_dh_kernel(q, k, v, g=None, g_gamma=None, gk=None, do=None, dht=Non
     del k, v, interpret
     C = chunk_size
     S = C if split_size is None else split_size
-    assert S % C == 0, f"The `split_size` (got {S}) must be a multiple of `chunk_size` {C}"
+    require(S % C == 0, f"The `split_size` (got {S}) must be a multiple of `chunk_size` {C}")
     _check(q.shape[1], S, cu_seqlens)
     KC = _kernel_chunk(C)
     gc = _rechunk_cumsum(_gate_cumsum(q, g, g_gamma, gk, C, cu_seqlens), C, KC, cu_seqlens)

@@ -18,7 +18,7 @@ import math
 import torch
 
 from ... import _lib
-from ..._lib import SeqLayout, call, check_device, dtype_code, ptr, stream_of
+from ..._lib import SeqLayout, call, check_device, dtype_code, ptr, require, stream_of
 from ...utils import pad_to_multiple
 
 __all__ = [
@@ -50,7 +50,7 @@ def _kernel_chunk(chunk_size: int) -> int:
     the others.
     """
     c = int(chunk_size)
-    assert c > 0 and c & (c - 1) == 0, "chunk_size must be power of 2"
+    require(c > 0 and c & (c - 1) == 0, "chunk_size must be power of 2")
     return 64
 
 
@@ -76,6 +76,14 @@ def _full_head(K, V, C, dtype, backward, *tensors):
     return _lib.full_head(K, V, C, dtype, backward)
 
 
+def _out_like(x, cu_list):
+    """Output buffer shaped like x; tokens after the last sequence (cu_seqlens[-1] < T) belong
+    to no sequence and stay zero, as in the reference's varlen outputs (``naive.py:52``)."""
+    if cu_list is not None and cu_list[-1] < x.shape[1]:
+        return torch.zeros_like(x)
+    return torch.empty_like(x)
+
+
 def _default_scale(scale, K):
     return K ** -0.5 if scale is None else float(scale)
 
@@ -84,16 +92,18 @@ def _shape_check(q, k=None, v=None, g=None, h0=None, N=None, name="initial_state
     """Shape consistency the kernels rely on (they index every tensor with q's B, T, H)."""
     B, T, H, K = q.shape
     if k is not None:
-        assert tuple(k.shape) == (B, T, H, K), f"Expected k shape {(B, T, H, K)}, got {tuple(k.shape)}"
+        require(tuple(k.shape) == (B, T, H, K),
+                f"Expected k shape {(B, T, H, K)}, got {tuple(k.shape)}")
     if g is not None:
-        assert tuple(g.shape) == (B, T, H, K), f"Expected g shape {(B, T, H, K)}, got {tuple(g.shape)}"
+        require(tuple(g.shape) == (B, T, H, K),
+                f"Expected g shape {(B, T, H, K)}, got {tuple(g.shape)}")
     if v is not None:
-        assert v.dim() == 4 and tuple(v.shape[:3]) == (B, T, H), \
-            f"Expected v shape {(B, T, H)} + (V,), got {tuple(v.shape)}"
+        require(v.dim() == 4 and tuple(v.shape[:3]) == (B, T, H),
+                f"Expected v shape {(B, T, H)} + (V,), got {tuple(v.shape)}")
     if h0 is not None:
         V = v.shape[-1] if v is not None else h0.shape[-1]
-        assert tuple(h0.shape) == (N, H, K, V), \
-            f"Expected {name} shape {(N, H, K, V)}, got {tuple(h0.shape)}"
+        require(tuple(h0.shape) == (N, H, K, V),
+                f"Expected {name} shape {(N, H, K, V)}, got {tuple(h0.shape)}")
 
 
 def _gates(g, g_gamma, q):
@@ -133,7 +143,7 @@ class _ChunkGLAFunction(torch.autograd.Function):
         dev = check_device(q, k, v, g, h0)
         seq = SeqLayout(B, T, chunk, cu_list, dev)
         dt = dtype_code(q.dtype)
-        o = torch.empty_like(v)
+        o = _out_like(v, cu_list)
         ht = (torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev)
               if output_final_state else None)
         # the states are the backward's residual: not kept when no gradient is wanted (the
@@ -161,10 +171,11 @@ class _ChunkGLAFunction(torch.autograd.Function):
         seq = SeqLayout(B, T, chunk, cu_list, dev)
         do = torch.zeros_like(v) if do is None else _c(do, v.dtype)
         dht = None if dht is None else _c(dht, torch.float32)
-        dq, dk, dv, dg = (torch.empty_like(x) for x in (q, k, v, g))
+        dq, dk, dv, dg = (_out_like(x, cu_list) for x in (q, k, v, g))
         need_dh0 = h0 is not None and ctx.needs_input_grad[4]
         dh0 = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if need_dh0 else None
-        dh_ws = (None if _full_head(K, V, chunk, q.dtype, True, q, k, v, g, h0, h_ws, do, dht)
+        dh_ws = (None if _full_head(K, V, chunk, q.dtype, True, q, k, v, g, h0, h_ws, do, dht,
+                                    dq, dk, dv, dg, dh0)
                  else torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev))
         ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list is not None, q.dtype, dev)
         call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(h_ws), ptr(do),
@@ -187,7 +198,7 @@ class _ScalarGateGLAFunction(torch.autograd.Function):
         dev = check_device(q, k, v, gs, h0)
         seq = SeqLayout(B, T, C, cu_list, dev)
         ts = 0 if gs.dim() == 1 else H
-        o = torch.empty_like(v)
+        o = _out_like(v, cu_list)
         ht = (torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev)
               if output_final_state else None)
         keep = any(ctx.needs_input_grad[:5])
@@ -212,9 +223,9 @@ class _ScalarGateGLAFunction(torch.autograd.Function):
         ts = 0 if gs.dim() == 1 else H
         do = torch.zeros_like(v) if do is None else _c(do, v.dtype)
         dht = None if dht is None else _c(dht, torch.float32)
-        dq, dk, dv = (torch.empty_like(x) for x in (q, k, v))
+        dq, dk, dv = (_out_like(x, cu_list) for x in (q, k, v))
         want_dg = ctx.needs_input_grad[3]
-        dg = torch.empty_like(q) if want_dg else None
+        dg = _out_like(q, cu_list) if want_dg else None
         need_dh0 = h0 is not None and ctx.needs_input_grad[4]
         dh0 = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if need_dh0 else None
         ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list is not None, q.dtype, dev)
@@ -240,6 +251,16 @@ def scalar_gate_gla(q, k, v, gs, initial_state, scale, output_final_state, cu_li
     B, T, H, K = q.shape
     V = v.shape[-1]
     cdt = _compute_dtype(q, k, v)
+    if cu_list is not None:
+        cu_kept, keep = _lib.drop_empty(cu_list)
+        if keep is not None:   # empty sequences: run the others, keep their initial states
+            o, ht = (torch.zeros(v.shape, dtype=cdt, device=v.device), None) if not keep else \
+                scalar_gate_gla(q, k, v, gs, _lib.gather_states(initial_state, keep), scale,
+                                output_final_state, cu_kept)
+            if output_final_state:
+                ht = _lib.scatter_states(ht, initial_state, keep, (len(cu_list) - 1, H, K, V),
+                                         v.device)
+            return o, ht
     q, k, v = _c(q, cdt), _c(k, cdt), _c(v, cdt)
     h0 = _c(initial_state, torch.float32)
     grad = torch.is_grad_enabled() and any(
@@ -272,20 +293,31 @@ def chunk_gla(q, k, v, g=None, g_gamma=None, scale=None, initial_state=None,
     dtype = q.dtype
     B, T, H, K = q.shape
     V = v.shape[-1]
-    assert k.shape == (B, T, H, K), f"Expected k shape {(B, T, H, K)}, got {tuple(k.shape)}"
-    assert v.shape[:3] == (B, T, H), f"Expected v shape {(B, T, H, V)}, got {tuple(v.shape)}"
+    require(k.shape == (B, T, H, K), f"Expected k shape {(B, T, H, K)}, got {tuple(k.shape)}")
+    require(v.shape[:3] == (B, T, H), f"Expected v shape {(B, T, H, V)}, got {tuple(v.shape)}")
     cu_list = None if cu_seqlens is None else _lib.to_list(cu_seqlens)
     N = B if cu_list is None else len(cu_list) - 1
     if initial_state is not None:
-        assert initial_state.shape == (N, H, K, V), \
-            f"Expected initial_state shape {(N, H, K, V)}, got {tuple(initial_state.shape)}"
+        require(initial_state.shape == (N, H, K, V),
+                f"Expected initial_state shape {(N, H, K, V)}, got {tuple(initial_state.shape)}")
+    if cu_list is not None:
+        cu_kept, keep = _lib.drop_empty(cu_list)
+        if keep is not None:   # empty sequences: run the others, keep their initial states
+            o, ht = (None, None) if not keep else chunk_gla(
+                q, k, v, g, g_gamma, scale, _lib.gather_states(initial_state, keep),
+                output_final_state, cu_kept, chunk_size)
+            if o is None:
+                o = torch.zeros(v.shape, dtype=dtype, device=v.device)
+            if not output_final_state:
+                return o, None
+            return o, _lib.scatter_states(ht, initial_state, keep, (N, H, K, V), v.device)
     gh = _per_head(g_gamma, H) if g is None and g_gamma is not None else None
     if gh is not None:   # a per-head constant decay: the scalar-gate kernels, gate in float32
         o, ht = scalar_gate_gla(q, k, v, gh, initial_state, _default_scale(scale, K),
                                 output_final_state, cu_list)
         return o.to(dtype), (ht if output_final_state else None)
     g = _gates(g, g_gamma, q)
-    assert g.shape == (B, T, H, K), f"Expected g shape {(B, T, H, K)}, got {tuple(g.shape)}"
+    require(g.shape == (B, T, H, K), f"Expected g shape {(B, T, H, K)}, got {tuple(g.shape)}")
     cdt = _compute_dtype(q, k, v, g)
     o, ht = _ChunkGLAFunction.apply(_c(q, cdt), _c(k, cdt), _c(v, cdt), _c(g, cdt),
                                     _c(initial_state, torch.float32),
@@ -307,7 +339,7 @@ def chunk_local_cumsum_vector(g, chunk_size, reverse=False, scale=None, cu_seqle
     ``cu_seqlens``.
     """
     del chunk_indices
-    assert chunk_size == 2 ** (chunk_size.bit_length() - 1), "chunk_size must be power of 2"
+    require(chunk_size == 2 ** (chunk_size.bit_length() - 1), "chunk_size must be power of 2")
     if head_first:
         B, H, T, S = g.shape
     else:
@@ -333,12 +365,12 @@ chunk_local_cumsum = chunk_local_cumsum_vector
 def chunk_local_cumsum_ref(g, chunk_size, scale=None, reverse=False, cu_seqlens_cpu=None):
     """``chunk_local_cumsum_ref`` (``tops/ops/gla/chunk.py:20-52``): T and cu_seqlens must be
     chunk-aligned, no reverse; computed by the same kernel."""
-    assert reverse is False, "Reverse mode not supported in chunk_local_cumsum"
-    assert g.shape[1] % chunk_size == 0, \
-        "T must be a multiple of chunk_size for chunk_local_cumsum"
+    require(reverse is False, "Reverse mode not supported in chunk_local_cumsum")
+    require(g.shape[1] % chunk_size == 0,
+            "T must be a multiple of chunk_size for chunk_local_cumsum")
     if cu_seqlens_cpu is not None:
-        assert all(c % chunk_size == 0 for c in _lib.to_list(cu_seqlens_cpu)), \
-            "cu_seqlens must be multiples of chunk_size for chunk_local_cumsum"
+        require(all(c % chunk_size == 0 for c in _lib.to_list(cu_seqlens_cpu)),
+                "cu_seqlens must be multiples of chunk_size for chunk_local_cumsum")
     return chunk_local_cumsum_vector(g, chunk_size, scale=scale, cu_seqlens=cu_seqlens_cpu)
 
 
@@ -353,10 +385,10 @@ def chunk_fwd_h(k, v, gk=None, h0=None, output_final_state=False, cu_seqlens_cpu
     B, T, H, K = k.shape
     V = v.shape[-1]
     C = chunk_size
-    assert T % C == 0, "T must be a multiple of chunk_size for chunk_fwd_h"
+    require(T % C == 0, "T must be a multiple of chunk_size for chunk_fwd_h")
     if cu_seqlens_cpu is not None:
-        assert all(c % C == 0 for c in _lib.to_list(cu_seqlens_cpu)), \
-            "cu_seqlens must be multiples of chunk_size for chunk_fwd_h"
+        require(all(c % C == 0 for c in _lib.to_list(cu_seqlens_cpu)),
+                "cu_seqlens must be multiples of chunk_size for chunk_fwd_h")
     if C not in _MFMA_CHUNKS:
         raise NotImplementedError(f"chunk_fwd_h: chunk_size {C} (kernels take 16, 32, 64)")
     N = B if cu_seqlens_cpu is None else len(_lib.to_list(cu_seqlens_cpu)) - 1
@@ -385,7 +417,7 @@ def chunk_gla_fwd_intra_gk(q, k, g, scale, chunk_size=64):
     """
     B, T, H, K = q.shape
     C = chunk_size
-    assert T % C == 0
+    require(T % C == 0)
     if C not in _MFMA_CHUNKS:
         raise NotImplementedError(f"chunk_gla_fwd_intra_gk: chunk_size {C}")
     _shape_check(q, k=k, g=g)
@@ -408,13 +440,14 @@ def chunk_gla_fwd_o_gk(q, v, g, A, h, scale, cu_seqlens=None, chunk_indices=None
     B, T, H, K = q.shape
     V = v.shape[-1]
     C = chunk_size
-    assert T % C == 0
+    require(T % C == 0)
     if C not in _MFMA_CHUNKS:
         raise NotImplementedError(f"chunk_gla_fwd_o_gk: chunk_size {C}")
     _shape_check(q, v=v, g=g)
-    assert tuple(A.shape) == (B, T, H, C), f"Expected A shape {(B, T, H, C)}, got {tuple(A.shape)}"
-    assert tuple(h.shape) == (B, T // C, H, K, V), \
-        f"Expected h shape {(B, T // C, H, K, V)}, got {tuple(h.shape)}"
+    require(tuple(A.shape) == (B, T, H, C),
+            f"Expected A shape {(B, T, H, C)}, got {tuple(A.shape)}")
+    require(tuple(h.shape) == (B, T // C, H, K, V),
+            f"Expected h shape {(B, T // C, H, K, V)}, got {tuple(h.shape)}")
     dev = check_device(q, v, g, A, h)
     cdt = _compute_dtype(q, v) if g.dtype == q.dtype else torch.float32
     gg = g * math.log(2.0) if use_exp2 else g
@@ -486,8 +519,9 @@ def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_fi
         g_cumsum = chunk_local_cumsum_vector(gp, C, cu_seqlens=new_cu)
         g_in, g_is_cumsum = gp, 0
     else:
-        assert tuple(g_cumsum.shape) == tuple(qp.shape), \
-            f"g_cumsum must be in the padded layout {tuple(qp.shape)}, got {tuple(g_cumsum.shape)}"
+        require(tuple(g_cumsum.shape) == tuple(qp.shape),
+                f"g_cumsum must be in the padded layout {tuple(qp.shape)}, got "
+                f"{tuple(g_cumsum.shape)}")
         g_in, g_is_cumsum = _c(g_cumsum, cdt), 1
     dt = dtype_code(cdt)
     st = stream_of(dev)
@@ -533,7 +567,7 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
     qq, kk, vv, gg, dd = (_c(x, cdt) for x in (q, k, v, g, do))
     seq = SeqLayout(B, T, C, cu_list, dev)
     if h is not None:
-        assert h.numel() == seq.NC * H * K * V, "h does not match the chunk layout"
+        require(h.numel() == seq.NC * H * K * V, "h does not match the chunk layout")
         h = _c(h, cdt)
     dq, dk, dv, dg = (torch.empty_like(x) for x in (qq, kk, vv, gg))
     want_dh0 = initial_state is not None or dht is not None
@@ -569,7 +603,7 @@ chunk_gla_bwd_with_pl = chunk_gla_bwd
 
 def _parts_prep(C, T, *xs):
     """float32 contiguous copies; result dtype = the inputs' promoted dtype (jnp's rule)."""
-    assert T % C == 0, f"T ({T}) must be a multiple of chunk_size ({C})"
+    require(T % C == 0, f"T ({T}) must be a multiple of chunk_size ({C})")
     dev = check_device(*xs)
     rdt = xs[0].dtype
     for x in xs[1:]:

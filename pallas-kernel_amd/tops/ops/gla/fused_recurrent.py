@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 
 from ... import _lib
-from ..._lib import SeqLayout, call, check_device, dtype_code, ptr, stream_of
+from ..._lib import SeqLayout, call, check_device, dtype_code, ptr, require, stream_of
 
 __all__ = ["fused_recurrent_gla", "fused_recurrent_gla_fwd", "fused_recurrent_gla_bwd"]
 
@@ -35,6 +35,16 @@ def _run(q, k, v, gk, gv, scale, initial_state, output_final_state, reverse, cu_
     cdt = _compute_dtype(q, k, v, gk, gv)
     c = lambda x: None if x is None else x.to(cdt).contiguous()  # noqa: E731
     odt = torch.float32 if out_dtype == torch.float32 or cdt == torch.float32 else cdt
+    if cu_seqlens is not None:
+        kept, keep = _lib.drop_empty(cu_seqlens)
+        if keep is not None:   # empty sequences: run the others, keep their initial states
+            o, ht = (torch.zeros(B, T, H, V, dtype=odt, device=dev), None) if not keep else \
+                _run(q, k, v, gk, gv, scale, _lib.gather_states(initial_state, keep),
+                     output_final_state, reverse, kept, out_dtype)
+            if output_final_state:
+                ht = _lib.scatter_states(ht, initial_state, keep,
+                                         (len(cu_seqlens) - 1, H, K, V), dev)
+            return o, ht
     seq = SeqLayout(B, T, 1, cu_seqlens, dev)
     o = _out(B, T, H, V, odt, dev, cu_seqlens)
     ht = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if output_final_state \
@@ -58,16 +68,17 @@ def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state
     cu = None if cu_seqlens is None else _lib.to_list(cu_seqlens)
     N = len(cu) - 1 if cu is not None else B
     scale = scale if scale is not None else K ** -0.5
-    assert tuple(k.shape) == (B, T, H, K), f"Expected k shape {(B, T, H, K)}, got {k.shape}"
-    assert tuple(v.shape) == (B, T, H, V), f"Expected v shape {(B, T, H, V)}, got {v.shape}"
-    assert (gk is None) or (tuple(gk.shape) == (B, T, H, K)), \
-        f"Expected gk shape {(B, T, H, K)}, got {gk.shape}"
-    assert (gv is None) or (tuple(gv.shape) == (B, T, H, V)), \
-        f"Expected gv shape {(B, T, H, V)}, got {gv.shape}"
-    assert (initial_state is None) or (tuple(initial_state.shape) == (N, H, K, V)), \
-        f"Expected initial_state shape {(N, H, K, V)}, got {initial_state.shape}"
-    assert (cu_seqlens is None) or (B == 1), \
-        f"Batch size must be 1 when using cu_seqlens, got {B}"
+    require(tuple(k.shape) == (B, T, H, K), f"Expected k shape {(B, T, H, K)}, got {k.shape}")
+    require(tuple(v.shape) == (B, T, H, V), f"Expected v shape {(B, T, H, V)}, got {v.shape}")
+    require((gk is None) or (tuple(gk.shape) == (B, T, H, K)),
+            f"Expected gk shape {(B, T, H, K)}, got {getattr(gk, 'shape', None)}")
+    require((gv is None) or (tuple(gv.shape) == (B, T, H, V)),
+            f"Expected gv shape {(B, T, H, V)}, got {getattr(gv, 'shape', None)}")
+    require((initial_state is None) or (tuple(initial_state.shape) == (N, H, K, V)),
+            f"Expected initial_state shape {(N, H, K, V)}, got "
+            f"{getattr(initial_state, 'shape', None)}")
+    require((cu_seqlens is None) or (B == 1),
+            f"Batch size must be 1 when using cu_seqlens, got {B}")
     return _run(q, k, v, gk, gv, scale, initial_state, output_final_state, reverse, cu,
                 torch.float32)
 
@@ -116,16 +127,17 @@ def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=Non
     V = v.shape[-1]
     cu = None if cu_seqlens is None else _lib.to_list(cu_seqlens)
     N = len(cu) - 1 if cu is not None else B
-    assert tuple(k.shape) == (B, T, H, K), f"Expected k shape {(B, T, H, K)}, got {k.shape}"
-    assert tuple(v.shape) == (B, T, H, V), f"Expected v shape {(B, T, H, V)}, got {v.shape}"
-    assert (gk is None) or (tuple(gk.shape) == (B, T, H, K)), \
-        f"Expected gk shape {(B, T, H, K)}, got {gk.shape}"
-    assert (gv is None) or (tuple(gv.shape) == (B, T, H, V)), \
-        f"Expected gv shape {(B, T, H, V)}, got {gv.shape}"
-    assert (initial_state is None) or (tuple(initial_state.shape) == (N, H, K, V)), \
-        f"Expected initial_state shape {(N, H, K, V)}, got {initial_state.shape}"
-    assert (cu_seqlens is None) or (B == 1), \
-        f"Batch size must be 1 when using cu_seqlens, got {B}"
+    require(tuple(k.shape) == (B, T, H, K), f"Expected k shape {(B, T, H, K)}, got {k.shape}")
+    require(tuple(v.shape) == (B, T, H, V), f"Expected v shape {(B, T, H, V)}, got {v.shape}")
+    require((gk is None) or (tuple(gk.shape) == (B, T, H, K)),
+            f"Expected gk shape {(B, T, H, K)}, got {getattr(gk, 'shape', None)}")
+    require((gv is None) or (tuple(gv.shape) == (B, T, H, V)),
+            f"Expected gv shape {(B, T, H, V)}, got {getattr(gv, 'shape', None)}")
+    require((initial_state is None) or (tuple(initial_state.shape) == (N, H, K, V)),
+            f"Expected initial_state shape {(N, H, K, V)}, got "
+            f"{getattr(initial_state, 'shape', None)}")
+    require((cu_seqlens is None) or (B == 1),
+            f"Batch size must be 1 when using cu_seqlens, got {B}")
     scale = scale if scale is not None else K ** -0.5
     return _FusedRecurrentGLAFunction.apply(q, k, v, gk, gv, initial_state, float(scale),
                                             bool(output_final_state), bool(reverse), cu)
@@ -138,6 +150,22 @@ def _bwd(q, k, v, gk, gv, o, do, dht, scale, initial_state, reverse, cu):
     cdt = _compute_dtype(q, k, v, gk, gv, do)
     c = lambda x: None if x is None else x.to(cdt).contiguous()  # noqa: E731
     f = lambda x: None if x is None else x.to(torch.float32).contiguous()  # noqa: E731
+    if cu is not None:
+        kept, keep = _lib.drop_empty(cu)
+        if keep is not None:   # empty sequences: gradients of the others; dh0 = dht for these
+            if keep:
+                dq, dk, dv, dgk, dgv, dh0 = _bwd(q, k, v, gk, gv, o, do,
+                                                 _lib.gather_states(dht, keep), scale,
+                                                 _lib.gather_states(initial_state, keep),
+                                                 reverse, kept)
+            else:
+                z = lambda D, on=True: (torch.zeros(B, T, H, D, dtype=torch.float32,  # noqa
+                                                    device=dev) if on else None)
+                dq, dk, dv, dgk, dgv, dh0 = (z(K), z(K), z(V), z(K, gk is not None),
+                                             z(V, gv is not None), None)
+            if initial_state is not None:
+                dh0 = _lib.scatter_states(dh0, dht, keep, tuple(initial_state.shape), dev)
+            return dq, dk, dv, dgk, dgv, dh0
     seq = SeqLayout(B, T, 1, cu, dev)
     dq = _out(B, T, H, K, torch.float32, dev, cu)
     dk = _out(B, T, H, K, torch.float32, dev, cu)
@@ -169,13 +197,13 @@ def fused_recurrent_gla_bwd(q, k, v, gk=None, gv=None, o=None, do=None, dht=None
     cu = None if cu_seqlens is None else _lib.to_list(cu_seqlens)
     N = len(cu) - 1 if cu is not None else B
     scale = scale if scale is not None else K ** -0.5
-    assert tuple(k.shape) == (B, T, H, K)
-    assert tuple(v.shape) == (B, T, H, V)
-    assert do is not None and tuple(do.shape) == (B, T, H, V)
-    assert (gk is None) or (tuple(gk.shape) == (B, T, H, K))
-    assert (gv is None) or (tuple(gv.shape) == (B, T, H, V))
-    assert (initial_state is None) or (tuple(initial_state.shape) == (N, H, K, V))
-    assert (dht is None) or (tuple(dht.shape) == (N, H, K, V))
-    assert (cu_seqlens is None) or (B == 1)
-    assert gv is None or o is not None, "o (forward output) is required when gv is used"
+    require(tuple(k.shape) == (B, T, H, K))
+    require(tuple(v.shape) == (B, T, H, V))
+    require(do is not None and tuple(do.shape) == (B, T, H, V))
+    require((gk is None) or (tuple(gk.shape) == (B, T, H, K)))
+    require((gv is None) or (tuple(gv.shape) == (B, T, H, V)))
+    require((initial_state is None) or (tuple(initial_state.shape) == (N, H, K, V)))
+    require((dht is None) or (tuple(dht.shape) == (N, H, K, V)))
+    require((cu_seqlens is None) or (B == 1))
+    require(gv is None or o is not None, "o (forward output) is required when gv is used")
     return _bwd(q, k, v, gk, gv, o, do, dht, scale, initial_state, reverse, cu)

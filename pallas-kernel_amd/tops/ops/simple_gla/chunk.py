@@ -13,6 +13,7 @@ from __future__ import annotations
 import torch
 
 from ... import _lib
+from ..._lib import require
 from ..gla.chunk import chunk_gla_fwd_intra_gk, chunk_gla_fwd_o_gk, scalar_gate_gla
 
 __all__ = [
@@ -62,16 +63,16 @@ def chunk_simple_gla_fwd(q, k, v, *, g=None, g_gamma=None, scale=None, h0=None, 
     into B sequences. Returns (o ``[B, T, H, V]`` in v's dtype, ht float32 or None).
     """
     B, T, H, K, V = *q.shape, v.shape[-1]
-    assert (B, T, H, K) == tuple(k.shape)
-    assert (B, T, H, V) == tuple(v.shape)
-    assert (g is None) or ((B, T, H) == tuple(g.shape))
-    assert (g_gamma is None) or ((H,) == tuple(g_gamma.shape))
-    assert (h0 is None) or ((B, H, K, V) == tuple(h0.shape))
-    assert (cu_seqlens is None) or ((B + 1,) == tuple(cu_seqlens.shape))
-    assert T % chunk_size == 0
+    require((B, T, H, K) == tuple(k.shape))
+    require((B, T, H, V) == tuple(v.shape))
+    require((g is None) or ((B, T, H) == tuple(g.shape)))
+    require((g_gamma is None) or ((H,) == tuple(g_gamma.shape)))
+    require((h0 is None) or ((B, H, K, V) == tuple(h0.shape)))
+    require((cu_seqlens is None) or ((B + 1,) == tuple(cu_seqlens.shape)))
+    require(T % chunk_size == 0)
     cu = None if cu_seqlens is None else _lib.to_list(cu_seqlens)
-    assert (cu is None) or all(c % chunk_size == 0 for c in cu)
-    assert (K % 128 == 0) and (V % 128 == 0)
+    require((cu is None) or all(c % chunk_size == 0 for c in cu))
+    require((K % 128 == 0) and (V % 128 == 0))
     scale = K ** -0.5 if scale is None else float(scale)
     gs = _scalar_gates(g, g_gamma, B, T, H, chunk_size, q.device)
     if cu is not None:   # one row of B * T tokens
@@ -94,9 +95,9 @@ def chunk_simple_gla_bwd(q, k, v, g_gamma, scale, initial_state, do, dht, chunk_
     V = v.shape[-1]
     for name, x, shp in (("q", q, (B, T, H, K)), ("k", k, (B, T, H, K)),
                          ("v", v, (B, T, H, V)), ("do", do, (B, T, H, V))):
-        assert tuple(x.shape) == shp, f"{name}: expected shape {shp}, got {tuple(x.shape)}"
-    assert K % 128 == 0 and V % 128 == 0
-    assert T % chunk_size == 0
+        require(tuple(x.shape) == shp, f"{name}: expected shape {shp}, got {tuple(x.shape)}")
+    require(K % 128 == 0 and V % 128 == 0)
+    require(T % chunk_size == 0)
     with torch.enable_grad():
         qq, kk, vv = (x.detach().requires_grad_(True) for x in (q, k, v))
         h0 = None if initial_state is None else \
@@ -124,7 +125,7 @@ def chunk_simple_gla_fwd_ref(q, k, v, g_gamma, scale, initial_state=None,
     B, T, H, K = q.shape
     C = chunk_size
     gh = g_gamma.reshape(-1)
-    assert gh.shape[0] == H
+    require(gh.shape[0] == H)
     Tp = -(-T // C) * C
     if Tp != T:
         q, k, v = (torch.nn.functional.pad(x, (0, 0, 0, 0, 0, Tp - T)) for x in (q, k, v))
@@ -139,7 +140,7 @@ def chunk_simple_gla_fwd_intra_ref(q, k, g_gamma, scale, chunk_size=64):
     """
     B, T, H, K = q.shape
     C = chunk_size
-    assert T % C == 0
+    require(T % C == 0)
     g = _ramp(g_gamma, B, T, H, K, C, q.device)
     return chunk_gla_fwd_intra_gk(q.to(torch.float32), k.to(torch.float32), g, scale, C)
 
@@ -149,7 +150,7 @@ def chunk_simple_gla_fwd_o_ref(q, v, g_gamma, A, h, scale, chunk_size=64):
     ``tops/ops/simple_gla/chunk.py:73-123``. h ``[B, T / C, H, K, V]``."""
     B, T, H, K = q.shape
     C = chunk_size
-    assert T % C == 0
+    require(T % C == 0)
     g = _ramp(g_gamma, B, T, H, K, C, q.device)
     f32 = torch.float32
     return chunk_gla_fwd_o_gk(q.to(f32), v.to(f32), g, A.to(f32), h.to(f32), scale,

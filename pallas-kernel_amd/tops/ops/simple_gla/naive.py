@@ -6,6 +6,7 @@ from __future__ import annotations
 import torch
 
 from ... import _lib
+from ..._lib import require
 from ..gla.fused_recurrent import fused_recurrent_gla
 
 __all__ = ["simple_gla_naive"]
@@ -25,8 +26,8 @@ def simple_gla_naive(q, k, v, *, g=None, g_gamma=None, scale=None, initial_state
     del chunk_size
     B, T, H, K = q.shape
     V = v.shape[-1]
-    assert (g is None) or (g.dim() == 4)
-    assert (g_gamma is None) or (g_gamma.dim() == 4)
+    require((g is None) or (g.dim() == 4))
+    require((g_gamma is None) or (g_gamma.dim() == 4))
     f32 = torch.float32
     if g is None:
         gate = g_gamma.to(f32).expand(B, T, H, K) if g_gamma is not None else None

@@ -4,6 +4,8 @@ from __future__ import annotations
 
 import torch
 
+from ._lib import require
+
 
 def next_power_of_2(n: int) -> int:
     """Smallest power of two >= n (``tops/utils.py:6-16``)."""
@@ -42,11 +44,11 @@ def assert_shape(x, expected_shape, name="tensor"):
         names = name if isinstance(name, (list, tuple)) and len(name) == len(x) else None
         for i, t in enumerate(x):
             nm = names[i] if names else f"{name}_{i}"
-            assert tuple(t.shape) == tuple(expected_shape), \
-                f"[{nm}] Expected shape {tuple(expected_shape)}, got {tuple(t.shape)}"
+            require(tuple(t.shape) == tuple(expected_shape),
+                    f"[{nm}] Expected shape {tuple(expected_shape)}, got {tuple(t.shape)}")
     else:
-        assert tuple(x.shape) == tuple(expected_shape), \
-            f"[{name}] Expected shape {tuple(expected_shape)}, got {tuple(x.shape)}"
+        require(tuple(x.shape) == tuple(expected_shape),
+                f"[{name}] Expected shape {tuple(expected_shape)}, got {tuple(x.shape)}")
 
 
 def assert_shape_or_none(x, expected_shape, name="tensor"):
@@ -68,8 +70,8 @@ def pad_to_multiple(x: torch.Tensor, multiple, axis, val=0):
         multiple = [multiple]
     if isinstance(axis, int):
         axis = [axis]
-    assert len(multiple) == len(axis), \
-        f"Length of multiple {len(multiple)} must match length of axis {len(axis)}"
+    require(len(multiple) == len(axis),
+            f"Length of multiple {len(multiple)} must match length of axis {len(axis)}")
     pads = [0] * (2 * x.dim())
     for ax, mu in zip(axis, multiple):
         ax = ax % x.dim()

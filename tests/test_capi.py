@@ -212,3 +212,51 @@ def test_seq_layout_refuses_bad_cu_seqlens():
                     ([0, 6, 4, 10], "strictly increasing"), ([0, 4, 12], "exceeds T")):
         with pytest.raises(AssertionError, match=msg):
             _lib.SeqLayout(1, 10, 4, cu, cpu)
+
+
+def test_argument_checks_survive_python_O():
+    """The host checks that keep the kernels in bounds are raises, not asserts: they hold
+    under ``python -O`` (which strips assert statements)."""
+    import subprocess
+    import sys
+
+    code = (
+        "import sys; sys.path[:0] = [%r]\n"
+        "import torch\n"
+        "from tops._lib import SeqLayout, ArgumentError\n"
+        "import tops.ops.gla as G\n"
+        "bad = [lambda: SeqLayout(1, 10, 64, [0, 5, 3], 'cpu'),\n"
+        "       lambda: SeqLayout(1, 10, 64, [0, 5, 12], 'cpu'),\n"
+        "       lambda: SeqLayout(2, 10, 64, [0, 5, 10], 'cpu'),\n"
+        "       lambda: G.chunk_gla(torch.zeros(1, 8, 2, 16), torch.zeros(1, 8, 2, 8),\n"
+        "                           torch.zeros(1, 8, 2, 16), torch.zeros(1, 8, 2, 16)),\n"
+        "       lambda: G.fused_recurrent_gla(torch.zeros(1, 8, 2, 16), torch.zeros(1, 8, 2, 16),\n"
+        "                                     torch.zeros(1, 7, 2, 16))]\n"
+        "n = 0\n"
+        "for f in bad:\n"
+        "    try:\n"
+        "        f()\n"
+        "    except ArgumentError as e:\n"
+        "        assert isinstance(e, ValueError) and isinstance(e, AssertionError)\n"
+        "        n += 1\n"
+        "print(n)\n" % os.path.join(ROOT, "pallas-kernel_amd"))
+    out = subprocess.run([sys.executable, "-O", "-c", code], capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "5", out.stdout + out.stderr
+
+
+def test_empty_sequences_are_left_out_on_the_host():
+    from tops import _lib
+
+    assert _lib.drop_empty([0, 3, 7]) == ([0, 3, 7], None)
+    assert _lib.drop_empty([0, 0, 3, 3, 7, 7]) == ([0, 3, 7], [1, 3])
+    assert _lib.drop_empty([0, 0]) == ([0], [])
+    import torch
+
+    h0 = torch.arange(4.0).reshape(4, 1)
+    part = torch.tensor([[10.0], [30.0]])
+    assert _lib.scatter_states(part, h0, [1, 3], (4, 1), "cpu").flatten().tolist() == \
+        [0.0, 10.0, 2.0, 30.0]
+    assert _lib.scatter_states(None, None, [], (2, 1), "cpu").flatten().tolist() == [0.0, 0.0]
+    assert _lib.gather_states(h0, [1, 3]).flatten().tolist() == [1.0, 3.0]

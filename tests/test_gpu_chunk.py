@@ -70,6 +70,11 @@ FWD_CASES = [
     # single token
     dict(B=1, T=700, H=2, K=128, V=128, seed=809, C=64, h0=True, cu=[0, 130, 131, 500, 700],
          gate_div=8.0),
+    # empty sequences (their final state is their initial state) on the main shape and on the
+    # per-chunk kernels, the latter with tokens after the last sequence (outputs zero there)
+    dict(B=1, T=200, H=2, K=128, V=128, seed=820, C=64, h0=True, cu=[0, 0, 70, 70, 200],
+         gate_div=8.0),
+    dict(B=1, T=60, H=2, K=32, V=64, seed=821, h0=True, cu=[0, 20, 20, 50]),
 ]
 
 
@@ -117,6 +122,24 @@ def test_chunk_gla_fwd_bf16(cfg):
     assert odt == torch.bfloat16
     check("o", o, on, "bf16")
     check("ht", ht, hn, "bf16")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_only_empty_sequences(dtype):
+    """Every sequence empty: nothing runs; o is zero, ht = h0, dh0 = dht, no other
+    gradient."""
+    G = _gla()
+    B, T, H, K, V = 1, 5, 2, 64, 64
+    q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, 830, h0=True, dht=True, N=2,
+                                          dtype=dtype)
+    tq, tk, tv, tg = (to_dev(x, dtype).requires_grad_() for x in (q, k, v, g))
+    th0 = to_dev(s0, "state").requires_grad_()
+    o, ht = G.chunk_gla(tq, tk, tv, tg, initial_state=th0, output_final_state=True,
+                        cu_seqlens=torch.tensor([0, 0, 0]), chunk_size=64)
+    assert o.shape == (B, T, H, V) and not o.float().abs().max().item()
+    assert torch.equal(ht, th0.detach())
+    (ht * to_dev(dht, "state")).sum().backward()
+    assert torch.equal(th0.grad, to_dev(dht, "state"))
 
 
 def test_forward_same_with_and_without_grad():
@@ -188,6 +211,10 @@ BWD_CASES = [
     # varlen on the main shape (full-head kernels): unaligned sequences, one of a single token
     dict(B=1, T=700, H=2, K=128, V=128, seed=819, C=64, h0=True, dht=True,
          cu=[0, 130, 131, 500, 700], gate_div=8.0),
+    # empty sequences: no gradient flows through them, dh0 = dht
+    dict(B=1, T=200, H=2, K=128, V=128, seed=820, C=64, h0=True, dht=True,
+         cu=[0, 0, 70, 70, 200], gate_div=8.0),
+    dict(B=1, T=50, H=2, K=32, V=64, seed=822, h0=True, dht=True, cu=[0, 20, 20, 50, 50]),
 ]
 
 
@@ -411,6 +438,41 @@ def test_segmented_scans_match_sequential(B, T, H):
     names = ["o", "ht", "h", "dq", "dk", "dv", "dg", "dh0"]
     for name, a, b in zip(names, *outs):
         check(name, to_np(b), to_np(a).astype(np.float64), "bf16")
+
+
+def test_chunk_bwd_misaligned_outputs_take_the_per_chunk_path():
+    """Gradient buffers that are not 16-byte aligned (a C caller's offset views) make
+    tops_gla_chunk_bwd leave the fused full-head backward, whose vector stores need the
+    alignment, and give the same gradients through the per-chunk kernels."""
+    from tops import _lib
+    from tops._lib import SeqLayout, call, ptr, stream_of
+
+    B, T, H, K, V, C = 1, 320, 2, 128, 128, 64
+    q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, 841, gate_div=8.0, h0=True, dht=True,
+                                          dtype="bf16")
+    d = lambda x: to_dev(x, "bf16")  # noqa: E731
+    q, k, v, g, do = (d(x) for x in (q, k, v, g, do))
+    h0, dht = to_dev(s0, "state"), to_dev(dht, "state")
+    dev = q.device
+    seq = SeqLayout(B, T, C, None, dev)
+    st = stream_of(dev)
+    o, h = torch.empty_like(v), torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev)
+    ht = torch.empty_like(h0)
+    call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(o), ptr(ht),
+         ptr(h), None, 0, K ** -0.5, B, T, H, K, V, C, *seq.args(), _lib.BF16, st)
+    outs = []
+    for off in (0, 1):   # element offset 1 = 2 bytes: every gradient buffer misaligned
+        bufs = [torch.empty(x.numel() + 8, dtype=x.dtype, device=dev) for x in (q, k, v, g)]
+        dq, dk, dv, dg = (b[off:off + x.numel()].view(x.shape) for b, x in
+                          zip(bufs, (q, k, v, g)))
+        dh0, dh = torch.empty_like(h0), torch.empty_like(h)
+        call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(h), ptr(do),
+             ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None, ptr(dh), None, 0,
+             K ** -0.5, B, T, H, K, V, C, *seq.args(), _lib.BF16, st)
+        torch.cuda.synchronize()
+        outs.append([x.clone() for x in (dq, dk, dv, dg, dh0)])
+    for name, a, b in zip(["dq", "dk", "dv", "dg", "dh0"], *outs):
+        check(name, to_np(b), to_np(a), "bf16")
 
 
 # The backward's parts over given intermediates (reference jnp exports chunk.py:504-743).

@@ -40,6 +40,8 @@ CASES = [
          scale=0.1),
     dict(B=1, T=256, H=2, K=256, V=512, seed=2, h0=True, gate_div=16.0),
     dict(B=1, T=64, H=2, K=200, V=70, seed=3),
+    # empty sequences keep their initial state; tokens after the last sequence give zeros
+    dict(B=1, T=26, H=2, K=16, V=32, seed=122, cu=[0, 0, 7, 7, 23], h0=True),
 ]
 
 
@@ -179,6 +181,9 @@ BWD_CASES = [
     dict(B=1, T=64, H=2, K=256, V=512, seed=3, gate="gk+gv", h0=True, gate_div=16.0),
     dict(B=1, T=40, H=2, K=200, V=70, seed=4, gate="gk+gv", h0=True),
     dict(B=2, T=20, H=1, K=512, V=24, seed=5, dht=True),
+    # empty sequences: dh0 = dht for them, no gradient through their (absent) tokens
+    dict(B=1, T=23, H=2, K=16, V=32, seed=122, cu=[0, 0, 7, 7, 23], h0=True,
+         gate="gk+gv"),
 ]
 
 
