@@ -333,8 +333,9 @@ int64_t tops_gla_short_conv_ws_bytes(int64_t B, int64_t T, int64_t D, int W, int
  * Measurement hook (no counterpart in the reference): with timing enabled, HIP events are
  * recorded on the launch stream around every launch of the fused full-head forward
  * (which = 0) and backward (which = 1) kernels (tops_gla_chunk_fwd / _bwd and the
- * scalar-gate entry points) and of the recurrent forward scan (which = 2,
- * tops_gla_fused_recurrent_fwd). tops_gla_kernel_ms waits for the last such launch and
+ * scalar-gate entry points), of the recurrent forward scan (which = 2,
+ * tops_gla_fused_recurrent_fwd) and of the per-chunk dq / dk / dg kernel (which = 3, the
+ * backward of shapes off the fused full-head backward, e.g. K = 256). tops_gla_kernel_ms waits for the last such launch and
  * returns the average duration in ms of the launches recorded since timing was enabled (the
  * last 256 of them; -1 if there is none).
  * A profiling aid with process-wide state: the first enable creates the host-side event

@@ -10,6 +10,17 @@ autodiff of an independent restatement, finite differences) is recorded in ``gla
 module docstring and exercised by ``tests/test_oracle.py``.
 """
 
+import importlib
+
 from .gla import *  # noqa: F401,F403
-from . import layer  # noqa: F401  (the GLA layer and its modules, float64 torch)
-from . import simple_gla  # noqa: F401  (scalar-gate GLA)
+
+_LAZY = ("layer",        # the GLA layer and its modules, float64 torch
+         "simple_gla")   # scalar-gate GLA
+
+
+def __getattr__(name):
+    """``layer`` (which imports torch) and ``simple_gla`` load on first use, so the numpy
+    part imports without torch (the CPU baseline's worker processes)."""
+    if name in _LAZY:
+        return importlib.import_module(f"{__name__}.{name}")
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")

@@ -629,8 +629,10 @@ static hipError_t launch_bwd(const BwdArgs& p, hipStream_t st, int which) {
     hipError_t e = hipFuncSetAttribute((const void*)chunk_bwd_dqkg_kernel<T, C, VEC>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
     if (e != hipSuccess) return e;
+    ktimer_mark(KT_BWD_DQKG, false, st);
     hipLaunchKernelGGL((chunk_bwd_dqkg_kernel<T, C, VEC>), dim3((unsigned)(nch * KT)),
                        dim3(256), Lay::bytes, st, p);
+    ktimer_mark(KT_BWD_DQKG, true, st);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

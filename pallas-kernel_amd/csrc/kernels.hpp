@@ -262,7 +262,7 @@ hipError_t run_head_bwd(const HeadBwdArgs& p, hipStream_t st);
 
 // Optional HIP-event timing of the fused full-head kernels (a measurement hook): when
 // enabled, an event is recorded on the launch stream right before and after the kernel.
-enum { KT_HEAD_FWD = 0, KT_HEAD_BWD = 1, KT_REC_FWD = 2, KT_COUNT = 3 };
+enum { KT_HEAD_FWD = 0, KT_HEAD_BWD = 1, KT_REC_FWD = 2, KT_BWD_DQKG = 3, KT_COUNT = 4 };
 void ktimer_mark(int which, bool stop, hipStream_t st);
 
 }  // namespace tops
