@@ -143,6 +143,28 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
                        void* stream);
 
 /*
+ * tops_gla_chunk_fwd without a caller workspace. No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Arguments and results are those of tops_gla_chunk_fwd
+ * without seg_ws / seg_ws_bytes; the caller still passes every input and output (and h_ws
+ * where tops_gla_chunk_fwd requires it). The sequence-segment workspace of the full-head
+ * kernels lives in a file-scope device array of 24 MiB per GPU (held by each GPU the
+ * library runs on until the process ends), whose address is taken once per device on the
+ * first call with that device current; a shape whose segment plan needs more returns
+ * TOPS_GLA_EINVAL (the plan never needs more than 17.04 MB). The wide heads' per-chunk
+ * gating workspace is not used. Nothing here calls hipMalloc or hipFree.
+ * Every call on one GPU shares that array: calls that overlap on one GPU (other streams,
+ * other threads) race and must be serialized by the caller. Each call writes every part of
+ * the array it later reads, so nothing needs clearing between calls.
+ */
+int tops_gla_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const void* g,
+                               const float* h0, void* o, float* ht, void* h_ws, float scale,
+                               int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                               int chunk_size, const int32_t* cu_seqlens,
+                               const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                               void* stream);
+
+/*
  * chunk_gla backward: (dq, dk, dv, dg, dh0). `h` are the forward states ([NC, H, K, V]); if
  * NULL they are recomputed into h_ws (then required). dh_ws ([NC, H, K, V], dtype) is
  * required off the fused full-head backward (tops_gla_full_head(..., 1)), which does not use

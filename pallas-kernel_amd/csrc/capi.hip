@@ -478,6 +478,87 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
   return hip_status(tops::run_chunk_fwd_o(p, dtype, st), "chunk_fwd (output)");
 }
 
+// ---------------------------------------------------------------------------
+// tops_gla_chunk_fwd without a caller workspace: the segment workspace lives in one
+// file-scope device array per GPU (`scratch`), shared by every call on that GPU.
+// ---------------------------------------------------------------------------
+namespace {
+
+// The full-head segment plan keeps sequences x heads x V tiles x segments <= 256, so the
+// segment part of the workspace is at most 256 x 128 x 128 x 4 B of states plus 256 x 256 x
+// 4 B of decays (17.04 MB); 24 MiB holds it with room to spare.
+constexpr long kScratchBytes = 24l << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current GPU's copy of `scratch`: hipGetSymbolAddress once per
+// device, with that device current (the array's host-side name is not a device address).
+int scratch_on(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (st != nullptr) {
+    hipDevice_t sd = -1;
+    e = hipStreamGetDevice(st, &sd);
+    if (e != hipSuccess) return hip_status(e, "hipStreamGetDevice");
+    if (sd != dev)
+      return fail(TOPS_GLA_EINVAL, "the stream belongs to device %d, the current device is %d",
+                  (int)sd, dev);
+  }
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(TOPS_GLA_EUNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(TOPS_GLA_EHIP, "hipGetSymbolAddress(scratch) gave NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TOPS_GLA_OK;
+}
+
+}  // namespace
+
+int tops_gla_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const void* g,
+                               const float* h0, void* o, float* ht, void* h_ws, float scale,
+                               int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                               int chunk_size, const int32_t* cu_seqlens,
+                               const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                               void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  if (B <= 0 || T <= 0 || H <= 0)   // nothing to segment: no scratch needed
+    return tops_gla_chunk_fwd(q, k, v, g, h0, o, ht, h_ws, nullptr, 0, scale, B, T, H, K, V,
+                              chunk_size, cu_seqlens, chunk_offsets, N, NC, dtype, stream);
+  long need = 0;
+  if (cu_seqlens == nullptr && K <= 256 &&
+      tops::head_supported(dtype, chunk_size, (int)K, (int)V, false)) {
+    int NS = 1, SL = 0;
+    tops::head_seg_plan((int)B, (int)H, (int)T, chunk_size, false, NS, SL,
+                        tops::head_vtiles((int)K, (int)V));
+    need = tops::head_seg_ws_bytes((int)B, NS, (int)H, (int)K, (int)V);
+  }
+  if (need > kScratchBytes)
+    return fail(TOPS_GLA_EINVAL,
+                "the segment workspace needs %ld bytes, the static scratch holds %ld; call "
+                "tops_gla_chunk_fwd with a workspace",
+                need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    rc = scratch_on((hipStream_t)stream, &ws);
+    if (rc) return rc;
+  }
+  // exactly the segment part: the wide heads' per-chunk gating workspace is not used (every
+  // V tile then gates its chunk itself)
+  return tops_gla_chunk_fwd(q, k, v, g, h0, o, ht, h_ws, ws, need, scale, B, T, H, K, V,
+                            chunk_size, cu_seqlens, chunk_offsets, N, NC, dtype, stream);
+}
+
 int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
                        const float* h0, const void* h, const void* dout, const float* dht,
                        void* dq, void* dk, void* dv, void* dg, float* dh0, void* h_ws,

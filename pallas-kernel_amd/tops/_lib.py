@@ -39,6 +39,8 @@ _SIGS = {
     "tops_gla_chunk_ws_bytes": [_I64, _I64, _I64, _I64, _I64, _I, _I, _I],
     "tops_gla_chunk_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _F, _I64, _I64, _I64, _I64,
                            _I64, _I, _P, _P, _I64, _I64, _I, _P],
+    "tops_gla_chunk_fwd_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64,
+                                   _I64, _I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_chunk_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                            _F, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_chunk_bwd_dqkg": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64,

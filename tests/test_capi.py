@@ -32,7 +32,7 @@ def _declared():
 
 def test_header_lists_entry_points():
     decl = _declared()
-    assert len(decl) == 30, decl
+    assert len(decl) == 31, decl
     assert set(decl) == set(_lib.EXPORTED)
 
 
@@ -260,3 +260,14 @@ def test_empty_sequences_are_left_out_on_the_host():
         [0.0, 10.0, 2.0, 30.0]
     assert _lib.scatter_states(None, None, [], (2, 1), "cpu").flatten().tolist() == [0.0, 0.0]
     assert _lib.gather_states(h0, [1, 3]).flatten().tolist() == [1.0, 3.0]
+
+
+def test_noalloc_forward_validates_on_the_host():
+    """tops_gla_chunk_fwd_noalloc refuses bad arguments before touching the GPU (no scratch
+    address is taken for them)."""
+    rc, msg = _rc("tops_gla_chunk_fwd_noalloc", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL,
+                  1.0, 1, 64, 1, 64, 64, 64, NULL, NULL, 1, 1, 7, NULL)
+    assert rc == 1 and "dtype" in msg
+    rc, msg = _rc("tops_gla_chunk_fwd_noalloc", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL,
+                  1.0, 1, 64, 1, 64, 64, 64, NULL, NULL, 1, 1, 1, NULL)
+    assert rc == 1 and "NULL" in msg
