@@ -42,6 +42,12 @@ CASES = [
     dict(B=1, T=64, H=2, K=200, V=70, seed=3),
     # empty sequences keep their initial state; tokens after the last sequence give zeros
     dict(B=1, T=26, H=2, K=16, V=32, seed=122, cu=[0, 0, 7, 7, 23], h0=True),
+    # strong gates: 16-step decays beyond e^-60 take the direct (unrescaled) stages, some
+    # stages only (gate_mul 5: about -64 per 16 steps) or all of them (gate_mul 12)
+    dict(B=1, T=100, H=2, K=32, V=64, seed=140, gate_mul=12.0, h0=True),
+    dict(B=1, T=200, H=2, K=64, V=64, seed=141, gate_mul=5.0, h0=True),
+    dict(B=1, T=100, H=2, K=32, V=64, seed=142, gate="gv", gate_mul=8.0, h0=True),
+    dict(B=1, T=100, H=2, K=32, V=64, seed=143, gate_mul=8.0, h0=True, reverse=True),
 ]
 
 
@@ -62,8 +68,9 @@ def _inputs(cfg, dtype):
     div = cfg.get("gate_div", 1.0)
     q, k = r.standard_normal((2, B, T, H, K))
     v = r.standard_normal((B, T, H, V))
-    gk = logsigmoid(r.standard_normal((B, T, H, K))) / div if "gk" in gate else None
-    gv = logsigmoid(r.standard_normal((B, T, H, V))) / div if "gv" in gate else None
+    mul = cfg.get("gate_mul", 1.0)
+    gk = logsigmoid(r.standard_normal((B, T, H, K))) / div * mul if "gk" in gate else None
+    gv = logsigmoid(r.standard_normal((B, T, H, V))) / div * mul if "gv" in gate else None
     cu = cfg.get("cu")
     N = len(cu) - 1 if cu else B
     s0 = r.standard_normal((N, H, K, V)) if cfg.get("h0") else None
@@ -184,6 +191,10 @@ BWD_CASES = [
     # empty sequences: dh0 = dht for them, no gradient through their (absent) tokens
     dict(B=1, T=23, H=2, K=16, V=32, seed=122, cu=[0, 0, 7, 7, 23], h0=True,
          gate="gk+gv"),
+    # strong gates: direct stages in every scan (all or some of the stages)
+    dict(B=1, T=100, H=2, K=32, V=64, seed=150, gate_mul=12.0, h0=True, dht=True),
+    dict(B=1, T=200, H=2, K=64, V=64, seed=151, gate_mul=5.0, h0=True, dht=True),
+    dict(B=1, T=100, H=2, K=32, V=64, seed=152, gate="gv", gate_mul=8.0, h0=True, dht=True),
 ]
 
 
