@@ -120,28 +120,62 @@ bool use_head(int dtype, int chunk, int64_t K, int64_t V, bool g_is_cumsum,
   return true;
 }
 
-// Sequence segmentation of the full-head kernels when the caller's workspace holds it
-// (state part first, then the decays); otherwise NS = 1.
-void seg_setup(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void* ws,
-               int64_t ws_bytes, int& NS, int& SL, float*& st, float*& gm,
-               void** gate = nullptr) {
-  tops::head_seg_plan(si.N, (int)H, si.T, si.C, si.cu != nullptr, NS, SL,
-                      tops::head_vtiles((int)K, (int)V));
-  const long need = tops::head_seg_ws_bytes(si.N, NS, (int)H, (int)K, (int)V);
-  st = gm = nullptr;
-  if (gate) *gate = nullptr;
+// Workspace of the full-head paths of tops_gla_chunk_fwd / _bwd, each part 256-byte aligned:
+//   [segment states, decays (NS > 1)] [gate-range flags, int32 per block]
+//   [wide heads' per-chunk gating (fixed length)] [fallback final states f32 [N, H, K, V]]
+// A workspace that ends early leaves the later parts out: no flags (no gate-range fallback),
+// no gating workspace (every V tile's block gates its chunks), no backward fallback.
+long align256(long x) { return (x + 255) / 256 * 256; }
+
+struct WsLayout {
+  int NS = 1, SL = 0, VT = 1;
+  long seg = 0, flags = 0, gate = 0, ht = 0;   // bytes of each part
+  long off_flags = 0, off_gate = 0, off_ht = 0, total = 0;
+};
+
+WsLayout ws_layout(int N, int T, int H, int K, int V, int C, bool varlen) {
+  WsLayout w;
+  w.VT = tops::head_vtiles(K, V);
+  tops::head_seg_plan(N, H, T, C, varlen, w.NS, w.SL, w.VT);
+  w.seg = align256(tops::head_seg_ws_bytes(N, w.NS, H, K, V));
+  w.flags = align256((long)N * w.NS * H * w.VT * 4);
+  w.gate = varlen ? 0 : align256(tops::head_gate_ws_bytes(N, T, H, K, V));
+  w.ht = tops::head_bwd_supported(K, V) ? align256((long)N * H * K * V * 4) : 0;
+  w.off_flags = w.seg;
+  w.off_gate = w.off_flags + w.flags;
+  w.off_ht = w.off_gate + w.gate;
+  w.total = w.off_ht + w.ht;
+  return w;
+}
+
+// The full-head kernels' workspace pointers from the caller's workspace (NULL parts are
+// absent; NS = 1 without the segment part).
+struct WsParts {
+  int NS = 1, SL = 0, VT = 1;
+  float *st = nullptr, *gm = nullptr;
+  void* gate = nullptr;
+  int* flags = nullptr;
+  float* ht = nullptr;
+};
+
+WsParts ws_parts(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void* ws,
+                 int64_t ws_bytes) {
+  const WsLayout w = ws_layout(si.N, si.T, (int)H, (int)K, (int)V, si.C, si.cu != nullptr);
+  WsParts p;
+  p.VT = w.VT;
   const bool usable = ws != nullptr && ((uintptr_t)ws & 255u) == 0;
-  if (NS <= 1 || !usable || ws_bytes < need) {
-    NS = 1;
-    SL = 0;
-  } else {
-    st = (float*)ws;
-    gm = (float*)((char*)ws + (long)si.N * NS * H * K * V * 4);
+  if (!usable) return p;
+  char* b = (char*)ws;
+  if (w.NS > 1 && ws_bytes >= w.seg) {
+    p.NS = w.NS;
+    p.SL = w.SL;
+    p.st = (float*)b;
+    p.gm = (float*)(b + (long)si.N * w.NS * H * K * V * 4);
   }
-  // the wide forward's per-chunk gating workspace follows the segment part
-  const long gbytes = si.cu ? 0 : tops::head_gate_ws_bytes(si.N, si.T, (int)H, (int)K, (int)V);
-  const long seg = NS > 1 ? need : 0;
-  if (gate && gbytes > 0 && usable && ws_bytes >= seg + gbytes) *gate = (char*)ws + seg;
+  if (ws_bytes >= w.off_gate) p.flags = (int*)(b + w.off_flags);
+  if (w.gate > 0 && ws_bytes >= w.off_ht) p.gate = b + w.off_gate;
+  if (w.ht > 0 && ws_bytes >= w.total) p.ht = (float*)(b + w.off_ht);
+  return p;
 }
 
 }  // namespace
@@ -217,15 +251,11 @@ int tops_gla_full_head(int64_t K, int64_t V, int chunk_size, int dtype, int back
 }
 
 int64_t tops_gla_chunk_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
-                                int chunk_size, int varlen, int dtype) {
+                                int chunk_size, int64_t N, int varlen, int dtype) {
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || K > 256 || V > (1 << 20)) return 0;
+  if (N <= 0 || N > kMaxInt || (!varlen && N != B)) return 0;
   if (!tops::head_supported(dtype, chunk_size, (int)K, (int)V, false)) return 0;
-  int NS, SL;
-  tops::head_seg_plan((int)B, (int)H, (int)T, chunk_size, varlen != 0, NS, SL,
-                      tops::head_vtiles((int)K, (int)V));
-  const long seg = NS > 1 ? tops::head_seg_ws_bytes((int)B, NS, (int)H, (int)K, (int)V) : 0;
-  const long gate = varlen ? 0 : tops::head_gate_ws_bytes((int)B, (int)T, (int)H, (int)K, (int)V);
-  return seg + gate;
+  return ws_layout((int)N, (int)T, (int)H, (int)K, (int)V, chunk_size, varlen != 0).total;
 }
 
 int tops_gla_chunk_local_cumsum(const void* g, void* out, int64_t B, int64_t T, int64_t H,
@@ -244,7 +274,7 @@ int tops_gla_chunk_local_cumsum(const void* g, void* out, int64_t B, int64_t T, 
   if (rc) return rc;
   if (NC * H > 2147483647LL || (S + 255) / 256 > 65535)
     return fail(TOPS_GLA_EUNSUPPORTED, "grid too large");
-  tops::CumsumArgs p;
+  tops::CumsumArgs p = {};
   p.g = g;
   p.out = out;
   p.H = (int)H;
@@ -280,7 +310,13 @@ int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_c
     s.s_init = h0;
     s.s_all = h;
     s.s_final = ht;
-    seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, s.NS, s.SL, s.seg_state, s.seg_gam);
+    {
+      const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+      s.NS = w.NS;
+      s.SL = w.SL;
+      s.seg_state = w.st;
+      s.seg_gam = w.gm;
+    }
     s.scale = 1.f;
     s.H = (int)H;
     s.K = (int)K;
@@ -288,7 +324,7 @@ int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_c
     s.si = si;
     return hip_status(tops::run_head_scan(s, false, (hipStream_t)stream), "chunk_fwd_h");
   }
-  tops::ScanArgs p;
+  tops::ScanArgs p = {};
   p.a = k;
   p.b = v;
   p.g = g;
@@ -326,7 +362,13 @@ int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const v
     s.s_init = dht;
     s.s_all = dh;
     s.s_final = dh0;
-    seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, s.NS, s.SL, s.seg_state, s.seg_gam);
+    {
+      const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+      s.NS = w.NS;
+      s.SL = w.SL;
+      s.seg_state = w.st;
+      s.seg_gam = w.gm;
+    }
     s.scale = scale;
     s.H = (int)H;
     s.K = (int)K;
@@ -334,7 +376,7 @@ int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const v
     s.si = si;
     return hip_status(tops::run_head_scan(s, true, (hipStream_t)stream), "chunk_bwd_dh");
   }
-  tops::ScanArgs p;
+  tops::ScanArgs p = {};
   p.a = q;
   p.b = dout;
   p.g = g;
@@ -369,7 +411,7 @@ int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void
   if (B * T > 0 && o != nullptr && v == nullptr)
     return fail(TOPS_GLA_EINVAL, "v is required for o");
   if (o == nullptr && A_out == nullptr) return ok();
-  tops::FwdOArgs p;
+  tops::FwdOArgs p = {};
   p.q = q;
   p.k = k;
   p.v = v;
@@ -415,17 +457,43 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
     f.o = o;
     f.h_out = h_ws;
     f.ht = ht;
-    seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, f.NS, f.SL, f.seg_state, f.seg_gam,
-              &f.gate_ws);
+    const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+    f.NS = w.NS;
+    f.SL = w.SL;
+    f.seg_state = w.st;
+    f.seg_gam = w.gm;
+    f.gate_ws = w.gate;
+    // the gate-range check runs where the forward gates its own chunks (wide heads that
+    // stream the gating workspace are left out)
+    f.flags = (K > 128 && w.gate) ? nullptr : w.flags;
     f.scale = scale;
     f.H = (int)H;
     f.K = (int)K;
     f.V = (int)V;
     f.si = si;
-    return hip_status(tops::run_head_fwd(f, st), "chunk_fwd (full-head)");
+    rc = hip_status(tops::run_head_fwd(f, st), "chunk_fwd (full-head)");
+    if (rc || f.flags == nullptr) return rc;
+    // sequences and heads with a chunk beyond the factoring's range: the recurrent forward
+    // (exact for any decay) rewrites their o and final state; the other blocks return at once
+    tops::RecArgs r = {};
+    r.q = q;
+    r.k = k;
+    r.v = v;
+    r.gk = g;
+    r.h0 = h0;
+    r.o = o;
+    r.ht = ht;
+    r.scale = scale;
+    r.H = (int)H;
+    r.K = (int)K;
+    r.V = (int)V;
+    r.si = si;
+    r.flags = {f.flags, w.NS, w.VT};
+    return hip_status(tops::run_recurrent_fwd(r, dtype, dtype, st),
+                      "chunk_fwd (gate-range fallback)");
   }
   if (tops::fused_fwd_supported(dtype, chunk_size, (int)K)) {
-    tops::FusedFwdArgs f;
+    tops::FusedFwdArgs f = {};
     f.q = q;
     f.k = k;
     f.v = v;
@@ -444,7 +512,7 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
     f.si = si;
     return hip_status(tops::run_chunk_fwd_fused(f, dtype, st), "chunk_fwd (fused)");
   }
-  tops::ScanArgs s;
+  tops::ScanArgs s = {};
   s.a = k;
   s.b = v;
   s.g = g;
@@ -460,7 +528,7 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
   s.si = si;
   rc = hip_status(tops::run_state_scan(s, false, dtype, st), "chunk_fwd (state scan)");
   if (rc) return rc;
-  tops::FwdOArgs p;
+  tops::FwdOArgs p = {};
   p.q = q;
   p.k = k;
   p.v = v;
@@ -532,17 +600,19 @@ int tops_gla_chunk_fwd_noalloc(const void* q, const void* k, const void* v, cons
                                void* stream) {
   int rc = check_mfma_common(K, V, chunk_size, dtype);
   if (rc) return rc;
+  // the arguments are checked before the scratch's address is taken
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || g == nullptr ||
+                    o == nullptr))
+    return fail(TOPS_GLA_EINVAL, "q, k, v, g and o must not be NULL");
   if (B <= 0 || T <= 0 || H <= 0)   // nothing to segment: no scratch needed
     return tops_gla_chunk_fwd(q, k, v, g, h0, o, ht, h_ws, nullptr, 0, scale, B, T, H, K, V,
                               chunk_size, cu_seqlens, chunk_offsets, N, NC, dtype, stream);
-  long need = 0;
-  if (cu_seqlens == nullptr && K <= 256 &&
-      tops::head_supported(dtype, chunk_size, (int)K, (int)V, false)) {
-    int NS = 1, SL = 0;
-    tops::head_seg_plan((int)B, (int)H, (int)T, chunk_size, false, NS, SL,
-                        tops::head_vtiles((int)K, (int)V));
-    need = tops::head_seg_ws_bytes((int)B, NS, (int)H, (int)K, (int)V);
-  }
+  long need = 0;   // the segment part and the gate-range flags
+  if (K <= 256 && tops::head_supported(dtype, chunk_size, (int)K, (int)V, false))
+    need = ws_layout(si.N, si.T, (int)H, (int)K, (int)V, chunk_size, si.cu != nullptr).off_gate;
   if (need > kScratchBytes)
     return fail(TOPS_GLA_EINVAL,
                 "the segment workspace needs %ld bytes, the static scratch holds %ld; call "
@@ -588,7 +658,15 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   int NS = 1, SL = 0;
   float *seg_st = nullptr, *seg_gm = nullptr;
   void* gate = nullptr;   // per-chunk gating of wide heads (when the workspace holds it)
-  if (head) seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, NS, SL, seg_st, seg_gm, &gate);
+  WsParts wp;
+  if (head) {
+    wp = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+    NS = wp.NS;
+    SL = wp.SL;
+    seg_st = wp.st;
+    seg_gm = wp.gm;
+    gate = wp.gate;
+  }
   if (head_bwd) gate = nullptr;
   if (gate) {   // gated q, k, A and the column factors once per (chunk, head): the scans and
                 // the dv kernel stream them
@@ -633,7 +711,7 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     h = h_ws;
   }
   if (h == nullptr) {
-    tops::ScanArgs s;
+    tops::ScanArgs s = {};
     s.a = k;
     s.b = v;
     s.g = g;
@@ -675,13 +753,41 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     b.K = (int)K;
     b.V = (int)V;
     b.si = si;
-    return hip_status(tops::run_head_bwd(b, st), "chunk_bwd (full-head)");
+    // gate-range check (and fallback) when the workspace holds the flags and, with dht, the
+    // fallback's final-state part
+    b.flags = (dht == nullptr || wp.ht != nullptr) ? wp.flags : nullptr;
+    rc = hip_status(tops::run_head_bwd(b, st), "chunk_bwd (full-head)");
+    if (rc || b.flags == nullptr) return rc;
+    // sequences and heads with a chunk beyond the factoring's range: the recurrent backward
+    // (exact for any decay) rewrites their dq, dk, dv, dg and dh0
+    tops::RecBwdArgs r = {};
+    r.q = q;
+    r.k = k;
+    r.v = v;
+    r.gk = g;
+    r.dout = dout;
+    r.h0 = h0;
+    r.dht = dht;
+    r.dq = dq;
+    r.dk = dk;
+    r.dv = dv;
+    r.dgk = dg;
+    r.dh0 = dh0;
+    r.ht_ws = wp.ht;
+    r.scale = scale;
+    r.H = (int)H;
+    r.K = (int)K;
+    r.V = (int)V;
+    r.si = si;
+    r.flags = {b.flags, NS, 1};
+    return hip_status(tops::run_recurrent_bwd(r, dtype, dtype, st),
+                      "chunk_bwd (gate-range fallback)");
   } else if (head) {
     // wide heads: the full-head reverse scan stores dh for the per-chunk gradient kernels
     rc = hip_status(head_scan(true, q, dout, dht, dh_ws, dh0, scale), "chunk_bwd (dh scan)");
     if (rc) return rc;
   } else {
-    tops::ScanArgs d;
+    tops::ScanArgs d = {};
     d.a = q;
     d.b = dout;
     d.g = g;
@@ -762,7 +868,13 @@ int tops_gla_simple_chunk_fwd(const void* q, const void* k, const void* v, const
   f.o = o;
   f.h_out = h_ws;
   f.ht = ht;
-  seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, f.NS, f.SL, f.seg_state, f.seg_gam);
+  {
+    const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+    f.NS = w.NS;
+    f.SL = w.SL;
+    f.seg_state = w.st;
+    f.seg_gam = w.gm;
+  }
   f.scale = scale;
   f.H = (int)H;
   f.K = (int)K;
@@ -799,7 +911,13 @@ int tops_gla_simple_chunk_bwd(const void* q, const void* k, const void* v, const
   hipStream_t st = (hipStream_t)stream;
   int NS = 1, SL = 0;
   float *seg_st = nullptr, *seg_gm = nullptr;
-  seg_setup(si, H, K, V, seg_ws, seg_ws_bytes, NS, SL, seg_st, seg_gm);
+  {
+    const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+    NS = w.NS;
+    SL = w.SL;
+    seg_st = w.st;
+    seg_gm = w.gm;
+  }
   if (h == nullptr) {
     tops::HeadScanArgs s = {};
     s.a = k;
@@ -937,7 +1055,7 @@ int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, co
     return fail(TOPS_GLA_EINVAL, "q, k, v and o must not be NULL");
   if ((int64_t)si.N * H * ((V + 31) / 32) > kMaxInt)
     return fail(TOPS_GLA_EUNSUPPORTED, "grid too large");
-  tops::RecArgs p;
+  tops::RecArgs p = {};
   p.q = q;
   p.k = k;
   p.v = v;
@@ -987,7 +1105,7 @@ int part_shape(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int C,
 
 int tops_gla_bwd_part_dA(const float* v, const float* dout, float* dA, float scale, int64_t B,
                          int64_t T, int64_t H, int64_t V, int chunk_size, void* stream) {
-  tops::PartArgs p;
+  tops::PartArgs p = {};
   int rc = part_shape(B, T, H, 1, V, chunk_size, {v, dout, dA}, &p);
   if (rc) return rc;
   p.v = v;
@@ -1001,7 +1119,7 @@ int tops_gla_bwd_part_dA(const float* v, const float* dout, float* dA, float sca
 int tops_gla_bwd_part_dv(const float* k, const float* g_cumsum, const float* A,
                          const float* dout, const float* dh, float* dv, int64_t B, int64_t T,
                          int64_t H, int64_t K, int64_t V, int chunk_size, void* stream) {
-  tops::PartArgs p;
+  tops::PartArgs p = {};
   int rc = part_shape(B, T, H, K, V, chunk_size, {k, g_cumsum, A, dout, dh, dv}, &p);
   if (rc) return rc;
   p.k = k;
@@ -1017,7 +1135,7 @@ int tops_gla_bwd_part_dv(const float* k, const float* g_cumsum, const float* A,
 int tops_gla_bwd_part_dqk_intra(const float* q, const float* k, const float* g_cumsum,
                                 const float* dA, float* dq, float* dk, int64_t B, int64_t T,
                                 int64_t H, int64_t K, int chunk_size, void* stream) {
-  tops::PartArgs p;
+  tops::PartArgs p = {};
   int rc = part_shape(B, T, H, K, 1, chunk_size, {q, k, g_cumsum, dA, dq, dk}, &p);
   if (rc) return rc;
   p.q = q;
@@ -1036,7 +1154,7 @@ int tops_gla_bwd_part_dqkg(const float* q, const float* k, const float* v, const
                            const float* dq, const float* dk, float* dq_out, float* dk_out,
                            float* dg, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
                            int64_t V, int chunk_size, void* stream) {
-  tops::PartArgs p;
+  tops::PartArgs p = {};
   int rc = part_shape(B, T, H, K, V, chunk_size,
                       {q, k, v, h, g_cumsum, dout, dh, dq, dk, dq_out, dk_out, dg}, &p);
   if (rc) return rc;
@@ -1184,7 +1302,7 @@ int tops_gla_short_conv_fwd(const void* x, const float* w, const float* bias, vo
                             int64_t B, int64_t T, int64_t D, int W, int silu,
                             const int32_t* cu_seqlens, int64_t N, int64_t max_len, int dtype,
                             void* stream) {
-  tops::ShortConvArgs p;
+  tops::ShortConvArgs p = {};
   int rc = conv_setup(B, T, D, W, cu_seqlens, N, max_len, dtype, &p);
   if (rc) return rc;
   if (B * T > 0 && (x == nullptr || w == nullptr || y == nullptr))
@@ -1203,7 +1321,7 @@ int tops_gla_short_conv_bwd(const void* x, const float* w, const float* bias, co
                             void* dx, float* dw_db, void* ws, int64_t ws_bytes, int64_t B,
                             int64_t T, int64_t D, int W, int silu, const int32_t* cu_seqlens,
                             int64_t N, int64_t max_len, int dtype, void* stream) {
-  tops::ShortConvArgs p;
+  tops::ShortConvArgs p = {};
   int rc = conv_setup(B, T, D, W, cu_seqlens, N, max_len, dtype, &p);
   if (rc) return rc;
   if (B * T > 0 && (x == nullptr || w == nullptr || dy == nullptr || dx == nullptr))
@@ -1258,7 +1376,7 @@ int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v, co
     return fail(TOPS_GLA_EINVAL, "ht_ws is required when dht and a gate are given");
   if ((int64_t)si.N * H * ((std::max(K, V) + 31) / 32) > kMaxInt)
     return fail(TOPS_GLA_EUNSUPPORTED, "grid too large");
-  tops::RecBwdArgs p;
+  tops::RecBwdArgs p = {};
   p.q = q;
   p.k = k;
   p.v = v;
@@ -1281,7 +1399,7 @@ int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v, co
   p.V = (int)V;
   p.reverse = reverse != 0;
   p.si = si;
-  return hip_status(tops::run_recurrent_bwd(p, dtype, (hipStream_t)stream),
+  return hip_status(tops::run_recurrent_bwd(p, dtype, tops::DT_F32, (hipStream_t)stream),
                     "fused_recurrent_bwd");
 }
 

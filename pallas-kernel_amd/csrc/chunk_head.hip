@@ -907,6 +907,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   }
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
+  float dmax = 0.f;   // largest |g~ - r| of the factors (base 2): the gate-range check
   f32x4 acc[NTV][NTK];
   {
     if (s > 0)
@@ -1041,6 +1042,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float d = gt[j][e] - r[e];
+          dmax = fmaxf(dmax, fabsf(d));
           xq[e] *= exp2_hw(d);
           xk[e] *= exp2_hw(-d);
           xd[e] = xk[e] * fkd[e];
@@ -1156,6 +1158,10 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   if (s == p.NS - 1 && p.ht)
     store_state_f32<NTV, NTK>(acc, p.ht + ((long)sg.seq * H + hh) * KV + cv, K, Vw, vt0, kt0,
                               lane, V);
+  if (p.flags) {   // uniform; every block writes its flag, so nothing needs clearing
+    const int bad = __syncthreads_or(dmax > kGateLimit2 ? 1 : 0);
+    if (tid == 0) p.flags[L0] = bad ? 1 : 0;
+  }
 }
 
 
@@ -1284,6 +1290,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   const int vd0 = (w % NVG) * VTW, jt0 = (w / NVG) * JT;   // dv^T tiles
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
+  int gbad = 0;          // uniform: a chunk had a factor beyond the gate-range limit
   f32x4 acc[NTV][NTK];   // dh[v][k]
   {
     if (s < p.NS - 1)
@@ -1432,6 +1439,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       float r[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = 0.5f * (first[e] + gam[e]);
+      float dmax = 0.f;
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
         const int row = rs * RPT + j;
@@ -1441,12 +1449,14 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           dd[j][e] -= r[e];
+          dmax = fmaxf(dmax, fabsf(dd[j][e]));
           xq[e] *= exp2_hw(dd[j][e]);
           xk[e] *= exp2_hw(-dd[j][e]);
         }
         *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pack8(xq);
         *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pack8(xk);
       }
+      gbad |= __ballot(dmax > kGateLimit2) != 0ull ? 1 : 0;
 #pragma unroll
       for (int j = 0; j < VRPT; ++j) {
         const int row = vrs * VRPT + j;
@@ -1735,6 +1745,10 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 
   if (s == 0 && p.dh0)
     store_state_f32<NTV, NTK>(acc, p.dh0 + ((long)sg.seq * H + hh) * KV, K, V, vt0, kt0, lane);
+  if (p.flags) {   // uniform; every block writes its flag, so nothing needs clearing
+    const int bad = __syncthreads_or(gbad);
+    if (tid == 0) p.flags[L] = bad ? 1 : 0;
+  }
 }
 
 // ---------------------------------------------------------------------------

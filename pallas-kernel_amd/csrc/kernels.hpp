@@ -92,6 +92,17 @@ struct CumsumArgs {
 hipError_t run_cumsum(const CumsumArgs& p, int in_dtype, int out_dtype, hipStream_t st);
 
 // Fused recurrent forward (recurrent.hip).
+// Per-block flags of the full-head kernels: 1 when one of the block's chunks has a gate
+// range beyond what the per-element factoring holds (|g~ - r| > kGateLimit2 in base 2),
+// written unconditionally by every block (no clearing). The block of (sequence seq, segment
+// s, head h, V tile t) writes at ((seq * ns + s) * H + h) * vt + t. The recurrent fallback
+// (exact for any decay) then recomputes the flagged (sequence, head) pairs.
+struct GateFlags {
+  int* p;      // nullable: no check, no fallback
+  int ns, vt;  // segments and V tiles per (sequence, head) in the flags' layout
+};
+constexpr float kGateLimit2 = 100.f;
+
 struct RecArgs {
   const void *q, *k, *v, *gk, *gv;  // gk / gv nullable
   const float* h0;                  // nullable
@@ -101,6 +112,7 @@ struct RecArgs {
   int H, K, V;
   int reverse;
   SeqInfo si;                       // C unused
+  GateFlags flags;                  // nullable: only the flagged (sequence, head) pairs run
 };
 hipError_t run_recurrent_fwd(const RecArgs& p, int dtype, int o_dtype, hipStream_t st);
 
@@ -121,22 +133,26 @@ struct RecScanArgs {
   // gate-gradient epilogue (dg nullable): dg = running sum of gx gxf - gy out
   // (+ sum_r s0 (.) hfin when hfin is given)
   const void* gx;
-  const float* gxf;
+  const void* gxf;   // out dtype, or float when gxf_f32
+  int gxf_f32;
   const void* gy;
   const float* hfin;
-  float* dg;
+  void* dg;          // out dtype
   SeqInfo si;  // C unused
+  GateFlags flags;   // nullable: only the flagged (sequence, head) pairs run
 };
 struct RecBwdArgs {
   const void *q, *k, *v, *gk, *gv, *dout;  // gk / gv nullable
   const float* o;                          // forward output f32 (needed with gv)
   const float *h0, *dht;                   // nullable
-  float *dq, *dk, *dv, *dgk, *dgv, *dh0;   // dgk / dgv / dh0 nullable
+  void *dq, *dk, *dv, *dgk, *dgv;         // out dtype; dgk / dgv nullable
+  float* dh0;                              // nullable
   float* ht_ws;                            // [N, H, K, V] f32, needed with dht and a gate
   float scale;
   int H, K, V;
   int reverse;
   SeqInfo si;
+  GateFlags flags;                         // nullable: only the flagged pairs run
 };
 // The backward's per-chunk parts over given intermediates (chunk_bwd_parts.hip), float32.
 enum { PART_DA = 0, PART_DV = 1, PART_DQK_INTRA = 2, PART_DQKG = 3 };
@@ -187,7 +203,7 @@ long short_conv_part_rows(long nseq, long len);   // len: T, or the longest sequ
 hipError_t run_short_conv(const ShortConvArgs& p, bool backward, int dtype, hipStream_t st);
 
 bool recurrent_supported(int K, int V);  // state rows K (forward) and V, K (backward)
-hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st);
+hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, int o_dtype, hipStream_t st);
 
 // Full-head kernels (chunk_head.hip): bf16, chunk 64, raw gates, K and V multiples of 8
 // (16-byte aligned rows); scans and forward for K <= 256 and any V (V tiles of 64 or 128
@@ -238,6 +254,7 @@ struct HeadFwdArgs {
   float scale;
   int H, K, V;
   SeqInfo si;
+  int* flags;             // nullable: per-block gate-range flags (GateFlags, vt = V tiles)
 };
 hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st);
 // Per-chunk gating of wide heads (K = 256) into p.gate_ws (q, k, g, scale, H, K, si read).
@@ -257,6 +274,7 @@ struct HeadBwdArgs {
   float scale;
   int H, K, V;
   SeqInfo si;
+  int* flags;             // nullable: per-block gate-range flags (GateFlags layout, vt = 1)
 };
 hipError_t run_head_bwd(const HeadBwdArgs& p, hipStream_t st);
 

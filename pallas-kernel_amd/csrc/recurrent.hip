@@ -182,6 +182,15 @@ __global__ __launch_bounds__(RNT) void rec_scan_kernel(RecScanArgs p) {
   const int ct = L % NCT;
   const int sh = L / NCT;
   const int seq = sh / H, hh = sh % H;
+  if (p.flags.p) {   // fallback launch: only the (sequence, head) pairs a block flagged
+    // the pair's flags (one per segment and column tile) read by the lanes of every wave
+    // at once, so an unflagged block returns after a single load
+    int f = 0;
+    for (int i = lane; i < p.flags.ns * p.flags.vt; i += 64)
+      f |= p.flags.p[((long)seq * p.flags.ns + i / p.flags.vt) * H * p.flags.vt +
+                     (long)hh * p.flags.vt + i % p.flags.vt];
+    if (__ballot(f != 0) == 0ull) return;   // uniform over the block: before any barrier
+  }
   int bos, eos;
   seq_bounds(p.si, seq, bos, eos);
   const int n = eos - bos;
@@ -289,7 +298,9 @@ __global__ __launch_bounds__(RNT) void rec_scan_kernel(RecScanArgs p) {
         pgc[k] = (cin && gi >= 0) ? y : 0.f;
       }
       if (grad) {
-        const float xd = to_f32(gx[co]) * p.gxf[co], xy = to_f32(gy[co]);
+        const float xf = p.gxf_f32 ? static_cast<const float*>(p.gxf)[co]
+                                   : to_f32(static_cast<const TO*>(p.gxf)[co]);
+        const float xd = to_f32(gx[co]) * xf, xy = to_f32(gy[co]);
         pxd[k] = cin ? xd : 0.f;
         py[k] = cin ? xy : 0.f;
       }
@@ -437,7 +448,8 @@ __global__ __launch_bounds__(RNT) void rec_scan_kernel(RecScanArgs p) {
 #pragma unroll 1
       for (int i = tid; i < nb * CB; i += RNT) {
         const int s = i / CB, c = i % CB;
-        if (cbase + c < C) p.dg[(long)tok(b0 + s) * rsC + (long)hh * C + cbase + c] = sXD[i];
+        if (cbase + c < C)
+          put<TO>(p.dg, (long)tok(b0 + s) * rsC + (long)hh * C + cbase + c, sXD[i]);
       }
     }
   }
@@ -524,16 +536,17 @@ hipError_t run_recurrent_fwd(const RecArgs& p, int dtype, int o_dtype, hipStream
   s.R = p.K;
   s.C = p.V;
   s.dir = p.reverse ? 1 : 0;
+  s.flags = p.flags;
   ktimer_mark(KT_REC_FWD, false, st);
   const hipError_t e = run_scan(s, dtype, o_dtype, st);
   ktimer_mark(KT_REC_FWD, true, st);
   return e;
 }
 
-hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st) {
+hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, int o_dtype, hipStream_t st) {
   if (dtype != DT_BF16 && dtype != DT_F32) return hipErrorInvalidValue;
   const bool need_ht = p.dht != nullptr && (p.gk != nullptr || p.gv != nullptr);
-  auto run = [&](const RecScanArgs& a) { return run_scan(a, dtype, DT_F32, st); };
+  auto run = [&](const RecScanArgs& a) { return run_scan(a, dtype, o_dtype, st); };
 
   // 1. dq (and h_T) : S = h^T, rows V, columns K, the forward's direction
   RecScanArgs s{};
@@ -553,6 +566,7 @@ hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st) {
   s.R = p.V;
   s.C = p.K;
   s.dir = p.reverse ? 1 : 0;
+  s.flags = p.flags;
   hipError_t e = run(s);
   if (e != hipSuccess) return e;
 
@@ -597,9 +611,11 @@ hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, hipStream_t st) {
   s3.C = p.V;
   s3.dir = p.reverse ? 0 : 1;
   s3.shift = 1;
+  s3.flags = p.flags;
   if (p.gv) {
     s3.gx = p.dout;
-    s3.gxf = p.o;
+    s3.gxf = p.o;   // the forward output, float
+    s3.gxf_f32 = 1;
     s3.gy = p.v;
     s3.hfin = need_ht ? p.ht_ws : nullptr;
     s3.dg = p.dgv;

@@ -36,7 +36,7 @@ _SIGS = {
                               _I64, _I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_chunk_fwd_o": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64,
                              _I64, _I, _P, _P, _I64, _I64, _I, _P],
-    "tops_gla_chunk_ws_bytes": [_I64, _I64, _I64, _I64, _I64, _I, _I, _I],
+    "tops_gla_chunk_ws_bytes": [_I64, _I64, _I64, _I64, _I64, _I, _I64, _I, _I],
     "tops_gla_chunk_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _F, _I64, _I64, _I64, _I64,
                            _I64, _I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_chunk_fwd_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64,
@@ -141,9 +141,13 @@ def full_head(K, V, chunk, dtype, backward):
     return bool(load().tops_gla_full_head(K, V, chunk, dtype_code(dtype), int(bool(backward))))
 
 
-def seg_workspace(B, T, H, K, V, chunk, varlen, dtype, device):
-    """Sequence-segment workspace of tops_gla_chunk_fwd / _bwd: (tensor or None, bytes)."""
-    n = int(load().tops_gla_chunk_ws_bytes(B, T, H, K, V, chunk, int(bool(varlen)),
+def seg_workspace(B, T, H, K, V, chunk, varlen, dtype, device, N=None):
+    """Workspace of tops_gla_chunk_fwd / _bwd (sequence segments, gate-range flags, wide
+    heads' gating, the backward fallback's states): (tensor or None, bytes). ``varlen``: the
+    cu_seqlens list (or a true value with ``N`` given), else falsy."""
+    if N is None:
+        N = len(varlen) - 1 if isinstance(varlen, (list, tuple)) else B
+    n = int(load().tops_gla_chunk_ws_bytes(B, T, H, K, V, chunk, N, int(bool(varlen)),
                                            dtype_code(dtype)))
     if n <= 0:
         return None, 0

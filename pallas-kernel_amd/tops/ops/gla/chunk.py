@@ -151,7 +151,7 @@ class _ChunkGLAFunction(torch.autograd.Function):
         keep = any(ctx.needs_input_grad[:5])
         h_ws = (torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev)
                 if keep or not _full_head(K, V, chunk, q.dtype, False, q, k, v, g, h0) else None)
-        ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list is not None, q.dtype, dev)
+        ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list, q.dtype, dev)
         call("tops_gla_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(o), ptr(ht),
              ptr(h_ws), ptr(ws), nws, scale, B, T, H, K, V, chunk, *seq.args(), dt,
              stream_of(dev))
@@ -177,7 +177,7 @@ class _ChunkGLAFunction(torch.autograd.Function):
         dh_ws = (None if _full_head(K, V, chunk, q.dtype, True, q, k, v, g, h0, h_ws, do, dht,
                                     dq, dk, dv, dg, dh0)
                  else torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev))
-        ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list is not None, q.dtype, dev)
+        ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list, q.dtype, dev)
         call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(h_ws), ptr(do),
              ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None, ptr(dh_ws), ptr(ws),
              nws, scale, B, T, H, K, V, chunk, *seq.args(), dtype_code(q.dtype),
@@ -203,7 +203,7 @@ class _ScalarGateGLAFunction(torch.autograd.Function):
               if output_final_state else None)
         keep = any(ctx.needs_input_grad[:5])
         h_ws = torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev) if keep else None
-        ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list is not None, q.dtype, dev)
+        ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list, q.dtype, dev)
         call("tops_gla_simple_chunk_fwd", ptr(q), ptr(k), ptr(v), ptr(gs), ts, ptr(h0), ptr(o),
              ptr(ht), ptr(h_ws), ptr(ws), nws, scale, B, T, H, K, V, C, *seq.args(),
              dtype_code(q.dtype), stream_of(dev))
@@ -228,7 +228,7 @@ class _ScalarGateGLAFunction(torch.autograd.Function):
         dg = _out_like(q, cu_list) if want_dg else None
         need_dh0 = h0 is not None and ctx.needs_input_grad[4]
         dh0 = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if need_dh0 else None
-        ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list is not None, q.dtype, dev)
+        ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list, q.dtype, dev)
         call("tops_gla_simple_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(gs), ts, ptr(h0),
              ptr(h_ws), ptr(do), ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None,
              ptr(ws), nws, scale, B, T, H, K, V, C, *seq.args(), dtype_code(q.dtype),
@@ -528,8 +528,8 @@ def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_fi
     h = torch.empty(B, seq.NC // B, H, K, V, dtype=cdt, device=dev)
     ht = torch.empty(seq.N, H, K, V, dtype=torch.float32, device=dev) if output_final_state \
         else None
-    ws, nws = (None, 0) if g_is_cumsum else _lib.seg_workspace(B, Tp, H, K, V, C,
-                                                                cu_list is not None, cdt, dev)
+    ws, nws = (None, 0) if g_is_cumsum else _lib.seg_workspace(B, Tp, H, K, V, C, new_cu,
+                                                                cdt, dev)
     call("tops_gla_chunk_fwd_h", ptr(kp), ptr(vp), ptr(g_in), g_is_cumsum,
          ptr(_c(initial_state, torch.float32)), ptr(h), ptr(ht), ptr(ws), nws, B, Tp, H, K, V,
          C, *seq.args(), dt, st)
@@ -575,7 +575,7 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
     h_ws = None if h is not None else torch.empty(seq.NC, H, K, V, dtype=cdt, device=dev)
     dh_ws = (None if _full_head(K, V, C, cdt, True, qq, kk, vv, gg, dd, h, dht, initial_state)
              else torch.empty(seq.NC, H, K, V, dtype=cdt, device=dev))
-    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list is not None, cdt, dev)
+    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list, cdt, dev)
     call("tops_gla_chunk_bwd", ptr(qq), ptr(kk), ptr(vv), ptr(gg),
          ptr(_c(initial_state, torch.float32)), ptr(h), ptr(dd), ptr(_c(dht, torch.float32)),
          ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), ptr(h_ws), ptr(dh_ws), ptr(ws), nws,

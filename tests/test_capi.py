@@ -160,22 +160,31 @@ def test_seq_layout_chunk_offsets():
 
 
 def test_segment_workspace_query():
-    """Host-only: the segment workspace covers [N, NS, H, K, V] f32 states + decays."""
+    """Host-only: the workspace = segment states [N, NS, H, K, V] f32 + decays, the per-block
+    gate-range flags (int32), the wide heads' gating, the backward fallback's final states
+    [N, H, K, V] f32; each part 256-byte aligned."""
     lib = _lib.load()
     q = lib.tops_gla_chunk_ws_bytes
+    a = lambda x: (x + 255) // 256 * 256  # noqa: E731
     # B4 T8192 H16 K=V=128 chunk 64 bf16: 128 chunks per sequence; 64 (sequence, head) blocks
     # -> 4 segments of 32 chunks (one block per CU of 256)
     st = 4 * 4 * 16 * 128 * 128 * 4
     gm = 4 * 4 * 16 * 128 * 4
-    assert q(4, 8192, 16, 128, 128, 64, 0, 1) == st + (gm + 255) // 256 * 256
-    assert q(4, 8192, 16, 128, 128, 64, 1, 1) == 0      # varlen: unsegmented
-    assert q(4, 8192, 16, 128, 128, 64, 0, 0) == 0      # float32: other kernels
-    assert q(4, 8192, 16, 128, 128, 32, 0, 1) == 0      # chunk 32: other kernels
-    assert q(1, 256, 2, 64, 64, 64, 0, 1) == 0          # 4 chunks: too short to split
-    # K = 256: V tiles of 64 columns (2 per head) -> 2 segments of 64 chunks
+    flags = a(4 * 4 * 16 * 4)
+    ht = 4 * 16 * 128 * 128 * 4
+    assert q(4, 8192, 16, 128, 128, 64, 4, 0, 1) == a(st + a(gm)) + flags + ht
+    # varlen (3 sequences): unsegmented, flags and fallback states only
+    assert q(1, 8192, 16, 128, 128, 64, 3, 1, 1) == a(3 * 16 * 4) + 3 * 16 * 128 * 128 * 4
+    assert q(4, 8192, 16, 128, 128, 64, 3, 0, 1) == 0    # fixed length needs N == B
+    assert q(4, 8192, 16, 128, 128, 64, 4, 0, 0) == 0    # float32: other kernels
+    assert q(4, 8192, 16, 128, 128, 32, 4, 0, 1) == 0    # chunk 32: other kernels
+    # 4 chunks: too short to split; flags and fallback states
+    assert q(1, 256, 2, 64, 64, 64, 1, 0, 1) == a(2 * 4) + 2 * 64 * 64 * 4
+    # K = 256: V tiles of 64 columns (2 per head) -> 2 segments of 64 chunks; no fused
+    # backward, so no fallback states
     st2, gm2 = 4 * 2 * 16 * 256 * 128 * 4, 4 * 2 * 16 * 256 * 4
-    assert q(4, 8192, 16, 256, 128, 64, 0, 1) == st2 + (gm2 + 255) // 256 * 256
-    assert q(4, 8192, 16, 320, 128, 64, 0, 1) == 0      # K > 256: other kernels
+    assert q(4, 8192, 16, 256, 128, 64, 4, 0, 1) == a(st2 + a(gm2)) + a(4 * 2 * 16 * 2 * 4)
+    assert q(4, 8192, 16, 320, 128, 64, 4, 0, 1) == 0    # K > 256: other kernels
 
 
 def test_kernel_timer_without_launches():

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import oracle as orc
-from gla_cases import check, make_inputs, to_dev, to_np
+from gla_cases import check, make_inputs, round_bf16, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -188,6 +188,10 @@ BWD_CASES = [
     dict(B=2, T=32, H=4, K=32, V=64, seed=200, scale=0.1),
     dict(B=1, T=256, H=2, K=32, V=64, seed=303, h0=True, dht=True),
     dict(B=2, T=64, H=4, K=32, V=64, seed=500, C=32),
+    # the reference table's chunk sizes 8 and 4 (test_pallas_chunk_bwd.py:43,45,73)
+    dict(B=1, T=128, H=2, K=32, V=64, seed=501, C=8, h0=True, dht=True),
+    dict(B=1, T=64, H=2, K=32, V=64, seed=503, C=4),
+    dict(B=1, T=64, H=2, K=16, V=32, seed=511, C=8, cu=[0, 32, 64]),
     dict(B=2, T=128, H=4, K=32, V=64, seed=502, C=64, h0=True, dht=True),
     dict(B=1, T=48, H=4, K=32, V=64, seed=20, cu=[0, 16, 48], h0=True, dht=True),
     dict(B=1, T=45, H=2, K=32, V=64, seed=604, cu=[0, 20, 45], h0=True, dht=True),
@@ -328,6 +332,35 @@ def test_chunk_gla_fwd_and_bwd_orchestrators_padded():
                              cu_seqlens=cu, chunk_size=C)
     for name, a, b in zip(["dq", "dk", "dv", "dg", "dh0"], grads, gref):
         check(name, to_np(a), b, "f32", atol=1e-4 * max(1.0, np.abs(b).max()))
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(B=1, T=128, H=2, K=32, V=64, seed=501, C=8, h0=True, dht=True),
+    dict(B=1, T=64, H=2, K=32, V=64, seed=503, C=4),
+    dict(B=1, T=64, H=2, K=16, V=32, seed=511, C=8, cu=[0, 32, 64]),
+], ids=["C8-h0-dht", "C4", "C8-varlen"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_chunk_gla_bwd_orchestrator_small_chunks(cfg, dtype):
+    """chunk_gla_bwd called directly with the reference table's chunk sizes 8 and 4
+    (test_pallas_chunk_bwd.py:43,45,73), against the oracle at the same chunk size."""
+    G = _gla()
+    B, T, H, K, V, C = (cfg[x] for x in "BTHKVC")
+    cu = cfg.get("cu")
+    N = len(cu) - 1 if cu else B
+    q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, cfg["seed"], h0=cfg.get("h0", False),
+                                          dht=cfg.get("dht", False), N=N, dtype=dtype)
+    d = lambda x: to_dev(x, dtype)  # noqa: E731
+    grads = G.chunk_gla_bwd(d(q), d(k), d(v), d(g), None, None, K ** -0.5,
+                            to_dev(s0, "state"), None, None, d(do), to_dev(dht, "state"),
+                            cu_seqlens=cu, chunk_size=C)
+    gref = orc.chunk_gla_bwd(q, k, v, g, None, None, K ** -0.5, s0, None, None, do, dht,
+                             cu_seqlens=cu, chunk_size=C)
+    for name, a, b in zip(["dq", "dk", "dv", "dg", "dh0"], grads, gref):
+        if b is None:
+            assert a is None, name
+            continue
+        atol = 1e-4 * max(1.0, float(np.abs(b).max())) if dtype == "f32" else None
+        check(name, to_np(a), b, dtype, atol=atol)
 
 
 def test_g_gamma_gradient_reduced():
@@ -626,3 +659,68 @@ def test_common_chunk_h(cfg):
                                         scale=0.5, cu_seqlens_cpu=cu, chunk_size=C)
         check("dh_ref", to_np(dh2), dh_ref, "f32", atol=tol(dh_ref))
         check("dh0_ref", to_np(dh02), dh0_ref, "f32", atol=tol(dh0_ref))
+
+
+# ---------------------------------------------------------------------------
+# gate ranges beyond the per-element factoring: flagged blocks, recurrent fallback
+# ---------------------------------------------------------------------------
+
+STRONG_CASES = [
+    # per-token log decays of about 4 (x5 on logsigmoid(randn)): chunk gate ranges near 256,
+    # far beyond the factoring's ~138; segmented (2048 tokens: 4 segments) and not
+    dict(B=1, T=2048, H=2, K=128, V=128, seed=861, mul=5.0, h0=True, dht=True),
+    dict(B=2, T=300, H=2, K=64, V=128, seed=862, mul=5.0, h0=True, dht=True),
+    # only one (sequence, head) pair strong: the others keep the chunked results
+    dict(B=2, T=512, H=2, K=128, V=128, seed=863, mul=5.0, only=(1, 0), h0=True, dht=True),
+    # varlen, an empty sequence, strong gates in the middle sequence only
+    dict(B=1, T=400, H=2, K=128, V=64, seed=864, mul=5.0, cu=[0, 100, 100, 300, 400],
+         only_seq=2, h0=True, dht=True),
+    # just inside the limit (ranges of about 120-130): the chunked kernels themselves
+    dict(B=1, T=1024, H=2, K=128, V=128, seed=865, mul=2.4, h0=True, dht=True),
+]
+
+
+def _strong_inputs(cfg):
+    B, T, H, K, V = (cfg[x] for x in "BTHKV")
+    cu = cfg.get("cu")
+    N = len(cu) - 1 if cu else B
+    q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, cfg["seed"], h0=cfg.get("h0", False),
+                                          dht=cfg.get("dht", False), N=N)
+    mul = np.ones_like(g)
+    if "only" in cfg:
+        b, h = cfg["only"]
+        mul[b, :, h] = cfg["mul"]
+    elif "only_seq" in cfg:
+        i = cfg["only_seq"]
+        mul[:, cu[i]:cu[i + 1]] = cfg["mul"]
+    else:
+        mul[:] = cfg["mul"]
+    q, k, v, g, do = (round_bf16(x) for x in (q, k, v, g * mul, do))
+    return q, k, v, g, s0, do, dht, cu
+
+
+@pytest.mark.parametrize("cfg", STRONG_CASES, ids=[f"s{c['seed']}" for c in STRONG_CASES])
+def test_strong_gates(cfg):
+    """bf16 chunk_gla forward and backward with per-token decays of about 4 (chunk gate
+    ranges beyond the full-head kernels' per-element factoring): the flagged (sequence,
+    head) pairs are recomputed by the recurrent scans; everything matches the float64
+    oracle at the bf16 bar, and stays finite."""
+    G = _gla()
+    q, k, v, g, s0, do, dht, cu = _strong_inputs(cfg)
+    K = cfg["K"]
+    tq, tk, tv, tg = (to_dev(x, "bf16").requires_grad_() for x in (q, k, v, g))
+    th0 = to_dev(s0, "state").requires_grad_()
+    o, ht = G.chunk_gla(tq, tk, tv, tg, initial_state=th0, output_final_state=True,
+                        cu_seqlens=None if cu is None else torch.tensor(cu), chunk_size=64)
+    loss = (o.float() * to_dev(do, "f32")).sum() + (ht * to_dev(dht, "state")).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    on, hn = orc.naive_recurrent_gla(q, k, v, g, initial_state=s0, output_final_state=True,
+                                     cu_seqlens=cu)
+    check("o", to_np(o), on, "bf16")
+    check("ht", to_np(ht), hn, "bf16")
+    ref = orc.chunk_gla_bwd(q, k, v, g, None, None, K ** -0.5, s0, None, None, do, dht,
+                            cu_seqlens=cu, chunk_size=16)
+    for name, x, r in zip(["dq", "dk", "dv", "dg"], (tq, tk, tv, tg), ref):
+        check(name, to_np(x.grad), r, "bf16")
+    check("dh0", to_np(th0.grad), ref[4], "bf16")
