@@ -682,17 +682,19 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   };
 
   if (nsteps > 0) {
-    // The first chunk is peeled so that the loop is entered with the same sequence of
-    // outstanding loads and stores as its back edge.
+    // Both register sets are consumed in every trip of the loop (the odd step after it):
+    // the loop is entered, and taken again, with the same outstanding loads -- the older
+    // set first -- so the waits for a step's loads leave the next step's in flight.
     Regs R0, R1;
     issue(0, R0);
     __builtin_amdgcn_sched_barrier(0);
     issue(1, R1);
-    body(0, R0);
-    for (int step = 1; step < nsteps; step += 2) {
-      body(step, R1);
-      if (step + 1 < nsteps) body(step + 1, R0);
+    int step = 0;
+    for (; step + 1 < nsteps; step += 2) {
+      body(step, R0);
+      body(step + 1, R1);
     }
+    if (step < nsteps) body(step, R0);
   }
 
   if (p.pass == 1) {
@@ -1140,15 +1142,18 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   };
 
   if (nsteps > 0 && PF == 2) {
+    // both register sets every trip (the odd chunk after the loop): entered and taken again
+    // with the same outstanding loads, so a chunk's waits leave the next chunk's in flight
     Regs R0, R1;
     issue(0, R0);
     __builtin_amdgcn_sched_barrier(0);
     issue(1, R1);
-    body(0, R0);
-    for (int step = 1; step < nsteps; step += 2) {
-      body(step, R1);
-      if (step + 1 < nsteps) body(step + 1, R0);
+    int step = 0;
+    for (; step + 1 < nsteps; step += 2) {
+      body(step, R0);
+      body(step + 1, R1);
     }
+    if (step < nsteps) body(step, R0);
   } else if (nsteps > 0) {
     Regs R0;
     issue(0, R0);
