@@ -62,6 +62,87 @@ struct HTilesN {
   static_assert(NTK >= 1, "tile split");
 };
 
+// LDS tiles of bf16, W columns (W a multiple of 16). Element (r, c) sits at
+//   r (W + 16) + 8 (r & ~7) + (c ^ (r & 8)):
+// rows padded by 16 elements, 64 more elements after every 8 rows, and the two 8-column
+// halves of every 16-column group swapped in the rows with bit 3 set. The LDS has 64 banks of
+// 4 bytes; ds_read_b128 serves each half-wave in two groups of 16 lanes (the quads with even,
+// then odd, parity of lane bits 2-4) and ds_read_b64_tr_b16 32 lanes at a time. In this layout
+// the 16-byte row fragments and the transposed fragments of every 16 x 32 / 32 x 16 MFMA
+// operand hit each bank once per group (4 and 2 LDS cycles per instruction); a plain
+// 16-element row pad conflicts 2-way on both (8 and 4 cycles, SQ_LDS_IDX_ACTIVE per
+// instruction on MI355X). The swizzle only touches lane-dependent address bits: for a tile
+// origin (r0, c0) with r0 and c0 multiples of 16, off(r0 + r, c0 + c) = at(r0, c0) + off(r, c),
+// so a fragment address is a per-lane part plus a constant.
+template <int W>
+struct LT {
+  static_assert(W % 16 == 0, "tile width");
+  static constexpr int P = W + 16;
+  // bytes of a tile of `rows` rows (rows % 8 == 0)
+  __host__ __device__ static constexpr int bytes(int rows) { return rows * (P + 8) * 2; }
+  // element offset of the tile origin (r0, c0), r0 % 16 == 0, c0 % 16 == 0
+  __host__ __device__ static constexpr int at(int r0, int c0) { return r0 * (P + 8) + c0; }
+  __device__ static __forceinline__ int off(int r, int c) {
+    return r * P + 8 * (r & ~7) + (c ^ (r & 8));
+  }
+  // per-lane parts: row fragment (row lane & 15, columns 8 (lane >> 4) + 0..7)
+  __device__ static __forceinline__ int row_frag(int lane) {
+    return off(lane & 15, 8 * (lane >> 4));
+  }
+  // transposed fragment, first read (row 8 (lane >> 4) + ((lane & 15) >> 2), columns
+  // 4 (lane & 3) + 0..3); the second read is 4 rows further (4 P: same 8-row group)
+  __device__ static __forceinline__ int tr_frag(int lane) {
+    return off(8 * (lane >> 4) + ((lane & 15) >> 2), 4 * (lane & 3));
+  }
+  // one transposed read of a 16 x 16 tile (rows 4 (lane >> 4) + ((lane & 15) >> 2)): lane l
+  // receives rows 4 (l >> 4) + 0..3 of column l & 15, the MFMA accumulator layout
+  __device__ static __forceinline__ int tr_rows4(int lane) {
+    return off(4 * (lane >> 4) + ((lane & 15) >> 2), 4 * (lane & 3));
+  }
+  // accumulator position (row lane & 15, columns 4 (lane >> 4) + 0..3)
+  __device__ static __forceinline__ int acc_pos(int lane) {
+    return off(lane & 15, 4 * (lane >> 4));
+  }
+};
+
+// Fragments of LT tiles; o = element offset (tile origin + per-lane part).
+__device__ __forceinline__ Frag<bf16> ldr(const bf16* t, int o) {
+  Frag<bf16> f;
+  f.d = *reinterpret_cast<const uint4*>(t + o);
+  return f;
+}
+template <int W>
+__device__ __forceinline__ Frag<bf16> ldt(const bf16* t, int o) {
+  const bf16* p1 = t + o;
+  const s4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4_t*)(p1));
+  const s4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4_t*)(p1 + 4 * LT<W>::P));
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  Frag<bf16> f;
+  f.d = make_uint4(ua.x, ua.y, ub.x, ub.y);
+  return f;
+}
+// acc += X Y^T over klen columns: X rows xr0.. of a WX-wide tile, Y rows yr0.. of a WY-wide
+// tile (row fragments of both)
+template <int WX, int WY>
+__device__ __forceinline__ void mma_rr(f32x4& acc, const bf16* X, int xr0, const bf16* Y,
+                                       int yr0, int klen, int lane) {
+  const int ox = LT<WX>::at(xr0, 0) + LT<WX>::row_frag(lane);
+  const int oy = LT<WY>::at(yr0, 0) + LT<WY>::row_frag(lane);
+  for (int kk = 0; kk < klen; kk += 32) mma(acc, ldr(X, ox + kk), ldr(Y, oy + kk));
+}
+// acc += X^T Y^T-rows: X stored [k][m] (columns xc0.. of a WX-wide tile, transposed
+// fragments), Y rows yr0.. of a WY-wide tile stored [n][k] (row fragments), over klen k
+template <int WX, int WY>
+__device__ __forceinline__ void mma_tr(f32x4& acc, const bf16* X, int xc0, const bf16* Y,
+                                       int yr0, int klen, int lane) {
+  const int ox = LT<WX>::at(0, xc0) + LT<WX>::tr_frag(lane);
+  const int oy = LT<WY>::at(yr0, 0) + LT<WY>::row_frag(lane);
+  for (int kk = 0; kk < klen; kk += 32)
+    mma(acc, ldt<WX>(X, ox + LT<WX>::at(kk, 0)), ldr(Y, oy + kk));
+}
+
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // A loop-invariant per-lane offset kept out of loop-invariant code motion: hoisted out of a
@@ -430,13 +511,13 @@ __device__ __forceinline__ void store_state_bf16(const f32x4 (&acc)[NTV][NTK], b
     }
 }
 
-// acc = acc * decay[k] + X^T Y over the chunk's CR rows: X = b [c][v] (sB), Y = a [c][k]
-// (sA), both read with transposed fragments.
+// acc = acc * decay[k] + X^T Y over the chunk's CR rows: X = b [c][v] (sB, a WB-wide LT
+// tile), Y = a [c][k] (sA, WA wide), both read with transposed fragments.
 // With `post`, the result is then scaled by post[k] (the update then reads
 // acc = post (.) (acc * decay + X^T Y)).
-template <int NTV, int NTK, int CR = HC>
-__device__ __forceinline__ void state_update(f32x4 (&acc)[NTV][NTK], const bf16* sB, int PB,
-                                             const bf16* sA, int PA, const float* decay,
+template <int NTV, int NTK, int WB, int WA, int CR = HC>
+__device__ __forceinline__ void state_update(f32x4 (&acc)[NTV][NTK], const bf16* sB,
+                                             const bf16* sA, const float* decay,
                                              int vt0, int kt0, int lane,
                                              const float* post = nullptr) {
 #pragma unroll
@@ -445,13 +526,14 @@ __device__ __forceinline__ void state_update(f32x4 (&acc)[NTV][NTK], const bf16*
 #pragma unroll
     for (int i = 0; i < NTV; ++i) acc[i][j] *= d;
   }
+  const int ob = LT<WB>::tr_frag(lane), oa = LT<WA>::tr_frag(lane);
 #pragma unroll
   for (int kk = 0; kk < CR; kk += 32) {
     Frag<bf16> x[NTV], y[NTK];
 #pragma unroll
-    for (int i = 0; i < NTV; ++i) x[i] = ld_frag_t(sB + kk * PB + (vt0 + i) * 16, PB, lane);
+    for (int i = 0; i < NTV; ++i) x[i] = ldt<WB>(sB, LT<WB>::at(kk, (vt0 + i) * 16) + ob);
 #pragma unroll
-    for (int j = 0; j < NTK; ++j) y[j] = ld_frag_t(sA + kk * PA + (kt0 + j) * 16, PA, lane);
+    for (int j = 0; j < NTK; ++j) y[j] = ldt<WA>(sA, LT<WA>::at(kk, (kt0 + j) * 16) + oa);
 #pragma unroll
     for (int i = 0; i < NTV; ++i)
 #pragma unroll
@@ -482,10 +564,9 @@ __host__ __device__ constexpr int head_vp(int KP, int V) {
 // the cumsum, the step's decays.
 template <int KP, int VP, int NT, int CR>
 struct HSLayout {
-  static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP);
   static constexpr int a = 0;
-  static constexpr int b = a + CR * PKP * 2;
-  static constexpr int tot = b + CR * PVP * 2;
+  static constexpr int b = a + LT<KP>::bytes(CR);
+  static constexpr int tot = b + LT<VP>::bytes(CR);
   static constexpr int gam = tot + (NT / 64) * KP * 4;
   static constexpr int bytes = gam + KP * 4;
 };
@@ -506,7 +587,6 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   using Lay = HSLayout<KP, VP, NT, CR>;
   static_assert(CR == HC || CR == 2 * HC, "chunk rows");
   constexpr int RPT = MA::RPT, VRPT = MB::RPT;
-  constexpr int PKP = Lay::PKP, PVP = Lay::PVP;
   constexpr int NTV = TL::NTV, NTK = TL::NTK;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   bf16* sA = reinterpret_cast<bf16*>(smem + Lay::a);
@@ -626,7 +706,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
         unpack8(mask16(R.a[j], colA ? ~0u : 0u), x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= fa[e];
-        *reinterpret_cast<uint4*>(sA + row * PKP + cg * 8) = pack8(x);
+        *reinterpret_cast<uint4*>(sA + LT<KP>::off(row, cg * 8)) = pack8(x);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) gam[e] = gs[e];
@@ -653,13 +733,13 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           x[e] *= REV ? p.scale * exp2_hw(gt[j][e]) : exp2_hw(gt[j][e]);
-        *reinterpret_cast<uint4*>(sA + row * PKP + cg * 8) = pack8(x);
+        *reinterpret_cast<uint4*>(sA + LT<KP>::off(row, cg * 8)) = pack8(x);
       }
     }
 #pragma unroll
     for (int j = 0; j < VRPT; ++j) {
       const int row = vrs * VRPT + j;
-      *reinterpret_cast<uint4*>(sB + row * PVP + vg * 8) =
+      *reinterpret_cast<uint4*>(sB + LT<VP>::off(row, vg * 8)) =
           mask16(R.b[j], (colB && row < len) ? ~0u : 0u);
     }
     if (rs == TRS) {
@@ -678,7 +758,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
         store_state_bf16<NTV, NTK>(acc, s_all + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K,
                                    Vw, vt0, kt0, lane, V);
     }
-    state_update<NTV, NTK, CR>(acc, sB, PVP, sA, PKP, sGam, vt0, kt0, lane);
+    state_update<NTV, NTK, VP, KP, CR>(acc, sB, sA, sGam, vt0, kt0, lane);
   };
 
   if (nsteps > 0) {
@@ -719,10 +799,9 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 
 template <int KP>
 struct GPLayout {
-  static constexpr int PKP = pitch_of<bf16>(KP);
   static constexpr int qg = 0;
-  static constexpr int kg = qg + HC * PKP * 2;
-  static constexpr int tot = kg + HC * PKP * 2;
+  static constexpr int kg = qg + LT<KP>::bytes(HC);
+  static constexpr int tot = kg + LT<KP>::bytes(HC);
   static constexpr int first = tot + HNW * KP * 4;
   static constexpr int bytes = first + KP * 4;
 };
@@ -731,7 +810,7 @@ template <int KP>
 __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
   using M = HMap<KP>;
   using Lay = GPLayout<KP>;
-  constexpr int RPT = M::RPT, PKP = Lay::PKP;
+  constexpr int RPT = M::RPT;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
   bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
@@ -780,8 +859,8 @@ __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
       xk[e] *= exp2_hw(-d);
     }
     const uint4 pq = pack8(xq), pk = pack8(xk);
-    *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pq;
-    *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pk;
+    *reinterpret_cast<uint4*>(sQg + LT<KP>::off(row, cg * 8)) = pq;
+    *reinterpret_cast<uint4*>(sKg + LT<KP>::off(row, cg * 8)) = pk;
     if (colA) {
       *reinterpret_cast<uint4*>(gq + row * K + cg * 8) = pq;
       *reinterpret_cast<uint4*>(gk + row * K + cg * 8) = pk;
@@ -805,8 +884,7 @@ __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
   for (int t = w; t < 16; t += HNW) {
     const int mi = t >> 2, ni = t & 3;
     f32x4 at = zero4();
-    if (ni <= mi)
-      mma_tile<bf16>(at, sQg + mi * 16 * PKP, PKP, sKg + ni * 16 * PKP, PKP, KP, lane);
+    if (ni <= mi) mma_rr<KP, KP>(at, sQg, mi * 16, sKg, ni * 16, KP, lane);
     const int jj = ni * 16 + (lane & 15);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
@@ -828,22 +906,20 @@ __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
 template <int KP, int VP, bool SG = false>
 struct HFLayout {
   static constexpr bool KD = KP <= 128;
-  static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP),
-                       PA = pitch_of<bf16>(HC);
   static constexpr int qg = 0;
-  static constexpr int kg = qg + HC * PKP * 2;
-  static constexpr int kd = kg + HC * PKP * 2;
-  static constexpr int v = kd + (KD ? HC * PKP * 2 : 0);
-  static constexpr int hk = v + HC * PVP * 2;      // h' [k][v]
-  static constexpr int a = hk + KP * PVP * 2;      // A  [i][j]
-  static constexpr int tot = a + HC * PA * 2;
-  static constexpr int first = tot + HNW * KP * 4;
+  static constexpr int kg = qg + LT<KP>::bytes(HC);
+  static constexpr int kd = kg + LT<KP>::bytes(HC);
+  static constexpr int v = kd + (KD ? LT<KP>::bytes(HC) : 0);
+  static constexpr int hk = v + LT<VP>::bytes(HC);      // h' [k][v]
+  static constexpr int a = hk + LT<VP>::bytes(KP);      // A  [i][j]
+  static constexpr int tot = a + LT<HC>::bytes(HC);   // cumsum wave totals (!SG)
+  static constexpr int first = tot + (SG ? 0 : HNW * KP * 4);
   static constexpr int gam = first + KP * 4;
   static constexpr int rsc = gam + KP * 4;
   static constexpr int pre = rsc + KP * 4;        // 2^r          (!KD)
   static constexpr int post = pre + KP * 4;       // 2^{gamma-r}  (!KD)
   static constexpr int v2 = post + KP * 4;        // SG only
-  static constexpr int grow = v2 + (SG ? HC * PVP * 2 : 0);
+  static constexpr int grow = v2 + (SG ? LT<VP>::bytes(HC) : 0);
   static constexpr int bytes = grow + (SG ? HC * 4 : 0);
 };
 
@@ -854,7 +930,6 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   using TL = HTiles<KP, VP>;
   using Lay = HFLayout<KP, VP, SG>;
   constexpr int RPT = M::RPT, VRPT = MV::RPT;
-  constexpr int PKP = Lay::PKP, PVP = Lay::PVP, PA = Lay::PA;
   constexpr int NTV = TL::NTV, NTK = TL::NTK;
   // chunks of inputs in flight: two register sets, one for the wide head (K = 256), whose
   // rows take twice the registers (and whose loop body is only inlined once)
@@ -902,7 +977,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   const bool colA = cg * 8 < K, colB = vg * 8 < Vw;
 
   // zero A once (its upper triangle is never written); PRE: the column factors past K too
-  for (int i = tid; i < HC * PA / 8; i += HNT)
+  for (int i = tid; i < LT<HC>::bytes(HC) / 16; i += HNT)
     reinterpret_cast<uint4*>(sA)[i] = make_uint4(0, 0, 0, 0);
   if constexpr (PRE) {
     for (int i = tid; i < KP; i += HNT) sRs[i] = sPre[i] = sPost[i] = 0.f;
@@ -953,6 +1028,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   };
 
   auto body = [&](int step, Regs& R) {
+    // lane taken through opaque() every chunk: the per-lane LDS offsets are recomputed in
+    // the loop instead of held in registers across it
+    const int ln = (int)opaque((uint32_t)lane);
     const int ci = sg.cb + step;
     const int t0 = sg.bos + ci * HC;
     const int len = min(HC, sg.eos - t0);
@@ -969,16 +1047,16 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {   // (rows past the chunk are zeros in the workspace)
         const int row = rs * RPT + j;
-        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = mask16(R.q[j], colA ? ~0u : 0u);
-        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = mask16(R.k[j], colA ? ~0u : 0u);
+        *reinterpret_cast<uint4*>(sQg + LT<KP>::off(row, cg * 8)) = mask16(R.q[j], colA ? ~0u : 0u);
+        *reinterpret_cast<uint4*>(sKg + LT<KP>::off(row, cg * 8)) = mask16(R.k[j], colA ? ~0u : 0u);
       }
 #pragma unroll
       for (int j = 0; j < VRPT; ++j) {
         const int row = vrs * VRPT + j;
-        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) =
+        *reinterpret_cast<uint4*>(sV + LT<VP>::off(row, vg * 8)) =
             mask16(R.v[j], (colB && row < len) ? ~0u : 0u);
       }
-      *reinterpret_cast<uint4*>(sA + (tid >> 3) * PA + (tid & 7) * 8) = R.a;
+      *reinterpret_cast<uint4*>(sA + LT<HC>::off(tid >> 3, (tid & 7) * 8)) = R.a;
       if (tid < 3 * K / 4) {   // factors: scale 2^r, 2^r, 2^{gamma-r} (K floats each)
         const int i4 = tid * 4, which = i4 / K, col = i4 % K;
         const int off = which == 0 ? Lay::rsc : which == 1 ? Lay::pre : Lay::post;
@@ -995,20 +1073,20 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       for (int j = 0; j < RPT; ++j) {
         const int row = rs * RPT + j;
         const uint32_t m = (colA && row < len) ? ~0u : 0u;
-        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = mask16(R.q[j], m);
-        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = mask16(R.k[j], m);
+        *reinterpret_cast<uint4*>(sQg + LT<KP>::off(row, cg * 8)) = mask16(R.q[j], m);
+        *reinterpret_cast<uint4*>(sKg + LT<KP>::off(row, cg * 8)) = mask16(R.k[j], m);
       }
 #pragma unroll
       for (int j = 0; j < VRPT; ++j) {
         const int row = vrs * VRPT + j;
         const uint4 vm = mask16(R.v[j], (colB && row < len) ? ~0u : 0u);
-        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) = vm;
+        *reinterpret_cast<uint4*>(sV + LT<VP>::off(row, vg * 8)) = vm;
         const float f = exp2_hw(gam_s - __shfl(Gl, row));
         float x[8];
         unpack8(vm, x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= f;
-        *reinterpret_cast<uint4*>(sV2 + row * PVP + vg * 8) = pack8(x);
+        *reinterpret_cast<uint4*>(sV2 + LT<VP>::off(row, vg * 8)) = pack8(x);
       }
       if (w == 0) sG[lane] = Gl;
       if (rs == 0) {
@@ -1049,14 +1127,14 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
           xk[e] *= exp2_hw(-d);
           xd[e] = xk[e] * fkd[e];
         }
-        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pack8(xq);
-        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pack8(xk);
-        if (Lay::KD) *reinterpret_cast<uint4*>(sKd + row * PKP + cg * 8) = pack8(xd);
+        *reinterpret_cast<uint4*>(sQg + LT<KP>::off(row, cg * 8)) = pack8(xq);
+        *reinterpret_cast<uint4*>(sKg + LT<KP>::off(row, cg * 8)) = pack8(xk);
+        if (Lay::KD) *reinterpret_cast<uint4*>(sKd + LT<KP>::off(row, cg * 8)) = pack8(xd);
       }
 #pragma unroll
       for (int j = 0; j < VRPT; ++j) {
         const int row = vrs * VRPT + j;
-        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) =
+        *reinterpret_cast<uint4*>(sV + LT<VP>::off(row, vg * 8)) =
             mask16(R.v[j], (colB && row < len) ? ~0u : 0u);
       }
       if (rs == 0) {
@@ -1085,24 +1163,24 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       const int mi = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
       const int ni = t - mi * (mi + 1) / 2;
       f32x4 at = zero4();
-      mma_tile<bf16>(at, sQg + mi * 16 * PKP, PKP, sKg + ni * 16 * PKP, PKP, KP, lane);
+      mma_rr<KP, KP>(at, sQg, mi * 16, sKg, ni * 16, KP, ln);
       const int jj = ni * 16 + (lane & 15);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int ii = mi * 16 + 4 * (lane >> 4) + rr;
         float a = at[rr] * p.scale;
         if constexpr (SG) a *= exp2_hw(jj <= ii ? sG[ii] - sG[jj] : 0.f);
-        sA[ii * PA + jj] = from_f32<bf16>(jj <= ii ? a : 0.f);
+        sA[LT<HC>::off(ii, jj)] = from_f32<bf16>(jj <= ii ? a : 0.f);
       }
     }
+    const int oacc = LT<VP>::acc_pos(ln);
 #pragma unroll
     for (int j = 0; j < NTK; ++j) {
       const int kk = (kt0 + j) * 16 + (lane & 15);
       const float f = sRs[kk];
 #pragma unroll
       for (int i = 0; i < NTV; ++i) {
-        const int vv = (vt0 + i) * 16 + 4 * (lane >> 4);
-        *reinterpret_cast<uint2*>(sHk + kk * PVP + vv) =
+        *reinterpret_cast<uint2*>(sHk + LT<VP>::at((kt0 + j) * 16, (vt0 + i) * 16) + oacc) =
             make_uint2(pack2_bf16(acc[i][j][0] * f, acc[i][j][1] * f),
                        pack2_bf16(acc[i][j][2] * f, acc[i][j][3] * f));
       }
@@ -1117,14 +1195,12 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
         const int vt = vt0 + i;
         f32x4 ot = zero4();
         if constexpr (SG) {   // inter term first, scaled by 2^{G_i} (column i of o^T)
-          mma_tile2<bf16, true, false>(ot, sHk + vt * 16, PVP, sQg + it * 16 * PKP, PKP, KP,
-                                       lane);
+          mma_tr<VP, KP>(ot, sHk, vt * 16, sQg, it * 16, KP, ln);
           ot *= exp2_hw(sG[it * 16 + (lane & 15)]);
-          mma_tile2<bf16, true, false>(ot, sV + vt * 16, PVP, sA + it * 16 * PA, PA, HC, lane);
+          mma_tr<VP, HC>(ot, sV, vt * 16, sA, it * 16, HC, ln);
         } else {
-          mma_tile2<bf16, true, false>(ot, sV + vt * 16, PVP, sA + it * 16 * PA, PA, HC, lane);
-          mma_tile2<bf16, true, false>(ot, sHk + vt * 16, PVP, sQg + it * 16 * PKP, PKP, KP,
-                                       lane);
+          mma_tr<VP, HC>(ot, sV, vt * 16, sA, it * 16, HC, ln);
+          mma_tr<VP, KP>(ot, sHk, vt * 16, sQg, it * 16, KP, ln);
         }
         const int row = it * 16 + (lane & 15);
         const int vv = vt * 16 + 4 * (lane >> 4);
@@ -1134,11 +1210,11 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       }
     }
     if constexpr (SG)
-      state_update<NTV, NTK>(acc, sV2, PVP, sKg, PKP, sGam, vt0, kt0, lane);
+      state_update<NTV, NTK, VP, KP>(acc, sV2, sKg, sGam, vt0, kt0, ln);
     else if (Lay::KD)
-      state_update<NTV, NTK>(acc, sV, PVP, sKd, PKP, sGam, vt0, kt0, lane);
+      state_update<NTV, NTK, VP, KP>(acc, sV, sKd, sGam, vt0, kt0, ln);
     else
-      state_update<NTV, NTK>(acc, sV, PVP, sKg, PKP, sPre, vt0, kt0, lane, sPost);
+      state_update<NTV, NTK, VP, KP>(acc, sV, sKg, sPre, vt0, kt0, ln, sPost);
   };
 
   if (nsteps > 0 && PF == 2) {
@@ -1196,27 +1272,25 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 // SG (scalar gates): q2 = scale q 2^{G_i} for the dh update and G (one float per row).
 template <int KP, int VP, int NW, bool SG = false>
 struct HBLayout {
-  static constexpr int PKP = pitch_of<bf16>(KP), PVP = pitch_of<bf16>(VP),
-                       PA = pitch_of<bf16>(HC);
   static constexpr int PX = KP + 4;                // fp32 exchange pitch
   // small fp32 arrays first: the exchange aliases the tiles only
   // row groups of the dq / dk tiles (waves sharing a k tile)
   static constexpr int NKT = KP / 16, KTW = NKT > NW ? NKT / NW : 1, NRG = NW / (NKT / KTW);
-  static constexpr int tot = 0;                    // [NW][KP] cumsum wave totals
-  static constexpr int suf = tot + NW * KP * 4;    // [NRG][KP] dg row-group totals
+  static constexpr int tot = 0;                    // [NW][KP] cumsum wave totals (!SG)
+  static constexpr int suf = tot + (SG ? 0 : NW * KP * 4);   // [NRG][KP] dg row-group totals
   static constexpr int first = suf + NRG * KP * 4;
   static constexpr int fr = first + KP * 4;        // scale 2^r
   static constexpr int fe = fr + KP * 4;           // 2^{gamma-r}
   static constexpr int dkc = fe + KP * 4;          // [NRG][KP] sum_rows kg (v dh'^T)
   static constexpr int qg = dkc + NRG * KP * 4;
-  static constexpr int kg = qg + HC * PKP * 2;
-  static constexpr int v = kg + HC * PKP * 2;
-  static constexpr int dout = v + HC * PVP * 2;
-  static constexpr int dh = dout + HC * PVP * 2;   // dh' [k][v] bf16
-  static constexpr int a = dh + KP * PVP * 2;
-  static constexpr int da = a + HC * PA * 2;
-  static constexpr int q2 = da + HC * PA * 2;      // SG only
-  static constexpr int grow = q2 + (SG ? HC * PKP * 2 : 0);
+  static constexpr int kg = qg + LT<KP>::bytes(HC);
+  static constexpr int v = kg + LT<KP>::bytes(HC);
+  static constexpr int dout = v + LT<VP>::bytes(HC);
+  static constexpr int dh = dout + LT<VP>::bytes(HC);   // dh' [k][v] bf16
+  static constexpr int a = dh + LT<VP>::bytes(KP);
+  static constexpr int da = a + LT<HC>::bytes(HC);
+  static constexpr int q2 = da + LT<HC>::bytes(HC);     // SG only
+  static constexpr int grow = q2 + (SG ? LT<KP>::bytes(HC) : 0);
   static constexpr int end_tiles = grow + (SG ? HC * 4 : 0);
   // exchange [HC][PX] x 3 (dq, dk pre-factors, dg) from v on (qg, kg stay intact for the
   // epilogue); it may reach A / dA, which are therefore rewritten in full (zero upper tiles)
@@ -1235,7 +1309,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   using MV = HMap<VP, NT>;
   using Lay = HBLayout<KP, VP, NW, SG>;
   constexpr int RPT = M::RPT, VRPT = MV::RPT;
-  constexpr int PKP = Lay::PKP, PVP = Lay::PVP, PA = Lay::PA, PX = Lay::PX;
+  constexpr int PX = Lay::PX;
   constexpr int NKT = KP / 16, NVT = VP / 16;
   // dh tiles per wave: v by halves (w & 1), k split over the NW / 2 wave pairs
   constexpr int NTV = VP / 32, NTK = NKT / (NW / 2);
@@ -1373,11 +1447,10 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       gam_s = __shfl(Gl, len - 1);
 #pragma unroll
       for (int j = 0; j < NTK; ++j) {
-        const int kk = (kt0 + j) * 16 + (lane & 15);
 #pragma unroll
         for (int i = 0; i < NTV; ++i) {
-          const int vv = (vt0 + i) * 16 + 4 * (lane >> 4);
-          *reinterpret_cast<uint2*>(sDh + kk * PVP + vv) =
+          *reinterpret_cast<uint2*>(sDh + LT<VP>::at((kt0 + j) * 16, (vt0 + i) * 16) +
+                                    LT<VP>::acc_pos(lane)) =
               make_uint2(pack2_bf16(acc[i][j][0], acc[i][j][1]),
                          pack2_bf16(acc[i][j][2], acc[i][j][3]));
         }
@@ -1387,21 +1460,21 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         const int row = rs * RPT + j;
         const uint32_t m = (colA && row < len) ? ~0u : 0u;
         const uint4 qm = mask16(Rq[j], m);
-        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = qm;
-        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = mask16(Rk[j], m);
+        *reinterpret_cast<uint4*>(sQg + LT<KP>::off(row, cg * 8)) = qm;
+        *reinterpret_cast<uint4*>(sKg + LT<KP>::off(row, cg * 8)) = mask16(Rk[j], m);
         const float f = p.scale * exp2_hw(__shfl(Gl, row));
         float x[8];
         unpack8(qm, x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= f;
-        *reinterpret_cast<uint4*>(sQ2 + row * PKP + cg * 8) = pack8(x);
+        *reinterpret_cast<uint4*>(sQ2 + LT<KP>::off(row, cg * 8)) = pack8(x);
       }
 #pragma unroll
       for (int j = 0; j < VRPT; ++j) {
         const int row = vrs * VRPT + j;
         const uint32_t m = (colB && row < len) ? ~0u : 0u;
-        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) = mask16(Rv[j], m);
-        *reinterpret_cast<uint4*>(sDo + row * PVP + vg * 8) = mask16(Rd[j], m);
+        *reinterpret_cast<uint4*>(sV + LT<VP>::off(row, vg * 8)) = mask16(Rv[j], m);
+        *reinterpret_cast<uint4*>(sDo + LT<VP>::off(row, vg * 8)) = mask16(Rd[j], m);
       }
       if (w == 0) sG[lane] = Gl;
       if (rs == 0) {   // fr = scale 2^gamma (the 2^gamma sum_v h dh term), fe = 2^gamma
@@ -1435,8 +1508,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         const float fe = exp2_hw(0.5f * (gk - sFirst[kk]));
 #pragma unroll
         for (int i = 0; i < NTV; ++i) {
-          const int vv = (vt0 + i) * 16 + 4 * (lane >> 4);
-          *reinterpret_cast<uint2*>(sDh + kk * PVP + vv) =
+          *reinterpret_cast<uint2*>(sDh + LT<VP>::at((kt0 + j) * 16, (vt0 + i) * 16) +
+                                    LT<VP>::acc_pos(lane)) =
               make_uint2(pack2_bf16(acc[i][j][0] * fe, acc[i][j][1] * fe),
                          pack2_bf16(acc[i][j][2] * fe, acc[i][j][3] * fe));
         }
@@ -1458,16 +1531,16 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
           xq[e] *= exp2_hw(dd[j][e]);
           xk[e] *= exp2_hw(-dd[j][e]);
         }
-        *reinterpret_cast<uint4*>(sQg + row * PKP + cg * 8) = pack8(xq);
-        *reinterpret_cast<uint4*>(sKg + row * PKP + cg * 8) = pack8(xk);
+        *reinterpret_cast<uint4*>(sQg + LT<KP>::off(row, cg * 8)) = pack8(xq);
+        *reinterpret_cast<uint4*>(sKg + LT<KP>::off(row, cg * 8)) = pack8(xk);
       }
       gbad |= __ballot(dmax > kGateLimit2) != 0ull ? 1 : 0;
 #pragma unroll
       for (int j = 0; j < VRPT; ++j) {
         const int row = vrs * VRPT + j;
         const uint32_t m = (colB && row < len) ? ~0u : 0u;
-        *reinterpret_cast<uint4*>(sV + row * PVP + vg * 8) = mask16(Rv[j], m);
-        *reinterpret_cast<uint4*>(sDo + row * PVP + vg * 8) = mask16(Rd[j], m);
+        *reinterpret_cast<uint4*>(sV + LT<VP>::off(row, vg * 8)) = mask16(Rv[j], m);
+        *reinterpret_cast<uint4*>(sDo + LT<VP>::off(row, vg * 8)) = mask16(Rd[j], m);
       }
       if (rs == 0) {
         float b8[8], c8[8];
@@ -1489,9 +1562,9 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       f32x4 at = zero4();
       if (ni <= mi) {
         if (t < 16)
-          mma_tile<bf16>(at, sQg + mi * 16 * PKP, PKP, sKg + ni * 16 * PKP, PKP, KP, lane);
+          mma_rr<KP, KP>(at, sQg, mi * 16, sKg, ni * 16, KP, lane);
         else
-          mma_tile<bf16>(at, sDo + mi * 16 * PVP, PVP, sV + ni * 16 * PVP, PVP, VP, lane);
+          mma_rr<VP, VP>(at, sDo, mi * 16, sV, ni * 16, VP, lane);
       }
       bf16* dst = t < 16 ? sA : sdA;
       const int jj = ni * 16 + (lane & 15);
@@ -1500,7 +1573,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         const int ii = mi * 16 + 4 * (lane >> 4) + rr;
         float a = at[rr] * p.scale;
         if constexpr (SG) a *= exp2_hw(jj <= ii ? sG[ii] - sG[jj] : 0.f);   // A, dA decayed
-        dst[ii * PA + jj] = from_f32<bf16>(jj <= ii ? a : 0.f);
+        dst[LT<HC>::off(ii, jj)] = from_f32<bf16>(jj <= ii ? a : 0.f);
       }
     }
     // dq pre: fr do h^T (h fragments from HBM); dk pre: v dh'^T
@@ -1516,13 +1589,14 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       for (int f = 0; f < NHF; ++f) {
         Frag<bf16> yh;
         yh.d = mask16(Rh[t][f], (hk < K && f * 32 + 8 * (lane >> 4) < V) ? ~0u : 0u);
-        const Frag<bf16> ydh = ld_frag(sDh + hk * PVP + f * 32 + 8 * (lane >> 4));
+        const Frag<bf16> ydh =
+            ldr(sDh, LT<VP>::at((kq0 + t) * 16, f * 32) + LT<VP>::row_frag(lane));
         hdp[t] = dot8_bf16(yh.d, ydh.d, hdp[t]);
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
-          const int ro = (rt0 + i) * 16 + (lane & 15);
-          mma(aq[t][i], ld_frag(sDo + ro * PVP + f * 32 + 8 * (lane >> 4)), yh);
-          mma(ak[t][i], ld_frag(sV + ro * PVP + f * 32 + 8 * (lane >> 4)), ydh);
+          const int o = LT<VP>::at((rt0 + i) * 16, f * 32) + LT<VP>::row_frag(lane);
+          mma(aq[t][i], ldr(sDo, o), yh);
+          mma(ak[t][i], ldr(sV, o), ydh);
         }
       }
       hdp[t] += __shfl_xor(hdp[t], 16);
@@ -1546,8 +1620,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       dkc[t] = 0.f;
 #pragma unroll
       for (int i = 0; i < RT; ++i) {
-        const bf16* pk = sKg + ((rt0 + i) * 16 + 4 * (ln >> 4) + ((ln & 15) >> 2)) * PKP +
-                         (kq0 + t) * 16 + 4 * (ln & 3);
+        const bf16* pk = sKg + LT<KP>::at((rt0 + i) * 16, (kq0 + t) * 16) + LT<KP>::tr_rows4(ln);
         const s4_t kv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) s4_t*)(pk));
 #pragma unroll
@@ -1568,8 +1641,9 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       Frag<bf16> fk[HC / 32], fq[HC / 32];   // kg^T, qg^T of this k tile
 #pragma unroll
       for (int kk = 0; kk < HC / 32; ++kk) {
-        fk[kk] = ld_frag_t(sKg + kk * 32 * PKP + kq * 16, PKP, lane);
-        fq[kk] = ld_frag_t(sQg + kk * 32 * PKP + kq * 16, PKP, lane);
+        const int o = LT<KP>::at(kk * 32, kq * 16) + LT<KP>::tr_frag(lane);
+        fk[kk] = ldt<KP>(sKg, o);
+        fq[kk] = ldt<KP>(sQg, o);
       }
 #pragma unroll
       for (int i = 0; i < RT; ++i) {
@@ -1577,9 +1651,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         // dq += dA kg; dk += dA^T qg
 #pragma unroll
         for (int kk = 0; kk < HC / 32; ++kk) {
-          mma(aq[t][i], ld_frag(sdA + (ro + (lane & 15)) * PA + (lane >> 4) * 8 + kk * 32),
-              fk[kk]);
-          mma(ak[t][i], ld_frag_t(sdA + kk * 32 * PA + ro, PA, lane), fq[kk]);
+          mma(aq[t][i], ldr(sdA, LT<HC>::at(ro, kk * 32) + LT<HC>::row_frag(lane)), fk[kk]);
+          mma(ak[t][i], ldt<HC>(sdA, LT<HC>::at(kk * 32, ro) + LT<HC>::tr_frag(lane)), fq[kk]);
         }
       }
     }
@@ -1588,9 +1661,11 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       const int vd = vd0 + u;
       Frag<bf16> fh[KP / 32], fd[HC / 32];   // dh'^T, do^T of this v tile
 #pragma unroll
-      for (int kk = 0; kk < KP / 32; ++kk) fh[kk] = ld_frag_t(sDh + kk * 32 * PVP + vd * 16, PVP, lane);
+      for (int kk = 0; kk < KP / 32; ++kk)
+        fh[kk] = ldt<VP>(sDh, LT<VP>::at(kk * 32, vd * 16) + LT<VP>::tr_frag(lane));
 #pragma unroll
-      for (int kk = 0; kk < HC / 32; ++kk) fd[kk] = ld_frag_t(sDo + kk * 32 * PVP + vd * 16, PVP, lane);
+      for (int kk = 0; kk < HC / 32; ++kk)
+        fd[kk] = ldt<VP>(sDo, LT<VP>::at(kk * 32, vd * 16) + LT<VP>::tr_frag(lane));
 #pragma unroll
       for (int i = 0; i < JT; ++i) {
         const int jt = jt0 + i;
@@ -1598,11 +1673,11 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         f32x4 avt = zero4();
 #pragma unroll
         for (int kk = 0; kk < KP / 32; ++kk)
-          mma(avt, fh[kk], ld_frag(sKg + (jt * 16 + (lane & 15)) * PKP + (lane >> 4) * 8 + kk * 32));
+          mma(avt, fh[kk], ldr(sKg, LT<KP>::at(jt * 16, kk * 32) + LT<KP>::row_frag(lane)));
         if constexpr (SG) avt *= exp2_hw(gam_s - sG[jt * 16 + (lane & 15)]);
 #pragma unroll
         for (int kk = 0; kk < HC / 32; ++kk)
-          mma(avt, fd[kk], ld_frag_t(sA + kk * 32 * PA + jt * 16, PA, lane));
+          mma(avt, fd[kk], ldt<HC>(sA, LT<HC>::at(kk * 32, jt * 16) + LT<HC>::tr_frag(lane)));
         const int jj = jt * 16 + (lane & 15);
         const int vv = vd * 16 + 4 * (lane >> 4);
         if (jj < len && vv < V) {
@@ -1626,9 +1701,11 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
     for (int kk = 0; kk < HC; kk += 32) {
       Frag<bf16> x[NTV], y[NTK];
 #pragma unroll
-      for (int i = 0; i < NTV; ++i) x[i] = ld_frag_t(sDo + kk * PVP + (vt0 + i) * 16, PVP, lane);
+      for (int i = 0; i < NTV; ++i)
+        x[i] = ldt<VP>(sDo, LT<VP>::at(kk, (vt0 + i) * 16) + LT<VP>::tr_frag(lane));
 #pragma unroll
-      for (int j = 0; j < NTK; ++j) y[j] = ld_frag_t(sQd + kk * PKP + (kt0 + j) * 16, PKP, lane);
+      for (int j = 0; j < NTK; ++j)
+        y[j] = ldt<KP>(sQd, LT<KP>::at(kk, (kt0 + j) * 16) + LT<KP>::tr_frag(lane));
 #pragma unroll
       for (int i = 0; i < NTV; ++i)
 #pragma unroll
@@ -1669,8 +1746,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
         for (int i = RT - 1; i >= 0; --i) {
           const int r0 = (rt0 + i) * 16 + 4 * (lane >> 4);
-          const int off = ((rt0 + i) * 16 + 4 * (ln >> 4) + ((ln & 15) >> 2)) * PKP +
-                          (kq0 + t) * 16 + 4 * (ln & 3);
+          const int off = LT<KP>::at((rt0 + i) * 16, (kq0 + t) * 16) + LT<KP>::tr_rows4(ln);
           const s4_t qv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (__attribute__((address_space(3))) s4_t*)(sQg + off));
           const s4_t kv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
