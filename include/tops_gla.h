@@ -25,7 +25,9 @@
  *  - Work is enqueued on `stream` (a hipStream_t); nothing synchronizes the device.
  *  - Return value: TOPS_GLA_OK, or an error code with a message from
  *    tops_gla_last_error() (thread-local). Invalid arguments never launch a kernel.
- *  - chunk_size: 16, 32 or 64 for the MFMA kernels; any power of two for the cumsum.
+ *  - chunk_size: 16, 32 or 64 for the MFMA kernels; also 4 and 8 for tops_gla_chunk_fwd_h,
+ *    tops_gla_chunk_bwd_dh and tops_gla_chunk_fwd_o (float32 vector kernels, K <= 2048,
+ *    seg_ws unused); any power of two for the cumsum.
  */
 #ifndef TOPS_GLA_H_
 #define TOPS_GLA_H_

@@ -88,6 +88,19 @@ int make_seq(int64_t B, int64_t T, int64_t H, int chunk, const int32_t* cu,
   return TOPS_GLA_OK;
 }
 
+bool small_chunk(int chunk) { return chunk == 4 || chunk == 8; }
+
+// Chunk sizes 4 and 8 (the sub-functions' small-chunk kernels): no layout limits beyond K
+// (the output kernel holds 2 x chunk x K floats of the chunk in LDS).
+int check_small_common(int64_t K, int64_t V, int dtype) {
+  if (!dtype_ok(dtype)) return fail(TOPS_GLA_EINVAL, "dtype must be F32 (0) or BF16 (1)");
+  if (K <= 0 || V <= 0) return fail(TOPS_GLA_EINVAL, "K and V must be positive");
+  if (K > tops::small_chunk_max_k())
+    return fail(TOPS_GLA_EUNSUPPORTED, "K=%lld exceeds %d at chunk sizes 4 and 8",
+                (long long)K, tops::small_chunk_max_k());
+  return TOPS_GLA_OK;
+}
+
 int check_mfma_common(int64_t K, int64_t V, int chunk, int dtype) {
   if (!dtype_ok(dtype)) return fail(TOPS_GLA_EINVAL, "dtype must be F32 (0) or BF16 (1)");
   if (K <= 0 || V <= 0) return fail(TOPS_GLA_EINVAL, "K and V must be positive");
@@ -295,13 +308,31 @@ int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_c
                          int64_t V, int chunk_size, const int32_t* cu_seqlens,
                          const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
                          void* stream) {
-  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  const bool small = small_chunk(chunk_size);
+  int rc = small ? check_small_common(K, V, dtype) : check_mfma_common(K, V, chunk_size, dtype);
   if (rc) return rc;
   tops::SeqInfo si;
   rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
   if (rc) return rc;
   if ((k == nullptr || v == nullptr || g == nullptr) && B * T > 0)
     return fail(TOPS_GLA_EINVAL, "k, v and g must not be NULL");
+  if (small) {
+    tops::ScanArgs p = {};
+    p.a = k;
+    p.b = v;
+    p.g = g;
+    p.g_is_cumsum = g_is_cumsum != 0;
+    p.s_init = h0;
+    p.s_all = h;
+    p.s_final = ht;
+    p.scale = 1.f;
+    p.H = (int)H;
+    p.K = (int)K;
+    p.V = (int)V;
+    p.si = si;
+    return hip_status(tops::run_small_state_scan(p, false, dtype, (hipStream_t)stream),
+                      "chunk_fwd_h");
+  }
   if (use_head(dtype, chunk_size, K, V, g_is_cumsum != 0, {k, v, g, h0, h, ht})) {
     tops::HeadScanArgs s = {};
     s.a = k;
@@ -347,13 +378,31 @@ int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const v
                           int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
                           const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
                           void* stream) {
-  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  const bool small = small_chunk(chunk_size);
+  int rc = small ? check_small_common(K, V, dtype) : check_mfma_common(K, V, chunk_size, dtype);
   if (rc) return rc;
   tops::SeqInfo si;
   rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
   if (rc) return rc;
   if ((q == nullptr || dout == nullptr || g == nullptr) && B * T > 0)
     return fail(TOPS_GLA_EINVAL, "q, g and do must not be NULL");
+  if (small) {
+    tops::ScanArgs p = {};
+    p.a = q;
+    p.b = dout;
+    p.g = g;
+    p.g_is_cumsum = g_is_cumsum != 0;
+    p.s_init = dht;
+    p.s_all = dh;
+    p.s_final = dh0;
+    p.scale = scale;
+    p.H = (int)H;
+    p.K = (int)K;
+    p.V = (int)V;
+    p.si = si;
+    return hip_status(tops::run_small_state_scan(p, true, dtype, (hipStream_t)stream),
+                      "chunk_bwd_dh");
+  }
   if (use_head(dtype, chunk_size, K, V, g_is_cumsum != 0, {q, dout, g, dht, dh, dh0})) {
     tops::HeadScanArgs s = {};
     s.a = q;
@@ -399,7 +448,8 @@ int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void
                          int64_t V, int chunk_size, const int32_t* cu_seqlens,
                          const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
                          void* stream) {
-  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  const bool small = small_chunk(chunk_size);
+  int rc = small ? check_small_common(K, V, dtype) : check_mfma_common(K, V, chunk_size, dtype);
   if (rc) return rc;
   tops::SeqInfo si;
   rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
@@ -426,6 +476,8 @@ int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void
   p.K = (int)K;
   p.V = (int)V;
   p.si = si;
+  if (small)
+    return hip_status(tops::run_small_chunk_fwd_o(p, dtype, (hipStream_t)stream), "chunk_fwd_o");
   return hip_status(tops::run_chunk_fwd_o(p, dtype, (hipStream_t)stream), "chunk_fwd_o");
 }
 

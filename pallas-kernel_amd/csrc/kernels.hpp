@@ -39,6 +39,12 @@ struct FwdOArgs {
 };
 hipError_t run_chunk_fwd_o(const FwdOArgs& p, int dtype, hipStream_t st);
 
+// The same two steps at chunk sizes 4 and 8 (small_chunk.hip): the per-chunk states (forward
+// or reverse; no segment workspace) and the intra matrix / output combine.
+hipError_t run_small_state_scan(const ScanArgs& p, bool reverse, int dtype, hipStream_t st);
+hipError_t run_small_chunk_fwd_o(const FwdOArgs& p, int dtype, hipStream_t st);
+int small_chunk_max_k();
+
 // Fused forward: state scan + output in one sequential pass (chunk_fwd_fused.hip).
 struct FusedFwdArgs {
   const void *q, *k, *v, *g;

@@ -18,7 +18,7 @@ from ..._lib import SeqLayout, call, check_device, dtype_code, ptr, require, str
 
 __all__ = ["chunk_fwd_h_kernel", "chunk_fwd_h_ref", "chunk_bwd_dh_kernel", "chunk_bwd_dh_ref"]
 
-_CHUNKS = (16, 32, 64)
+_CHUNKS = (4, 8, 16, 32, 64)
 
 
 def _gate_cumsum(like, g, g_gamma, gk, C, cu):
@@ -46,13 +46,14 @@ def _check(T, C, cu):
 
 
 def _kernel_chunk(C):
-    """Kernel chunk for chunk size C: C itself (16, 32, 64) or 64 for multiples of 64 (the
+    """Kernel chunk for chunk size C: C itself (4, 8, 16, 32, 64) or 64 for multiples of 64 (the
     states at C-row boundaries are among the 64-row ones)."""
     if C in _CHUNKS:
         return C
     if C % 64 == 0:
         return 64
-    raise NotImplementedError(f"chunk_size {C}: the kernels take 16, 32, 64 or multiples of 64")
+    raise NotImplementedError(f"chunk_size {C}: the kernels take 4, 8, 16, 32, 64 or multiples "
+                              "of 64")
 
 
 def _rechunk_cumsum(gc, C, KC, cu):

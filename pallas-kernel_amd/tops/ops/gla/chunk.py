@@ -39,7 +39,8 @@ __all__ = [
     "chunk_gla_bwd_dqkg_ref",
 ]
 
-_MFMA_CHUNKS = (16, 32, 64)
+# chunk sizes of the per-chunk kernels (4 and 8 on the small-chunk vector kernels)
+_KERNEL_CHUNKS = (4, 8, 16, 32, 64)
 
 
 def _kernel_chunk(chunk_size: int) -> int:
@@ -389,8 +390,8 @@ def chunk_fwd_h(k, v, gk=None, h0=None, output_final_state=False, cu_seqlens_cpu
     if cu_seqlens_cpu is not None:
         require(all(c % C == 0 for c in _lib.to_list(cu_seqlens_cpu)),
                 "cu_seqlens must be multiples of chunk_size for chunk_fwd_h")
-    if C not in _MFMA_CHUNKS:
-        raise NotImplementedError(f"chunk_fwd_h: chunk_size {C} (kernels take 16, 32, 64)")
+    if C not in _KERNEL_CHUNKS:
+        raise NotImplementedError(f"chunk_fwd_h: chunk_size {C} (kernels take 4, 8, 16, 32, 64)")
     N = B if cu_seqlens_cpu is None else len(_lib.to_list(cu_seqlens_cpu)) - 1
     _shape_check(k, v=v, g=gk, h0=h0, N=N)
     dev = check_device(k, v, gk, h0)
@@ -418,7 +419,7 @@ def chunk_gla_fwd_intra_gk(q, k, g, scale, chunk_size=64):
     B, T, H, K = q.shape
     C = chunk_size
     require(T % C == 0)
-    if C not in _MFMA_CHUNKS:
+    if C not in _KERNEL_CHUNKS:
         raise NotImplementedError(f"chunk_gla_fwd_intra_gk: chunk_size {C}")
     _shape_check(q, k=k, g=g)
     dev = check_device(q, k, g)
@@ -441,7 +442,7 @@ def chunk_gla_fwd_o_gk(q, v, g, A, h, scale, cu_seqlens=None, chunk_indices=None
     V = v.shape[-1]
     C = chunk_size
     require(T % C == 0)
-    if C not in _MFMA_CHUNKS:
+    if C not in _KERNEL_CHUNKS:
         raise NotImplementedError(f"chunk_gla_fwd_o_gk: chunk_size {C}")
     _shape_check(q, v=v, g=g)
     require(tuple(A.shape) == (B, T, H, C),
@@ -503,8 +504,8 @@ def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_fi
     B, T, H, K = q.shape
     V = v.shape[-1]
     C = chunk_size
-    if C not in _MFMA_CHUNKS:
-        raise NotImplementedError(f"chunk_gla_fwd: chunk_size {C} (kernels take 16, 32, 64)")
+    if C not in _KERNEL_CHUNKS:
+        raise NotImplementedError(f"chunk_gla_fwd: chunk_size {C} (kernels take 4, 8, 16, 32, 64)")
     g = _gates(g, g_gamma, q)
     cu_list = None if cu_seqlens is None else _lib.to_list(cu_seqlens)
     N = B if cu_list is None else len(cu_list) - 1

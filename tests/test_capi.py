@@ -93,6 +93,20 @@ def test_lds_budget_reported():
     assert rc == 2 and "LDS" in msg
 
 
+def test_small_chunks_validated_on_the_host():
+    """Chunk sizes 4 and 8 reach the small-chunk kernels' own checks (K limit, NULL inputs)."""
+    for C in (4, 8):
+        rc, msg = _rc("tops_gla_chunk_fwd_o", NULL, NULL, NULL, NULL, 0, NULL, NULL, NULL, NULL,
+                      1.0, 1, 64, 1, 4096, 64, C, NULL, NULL, 1, 64 // C, 0, NULL)
+        assert rc == 2 and "K=4096" in msg, msg
+        rc, msg = _rc("tops_gla_chunk_fwd_h", NULL, NULL, NULL, 0, NULL, NULL, NULL, NULL, 0, 1,
+                      64, 1, 64, 64, C, NULL, NULL, 1, 64 // C, 1, NULL)
+        assert rc == 1 and "NULL" in msg, msg
+        rc, msg = _rc("tops_gla_chunk_bwd_dh", NULL, NULL, 0, NULL, NULL, NULL, NULL, NULL, 0,
+                      1.0, 1, 64, 1, 64, 64, C, NULL, NULL, 1, 64 // C + 1, 1, NULL)
+        assert rc == 1 and "NC" in msg, msg
+
+
 def test_recurrent_rejects_large_k():
     rc, msg = _rc("tops_gla_fused_recurrent_fwd", NULL, NULL, NULL, NULL, NULL, NULL, NULL,
                   NULL, 1.0, 0, 1, 8, 1, 1024, 64, NULL, 1, 1, 0, NULL)

@@ -313,6 +313,62 @@ def test_fwd_subfunctions_compose():
     check("fwd.ht", to_np(ht2), ht_ref, "f32")
 
 
+SMALL_FWD_CASES = [
+    # the reference table's chunk sizes 8 and 4 (test_pallas_chunk_bwd.py:43,45,73)
+    dict(B=1, T=128, H=2, K=32, V=64, seed=501, C=8, h0=True),
+    dict(B=1, T=64, H=2, K=32, V=64, seed=503, C=4),
+    dict(B=1, T=64, H=2, K=16, V=32, seed=511, C=8, cu=[0, 32, 64]),
+    # unaligned T and varlen (padded per segment by the orchestrator), K != V, wide K
+    dict(B=2, T=37, H=3, K=16, V=24, seed=512, C=8, h0=True),
+    dict(B=1, T=30, H=2, K=16, V=32, seed=513, C=4, cu=[0, 10, 30], h0=True),
+    dict(B=1, T=32, H=1, K=256, V=8, seed=514, C=8),
+]
+
+
+@pytest.mark.parametrize("cfg", SMALL_FWD_CASES,
+                         ids=[f"C{c['C']}-T{c['T']}-K{c['K']}{'-varlen' if c.get('cu') else ''}"
+                              for c in SMALL_FWD_CASES])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_small_chunk_forward_subfunctions(cfg, dtype):
+    """chunk_gla_fwd and its pieces (chunk_fwd_h, chunk_gla_fwd_intra_gk, chunk_gla_fwd_o_gk)
+    at chunk sizes 4 and 8 against the oracle at the same chunk size; chunk_bwd_dh on the
+    same gates."""
+    from tops.ops.common import chunk_h as CH
+
+    G = _gla()
+    B, T, H, K, V, C = (cfg[x] for x in "BTHKVC")
+    cu = cfg.get("cu")
+    N = len(cu) - 1 if cu else B
+    q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, cfg["seed"], h0=cfg.get("h0", False),
+                                          dht=True, N=N, dtype=dtype)
+    d = lambda x: to_dev(x, dtype)  # noqa: E731
+    tol = (lambda ref: 1e-4 * max(1.0, float(np.abs(ref).max()))) if dtype == "f32" \
+        else (lambda ref: None)  # noqa: E731
+    scale = K ** -0.5
+    out = G.chunk_gla_fwd(d(q), d(k), d(v), d(g), None, None, scale,
+                          to_dev(s0, "state"), True, cu_seqlens=cu, chunk_size=C)
+    ref = orc.chunk_gla_fwd(q, k, v, g, None, None, scale, s0, True, cu_seqlens=cu,
+                            chunk_size=C)
+    for name, a, b in zip(["g_cumsum", "A", "h", "ht", "o"], out, ref):
+        check(name, to_np(a), b, dtype, atol=tol(b))
+    if T % C or cu is not None:
+        return   # the pieces below take chunk-aligned, fixed-length inputs
+    gc_ref = ref[0]
+    gc = out[0]
+    h, ht = G.chunk_fwd_h(d(k), d(v), gc, to_dev(s0, "state"), True, chunk_size=C)
+    check("h", to_np(h), ref[2], dtype, atol=tol(ref[2]))
+    check("ht", to_np(ht), ref[3], dtype, atol=tol(ref[3]))
+    A = G.chunk_gla_fwd_intra_gk(d(q), d(k), gc, scale, chunk_size=C)
+    check("A", to_np(A), ref[1], dtype, atol=tol(ref[1]))
+    o = G.chunk_gla_fwd_o_gk(d(q), d(v), gc, A, h, scale, chunk_size=C)
+    check("o", to_np(o), ref[4], dtype, atol=tol(ref[4]))
+    dh_ref, dh0_ref = orc.chunk_bwd_dh(q, gc_ref, do, s0, dht, scale, chunk_size=C)
+    dh, dh0 = CH.chunk_bwd_dh_ref(d(q), None, None, gc, d(do), h0=to_dev(s0, "state"),
+                                  dht=to_dev(dht, "state"), scale=scale, chunk_size=C)
+    check("dh", to_np(dh), dh_ref, dtype, atol=tol(dh_ref))
+    check("dh0", to_np(dh0), dh0_ref, dtype, atol=tol(dh0_ref))
+
+
 def test_chunk_gla_fwd_and_bwd_orchestrators_padded():
     G = _gla()
     B, T, H, K, V, C = 1, 45, 2, 32, 64, 16
@@ -592,6 +648,10 @@ CH_CASES = [
     dict(B=1, T=256, H=2, K=32, V=64, C=64, S=128, gate="gk", seed=915),
     dict(B=1, T=192, H=2, K=32, V=64, C=64, gate="gk", seed=916, cu=[0, 64, 192]),
     dict(B=1, T=256, H=1, K=128, V=128, C=128, S=256, gate="g_gamma", seed=917),
+    # chunk sizes 4 and 8 (the small-chunk kernels)
+    dict(B=2, T=64, H=2, K=32, V=64, C=8, gate="gk", seed=918),
+    dict(B=1, T=64, H=2, K=16, V=32, C=4, S=16, gate="gk", seed=919),
+    dict(B=1, T=64, H=2, K=32, V=48, C=8, gate="g", seed=920, cu=[0, 24, 64]),
 ]
 
 
