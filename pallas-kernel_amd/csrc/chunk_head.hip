@@ -215,6 +215,15 @@ __device__ __forceinline__ void hload(uint4 (&r)[RPT], const bf16* __restrict__ 
   }
 }
 
+// Zeroes, in place, a thread's N rows (16-byte column groups) at or past `len` and every row
+// when its column group lies past the tile's width. Callers skip it (a uniform branch) for
+// full tiles: it only matters for a sequence's partial last chunk and for narrow heads.
+template <int N>
+__device__ __forceinline__ void mask_rows(uint4 (&r)[N], int row0, int len, bool col_ok) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) r[j] = mask16(r[j], (col_ok && row0 + j < len) ? ~0u : 0u);
+}
+
 // Chunk range of the block's segment.
 struct Seg {
   int seq, s, bos, eos, c0, cb, ce;
@@ -691,6 +700,15 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   auto body = [&](int step, Regs& R) {
     int t0, len, ci;
     span(step, t0, len, ci);
+    // zero the rows past the step and the columns past the tile (a sequence's partial last
+    // step, narrow heads); full steps skip it
+    if (!(len == CR && K == KP && Vw == VP)) {
+      if constexpr (!PRE) {
+        mask_rows<RPT>(R.a, rs * RPT, len, colA);
+        if constexpr (!SG) mask_rows<RPT>(R.g, rs * RPT, len, colA);
+      }
+      mask_rows<VRPT>(R.b, vrs * VRPT, len, colB);
+    }
     float gt[RPT][8], gam[8];
     if constexpr (PRE) {
       __syncthreads();   // the previous step's reads of the tiles are done
@@ -720,8 +738,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
       scan_cumsum_f<KP, NT, CR, REV>(gt, gam, sTot, cg, lane, w);
     } else {
 #pragma unroll
-      for (int j = 0; j < RPT; ++j)
-        unpack8(mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u), gt[j]);
+      for (int j = 0; j < RPT; ++j) unpack8(R.g[j], gt[j]);
       scan_cumsum_f<KP, NT, CR, REV>(gt, gam, sTot, cg, lane, w);
     }
     if constexpr (!PRE) {
@@ -729,7 +746,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
       for (int j = 0; j < RPT; ++j) {
         const int row = rs * RPT + j;
         float x[8];
-        unpack8(mask16(R.a[j], (colA && row < len) ? ~0u : 0u), x);
+        unpack8(R.a[j], x);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           x[e] *= REV ? p.scale * exp2_hw(gt[j][e]) : exp2_hw(gt[j][e]);
@@ -739,8 +756,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 #pragma unroll
     for (int j = 0; j < VRPT; ++j) {
       const int row = vrs * VRPT + j;
-      *reinterpret_cast<uint4*>(sB + LT<VP>::off(row, vg * 8)) =
-          mask16(R.b[j], (colB && row < len) ? ~0u : 0u);
+      *reinterpret_cast<uint4*>(sB + LT<VP>::off(row, vg * 8)) = R.b[j];
     }
     if (rs == TRS) {
       float eg[8];
@@ -1100,12 +1116,16 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
         st_f8(sRs + cg * 8, er);
       }
     } else {
+      // zero the rows past the chunk and the columns past the tile (a sequence's partial last
+      // chunk, narrow heads); full chunks skip it
+      if (!(len == HC && K == KP && Vw == VP)) {
+        mask_rows<RPT>(R.g, rs * RPT, len, colA);
+        mask_rows<RPT>(R.q, rs * RPT, len, colA);
+        mask_rows<RPT>(R.k, rs * RPT, len, colA);
+        mask_rows<VRPT>(R.v, vrs * VRPT, len, colB);
+      }
       float gt[RPT][8], gam[8], first[8];
-      uint4 gmk[RPT];
-#pragma unroll
-      for (int j = 0; j < RPT; ++j)
-        gmk[j] = mask16(R.g[j], (colA && rs * RPT + j < len) ? ~0u : 0u);
-      head_cumsum<KP>(gmk, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
+      head_cumsum<KP>(R.g, gt, gam, first, sTot, sFirst, cg, rs, lane, w);
       float r[8], fkd[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -1115,10 +1135,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
         const int row = rs * RPT + j;
-        const uint32_t m = (colA && row < len) ? ~0u : 0u;
         float xq[8], xk[8], xd[8];
-        unpack8(mask16(R.q[j], m), xq);
-        unpack8(mask16(R.k[j], m), xk);
+        unpack8(R.q[j], xq);
+        unpack8(R.k[j], xk);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float d = gt[j][e] - r[e];
@@ -1134,8 +1153,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 #pragma unroll
       for (int j = 0; j < VRPT; ++j) {
         const int row = vrs * VRPT + j;
-        *reinterpret_cast<uint4*>(sV + LT<VP>::off(row, vg * 8)) =
-            mask16(R.v[j], (colB && row < len) ? ~0u : 0u);
+        *reinterpret_cast<uint4*>(sV + LT<VP>::off(row, vg * 8)) = R.v[j];
       }
       if (rs == 0) {
         float eg[8], er[8];
@@ -1369,6 +1387,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   const int vd0 = (w % NVG) * VTW, jt0 = (w / NVG) * JT;   // dv^T tiles
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
+  const bool full_kv = K == KP && V == VP;   // no column of the tiles lies past the head
   int gbad = 0;          // uniform: a chunk had a factor beyond the gate-range limit
   f32x4 acc[NTV][NTK];   // dh[v][k]
   {
@@ -1488,13 +1507,21 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         st_f8(sFe + cg * 8, c8);
       }
     } else {
+      // zero the rows past the chunk and the columns past the tile (a sequence's partial last
+      // chunk, narrow heads); full chunks skip it
+      if (!(len == HC && full_kv)) {
+        mask_rows<RPT>(Rg, rs * RPT, len, colA);
+        mask_rows<RPT>(Rq, rs * RPT, len, colA);
+        mask_rows<RPT>(Rk, rs * RPT, len, colA);
+        mask_rows<VRPT>(Rv, vrs * VRPT, len, colB);
+        mask_rows<VRPT>(Rd, vrs * VRPT, len, colB);
+      }
       uint4 qm[RPT], km[RPT];
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
-        const uint32_t m = (colA && rs * RPT + j < len) ? ~0u : 0u;
-        unpack8(mask16(Rg[j], m), dd[j]);
-        qm[j] = mask16(Rq[j], m);
-        km[j] = mask16(Rk[j], m);
+        unpack8(Rg[j], dd[j]);
+        qm[j] = Rq[j];
+        km[j] = Rk[j];
       }
       float gam[8], first[8];
       head_cumsum_f<KP, NT>(dd, gam, first, sTot, sFirst, cg, rs, lane, w);
@@ -1538,9 +1565,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
       for (int j = 0; j < VRPT; ++j) {
         const int row = vrs * VRPT + j;
-        const uint32_t m = (colB && row < len) ? ~0u : 0u;
-        *reinterpret_cast<uint4*>(sV + LT<VP>::off(row, vg * 8)) = mask16(Rv[j], m);
-        *reinterpret_cast<uint4*>(sDo + LT<VP>::off(row, vg * 8)) = mask16(Rd[j], m);
+        *reinterpret_cast<uint4*>(sV + LT<VP>::off(row, vg * 8)) = Rv[j];
+        *reinterpret_cast<uint4*>(sDo + LT<VP>::off(row, vg * 8)) = Rd[j];
       }
       if (rs == 0) {
         float b8[8], c8[8];
@@ -1588,7 +1614,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
       for (int f = 0; f < NHF; ++f) {
         Frag<bf16> yh;
-        yh.d = mask16(Rh[t][f], (hk < K && f * 32 + 8 * (lane >> 4) < V) ? ~0u : 0u);
+        yh.d = full_kv ? Rh[t][f]
+                       : mask16(Rh[t][f], (hk < K && f * 32 + 8 * (lane >> 4) < V) ? ~0u : 0u);
         const Frag<bf16> ydh =
             ldr(sDh, LT<VP>::at((kq0 + t) * 16, f * 32) + LT<VP>::row_frag(lane));
         hdp[t] = dot8_bf16(yh.d, ydh.d, hdp[t]);
