@@ -1283,9 +1283,11 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 // fragments are read straight from HBM (16 bytes per lane).
 // Waves: dq/dk own KTW k tiles x RT row tiles, dv^T VTW v tiles x JT row tiles, dh as in
 // the scans. The next chunk's gates (needed first, by the cumsum) are fetched during the
-// epilogue; its q, k, v, do and h when it starts (the cumsum runs under those loads). There
-// are no registers to hold more of the next chunk in flight: prefetching q and k as well
-// measured slower (spills).
+// epilogue; its q, k, v and do when it starts (the cumsum runs under those loads) and h --
+// needed last, in the second phase -- once dh' is in LDS, so that the vector memory path
+// takes a chunk's loads in two smaller bursts (all waves issuing 14 loads at once kept them
+// stalled for about 10 % of the chunk). There are no registers to hold more of the next
+// chunk in flight: prefetching q and k (or v and do) as well spilled and measured slower.
 // ---------------------------------------------------------------------------
 // SG (scalar gates): q2 = scale q 2^{G_i} for the dh update and G (one float per row).
 template <int KP, int VP, int NW, bool SG = false>
@@ -1449,7 +1451,6 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
     chunk_of(step, t0, len, ci);
     issue_qk(step);
     issue_vd(step);
-    issue_h(step);
     // lane / thread indices for the per-lane offsets of the dv, dq, dk, dg stores and of the
     // transposed kg / qg reads: taken through opaque() every chunk so that those offsets are
     // recomputed in the loop (hoisted, they are long-lived registers the kernel cannot hold)
@@ -1474,6 +1475,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
                          pack2_bf16(acc[i][j][2], acc[i][j][3]));
         }
       }
+      issue_h(step);
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
         const int row = rs * RPT + j;
@@ -1541,6 +1543,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
                          pack2_bf16(acc[i][j][2] * fe, acc[i][j][3] * fe));
         }
       }
+      issue_h(step);
       float r[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = 0.5f * (first[e] + gam[e]);
