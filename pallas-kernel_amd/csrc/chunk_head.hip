@@ -201,6 +201,53 @@ __device__ __forceinline__ void st8(void* base, uint32_t off, const uint2& x) {
   *reinterpret_cast<uint2*>(reinterpret_cast<char*>(base) + off) = x;
 }
 
+// 16 bytes, nontemporal. The kernels' outputs are written once and not read again in the
+// launch: streamed past the L2 they leave no dirty lines for the writeback at the end of
+// the launch, which otherwise holds up the next launch (on MI355X 15-20 us after the fused
+// kernels). Only for whole 128-byte row pieces: partial lines written this way are slow.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st16_nt(void* base, uint32_t off, const uint4& x) {
+  const u32x4_t v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(base) + off));
+}
+// st16_nt when `nt`, else st16. The empty asm statements keep the two stores from being
+// merged into one (which would drop the nontemporal hint).
+__device__ __forceinline__ void st16_sel(void* base, uint32_t off, const uint4& x, bool nt) {
+  if (nt) {
+    st16_nt(base, off, x);
+  } else {
+    asm volatile("");
+    st16(base, off, x);
+    asm volatile("");
+  }
+}
+
+// A wave's 16 x 64 bf16 block written to HBM as whole rows: staged tile by tile
+// (stage_tile: a 16 x 16 tile whose lane holds 4 consecutive columns, 4 (lane >> 4) + 0..3,
+// of row lane & 15) in the wave's own 16 x 72 LDS area `stg` (no other wave touches it; a
+// wave's LDS accesses complete in order), then read back 16 bytes a lane, 8 lanes a
+// 128-byte row (rows_out), and stored at dst + row * ld + column (elements): nontemporally
+// when `nt` (whole lines: ld, the columns and dst 64-element aligned). Rows >= nrows and
+// columns >= ncols (a multiple of 8) are not stored.
+constexpr int kStgPitch = 72;                       // 144-byte rows: 16-byte aligned
+constexpr int kStgBytes = 16 * kStgPitch * 2;       // per wave
+__device__ __forceinline__ void stage_tile(bf16* stg, int i, const uint2& x, int lane) {
+  *reinterpret_cast<uint2*>(stg + (lane & 15) * kStgPitch + i * 16 + 4 * (lane >> 4)) = x;
+}
+__device__ __forceinline__ void rows_out(const bf16* stg, bf16* dst, uint32_t ld, int nrows,
+                                         int ncols, bool nt, int lane) {
+  __builtin_amdgcn_wave_barrier();
+  const int c = 8 * (lane & 7);
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const int r = (lane >> 3) + 8 * hf;
+    const uint4 y = *reinterpret_cast<const uint4*>(stg + r * kStgPitch + c);
+    const uint32_t off = ((uint32_t)r * ld + (uint32_t)c) * 2u;
+    if (r < nrows && c < ncols) st16_sel(dst, off, y, nt);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
 // RPT rows x 16 bytes starting at (row0, col0) of a row-major bf16 tile at `base` with
 // row stride rs elements. Unconditional: rows are clamped to len-1 and the column to w-8
 // (w % 8 == 0, w >= 8); the caller masks what it consumes.
@@ -952,6 +999,11 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   constexpr int PF = KP > 128 ? 1 : 2;
   static_assert(!PRE || (!SG && !Lay::KD), "PRE: wide heads with per-element gates");
   static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
+  // o and h out as whole rows (stage_tile, rows_out), staged in the kg tile: it is read by A only
+  // (the state update takes kd), so it is free from the barrier before the products to the
+  // next chunk's gating, which comes after the cumsum's barrier
+  constexpr bool ROWS =
+      !SG && !PRE && Lay::KD && NTV == 4 && HNW * kStgBytes <= LT<KP>::bytes(HC);
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
   bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
@@ -1000,6 +1052,8 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   }
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
+  bf16* sStg = sKg + w * (kStgBytes / 2);   // ROWS: this wave's staging area
+  const bool ntv = V % 64 == 0;              // ROWS: the row pieces are whole lines
   float dmax = 0.f;   // largest |g~ - r| of the factors (base 2): the gate-range check
   f32x4 acc[NTV][NTK];
   {
@@ -1052,9 +1106,23 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     const int len = min(HC, sg.eos - t0);
     // h_n to HBM first: the vector memory path is idle here (the next chunk's loads are
     // issued at the end of the gating, and stores queued behind them wait for them)
-    if (hout)
-      store_state_bf16<NTV, NTK>(acc, hout + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K, Vw,
-                                 vt0, kt0, lane, V);
+    if (hout) {
+      bf16* hb = hout + ((long)(sg.c0 + ci) * H + hh) * KV + cv;
+      if constexpr (ROWS) {
+#pragma unroll
+        for (int j = 0; j < NTK; ++j) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            stage_tile(sStg, i,
+                       make_uint2(pack2_bf16(acc[i][j][0], acc[i][j][1]),
+                                  pack2_bf16(acc[i][j][2], acc[i][j][3])), ln);
+          rows_out(sStg, hb + (long)((kt0 + j) * 16) * V + vt0 * 16, (uint32_t)V,
+                   K - (kt0 + j) * 16, Vw - vt0 * 16, ntv, ln);
+        }
+      } else {
+        store_state_bf16<NTV, NTK>(acc, hb, K, Vw, vt0, kt0, lane, V);
+      }
+    }
 
     // ---- (1) cumsum, gating ----
     float Gl = 0.f, gam_s = 0.f;   // SG: G of row `lane`, the chunk's total (base 2)
@@ -1220,12 +1288,20 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
           mma_tr<VP, HC>(ot, sV, vt * 16, sA, it * 16, HC, ln);
           mma_tr<VP, KP>(ot, sHk, vt * 16, sQg, it * 16, KP, ln);
         }
-        const int row = it * 16 + (lane & 15);
-        const int vv = vt * 16 + 4 * (lane >> 4);
-        if (row < len && vv < Vw)
-          st8(o + (long)t0 * rsV + (long)hh * V + cv, ((uint32_t)row * (uint32_t)rsV + vv) * 2u,
-              make_uint2(pack2_bf16(ot[0], ot[1]), pack2_bf16(ot[2], ot[3])));
+        const uint2 ox = make_uint2(pack2_bf16(ot[0], ot[1]), pack2_bf16(ot[2], ot[3]));
+        if constexpr (ROWS) {
+          stage_tile(sStg, i, ox, ln);
+        } else {
+          const int row = it * 16 + (lane & 15);
+          const int vv = vt * 16 + 4 * (lane >> 4);
+          if (row < len && vv < Vw)
+            st8(o + (long)t0 * rsV + (long)hh * V + cv,
+                ((uint32_t)row * (uint32_t)rsV + vv) * 2u, ox);
+        }
       }
+      if constexpr (ROWS)
+        rows_out(sStg, o + (long)(t0 + it * 16) * rsV + (long)hh * V + cv + vt0 * 16,
+                 (uint32_t)rsV, len - it * 16, Vw - vt0 * 16, ntv, ln);
     }
     if constexpr (SG)
       state_update<NTV, NTK, VP, KP>(acc, sV2, sKg, sGam, vt0, kt0, ln);
@@ -1390,6 +1466,9 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
   const bool full_kv = K == KP && V == VP;   // no column of the tiles lies past the head
+  // dq, dk, dg stored nontemporally where their row pieces are whole 128-byte lines (dv, in
+  // the accumulator layout, goes out in 32-byte pieces: plain stores)
+  const bool ntk = K % 64 == 0;
   int gbad = 0;          // uniform: a chunk had a factor beyond the gate-range limit
   f32x4 acc[NTV][NTK];   // dh[v][k]
   {
@@ -1828,8 +1907,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       const uint32_t a =
           ((uint32_t)((tl / M::NCG) * RPT + j) * (uint32_t)rsK + (tl % M::NCG) * 8) * 2u;
       if (st_ok) {
-        st16(dq + b0, a, pack8(xq));
-        st16(dk + b0, a, pack8(xk));
+        st16_sel(dq + b0, a, pack8(xq), ntk);
+        st16_sel(dk + b0, a, pack8(xk), ntk);
       }
       if (p.dg) {
         float xg[8];
@@ -1849,7 +1928,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
             }
           }
         }
-        if (st_ok) st16(dg + b0, a, pack8(xg));
+        if (st_ok) st16_sel(dg + b0, a, pack8(xg), ntk);
       }
     }
   }
