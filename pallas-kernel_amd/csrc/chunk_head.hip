@@ -1001,9 +1001,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
   // o and h out as whole rows (stage_tile, rows_out), staged in the kg tile: it is read by A only
   // (the state update takes kd), so it is free from the barrier before the products to the
-  // next chunk's gating, which comes after the cumsum's barrier
-  constexpr bool ROWS =
-      !SG && !PRE && Lay::KD && NTV == 4 && HNW * kStgBytes <= LT<KP>::bytes(HC);
+  // next chunk's gating, which comes after the cumsum's barrier. Scalar gates stage in the kd
+  // tile, which they do not use.
+  constexpr bool ROWS = !PRE && Lay::KD && NTV == 4 && HNW * kStgBytes <= LT<KP>::bytes(HC);
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
   bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
@@ -1052,7 +1052,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   }
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
-  bf16* sStg = sKg + w * (kStgBytes / 2);   // ROWS: this wave's staging area
+  bf16* sStg = (SG ? sKd : sKg) + w * (kStgBytes / 2);   // ROWS: this wave's staging area
   const bool ntv = V % 64 == 0;              // ROWS: the row pieces are whole lines
   float dmax = 0.f;   // largest |g~ - r| of the factors (base 2): the gate-range check
   f32x4 acc[NTV][NTK];
