@@ -1568,7 +1568,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
     hload<RPT>(Rq, q + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     hload<RPT>(Rk, k + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
   };
-  auto issue_qkg = [&](int step) {
+  auto issue_g = [&](int step) {
     int t0, len, ci;
     chunk_of(step, t0, len, ci);
     const long oa = (long)t0 * rsK + (long)hh * K;
@@ -1598,7 +1598,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   };
 
 
-  if (nsteps > 0) issue_qkg(0);
+  if (nsteps > 0) issue_g(0);
   for (int step = 0; step < nsteps; ++step) {
     int t0, len, ci;
     chunk_of(step, t0, len, ci);
@@ -1618,6 +1618,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       __syncthreads();   // the previous chunk's epilogue reads are done
       const float Gl = sg_row_cumsum(Rs, lane, len);
       gam_s = __shfl(Gl, len - 1);
+      if (step + 1 < nsteps) issue_g(step + 1);   // the next chunk's gates, as below
 #pragma unroll
       for (int j = 0; j < NTK; ++j) {
 #pragma unroll
@@ -1680,6 +1681,10 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       }
       float gam[8], first[8];
       head_cumsum_f<KP, NT>(dd, gam, first, sTot, sFirst, cg, rs, lane, w);
+      // the next chunk's gates: their registers are free once the cumsum has them, and a
+      // whole chunk ahead they have arrived by the next cumsum (issued in the epilogue they
+      // had not: head_bwd 364 -> 351 us)
+      if (step + 1 < nsteps) issue_g(step + 1);
       // gamma of this lane's dh rows from the wave totals (same order of sums as gam)
 #pragma unroll
       for (int j = 0; j < NTK; ++j) {
@@ -1955,10 +1960,6 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       }
     }
     __syncthreads();
-
-    // the next chunk's q, k and gates (needed first: cumsum and gating): their registers
-    // are free from here on, and the loads run under the epilogue
-    if (step + 1 < nsteps) issue_qkg(step + 1);
 
     // ---- (5) epilogue: dq, dk, dg rows ----
     // (the next chunk's first barrier, in its gating, comes before anything overwrites the
