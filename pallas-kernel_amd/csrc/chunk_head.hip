@@ -348,19 +348,22 @@ __device__ __forceinline__ void head_cumsum_f(GateRows<KP, NT, CR>& gt, float (&
   if (lane >= 64 - M::NCG) st_f8(sTot + w * KP + cg * 8, x);   // wave total
   if (rs == 0) st_f8(sFirst + cg * 8, gt[0]);
   __syncthreads();
-  // earlier waves' totals (w is wave-uniform: plain loops, no per-lane selects)
+  // earlier waves' totals (w is wave-uniform: plain loops, no per-lane selects); the lane's
+  // column offset taken through opaque() so that it is formed here, not held (and spilled)
+  // across the callers' chunk loops
   float off[8], t[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) off[e] = 0.f;
+  const int c8 = (int)opaque((uint32_t)(cg * 8));
   for (int ww = 0; ww < w; ++ww) {
-    ld_f8(sTot + ww * KP + cg * 8, t);
+    ld_f8(sTot + ww * KP + c8, t);
 #pragma unroll
     for (int e = 0; e < 8; ++e) off[e] += t[e];
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) gam[e] = off[e];
   for (int ww = w; ww < NT / 64; ++ww) {
-    ld_f8(sTot + ww * KP + cg * 8, t);
+    ld_f8(sTot + ww * KP + c8, t);
 #pragma unroll
     for (int e = 0; e < 8; ++e) gam[e] += t[e];
   }
@@ -1443,6 +1446,11 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 template <int KP, int VP, int NW, bool SG = false>
 struct HBLayout {
   static constexpr int PX = KP + 4;                // fp32 exchange pitch
+  // element (r, c) of an exchange array: the float4 halves of each 8-column group swapped in
+  // rows with bit 1 set. A wave's row reads (8 columns a lane, two rows two apart) then hit
+  // every bank once per group of 16 lanes (2-way conflicts unswizzled); the accumulator-layout
+  // writes (rows r, r + 4, r + 8, r + 12) stay conflict-free.
+  __device__ static int xo(int r, int c) { return r * PX + (c ^ (4 * ((r >> 1) & 1))); }
   // small fp32 arrays first: the exchange aliases the tiles only
   // row groups of the dq / dk tiles (waves sharing a k tile)
   static constexpr int NKT = KP / 16, KTW = NKT > NW ? NKT / NW : 1, NRG = NW / (NKT / KTW);
@@ -1471,6 +1479,15 @@ struct HBLayout {
   static constexpr int end_x = xg + HC * PX * 4;
   static constexpr int bytes = end_tiles > end_x ? end_tiles : end_x;
 };
+
+// The 8 floats of columns c..c+7 (c a multiple of 8) of row r of an exchange array (HBLayout::xo).
+template <class Lay>
+__device__ __forceinline__ void ld_x8(const float* x, int r, int c, float (&v)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(x + Lay::xo(r, c));
+  const float4 b = *reinterpret_cast<const float4*>(x + Lay::xo(r, c + 4));
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
 
 template <int KP, int VP, int NT, bool SG>
 __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
@@ -1924,8 +1941,8 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int ro = (rt0 + i) * 16 + 4 * (lane >> 4) + rr;
-          XQ[ro * PX + hk] = aq[t][i][rr];
-          XK[ro * PX + hk] = ak[t][i][rr];
+          XQ[Lay::xo(ro, hk)] = aq[t][i][rr];
+          XK[Lay::xo(ro, hk)] = ak[t][i][rr];
         }
       }
       if (p.dg) {   // uniform: absent for scalar gates without a gate gradient
@@ -1950,7 +1967,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
           float tot;
           const float later = rows4_suffix(x[0], lane, &tot) - x[0] + carry;
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) XG[(r0 + rr) * PX + hk] = x[rr] + later;
+          for (int rr = 0; rr < 4; ++rr) XG[Lay::xo(r0 + rr, hk)] = x[rr] + later;
           carry += tot;
         }
         if (Lay::NRG > 1 && lane < 16) {
@@ -1967,9 +1984,10 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
       const int row = rs * RPT + j;
+      const int xr = (tl / M::NCG) * RPT + j, xc = (tl % M::NCG) * 8;   // row, cg * 8
       float xq[8], xk[8];
-      ld_f8(XQ + row * PX + cg * 8, xq);
-      ld_f8(XK + row * PX + cg * 8, xk);
+      ld_x8<Lay>(XQ, xr, xc, xq);
+      ld_x8<Lay>(XK, xr, xc, xk);
       if constexpr (!SG) {   // scalar gates: the factors are in already
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -1987,7 +2005,7 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       }
       if (p.dg) {
         float xg[8];
-        ld_f8(XG + row * PX + cg * 8, xg);
+        ld_x8<Lay>(XG, xr, xc, xg);
         if constexpr (Lay::NRG > 1) {   // later row groups' totals; every group's dk sum
           const int rg = row / (RT * 16);
           float t8[8];
