@@ -1350,6 +1350,17 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     // ---- (3) o^T = v^T A^T + h'^T qg^T (wave: v tiles of half w&1, row tile w>>1) ----
     {
       const int it = w >> 1;
+      // per-element gates: the row fragments of A and qg of row tile it, shared by the wave's
+      // v tiles, read once (scalar gates read them per tile: hoisted they measured slower)
+      Frag<bf16> fa[SG ? 1 : HC / 32], fq[SG ? 1 : KP / 32];
+      if constexpr (!SG) {
+#pragma unroll
+        for (int kk = 0; kk < HC / 32; ++kk)
+          fa[kk] = ldr(sA, LT<HC>::at(it * 16, kk * 32) + LT<HC>::row_frag(ln));
+#pragma unroll
+        for (int kk = 0; kk < KP / 32; ++kk)
+          fq[kk] = ldr(sQg, LT<KP>::at(it * 16, kk * 32) + LT<KP>::row_frag(ln));
+      }
 #pragma unroll
       for (int i = 0; i < NTV; ++i) {
         const int vt = vt0 + i;
@@ -1358,9 +1369,13 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
           mma_tr<VP, KP>(ot, sHk, vt * 16, sQg, it * 16, KP, ln);
           ot *= exp2_hw(sG[it * 16 + (lane & 15)]);
           mma_tr<VP, HC>(ot, sV, vt * 16, sA, it * 16, HC, ln);
-        } else {
-          mma_tr<VP, HC>(ot, sV, vt * 16, sA, it * 16, HC, ln);
-          mma_tr<VP, KP>(ot, sHk, vt * 16, sQg, it * 16, KP, ln);
+        } else {   // v^T A^T + h'^T qg^T
+#pragma unroll
+          for (int kk = 0; kk < HC / 32; ++kk)
+            mma(ot, ldt<VP>(sV, LT<VP>::at(kk * 32, vt * 16) + LT<VP>::tr_frag(ln)), fa[kk]);
+#pragma unroll
+          for (int kk = 0; kk < KP / 32; ++kk)
+            mma(ot, ldt<VP>(sHk, LT<VP>::at(kk * 32, vt * 16) + LT<VP>::tr_frag(ln)), fq[kk]);
         }
         const uint2 ox = make_uint2(pack2_bf16(ot[0], ot[1]), pack2_bf16(ot[2], ot[3]));
         if constexpr (ROWS) {
