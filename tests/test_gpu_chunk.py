@@ -59,6 +59,10 @@ FWD_CASES = [
     # tile), segmented (1024 tokens -> 2 segments x 3 V tiles)
     dict(B=1, T=1024, H=2, K=256, V=160, seed=804, C=64, h0=True, gate_div=16.0),
     dict(B=1, T=300, H=2, K=200, V=72, seed=805, C=64, h0=True),
+    # V in (64, 128] but not a multiple of 64 (whole-row o / h stores with plain stores, a
+    # partial second v half), K not a multiple of 64; partial last chunk, two segments
+    dict(B=1, T=1100, H=2, K=112, V=96, seed=830, C=64, h0=True, gate_div=8.0),
+    dict(B=2, T=700, H=1, K=64, V=80, seed=831, C=64),
     # K = 200 (a partial last 64-column K slice) with three V tiles: per-chunk gating
     # workspace, partial last chunk; 1100 tokens -> two segments streaming it
     dict(B=1, T=300, H=2, K=200, V=200, seed=806, C=64, h0=True, gate_div=4.0),
@@ -203,6 +207,10 @@ BWD_CASES = [
     dict(B=2, T=1536, H=1, K=96, V=40, seed=813, C=64, dht=True, gate_div=4.0),
     # 128 x 64 state tiles: the backward's fp32 exchange must not alias the A / dA tiles
     dict(B=1, T=1024, H=2, K=128, V=64, seed=814, C=64, h0=True, dht=True, gate_div=4.0),
+    # K, V not multiples of 64: the dq / dk / dg rows and o / h rows are not whole lines (plain
+    # stores), a partial second v half, a partial last chunk, two segments
+    dict(B=1, T=1100, H=2, K=112, V=96, seed=832, C=64, h0=True, dht=True, gate_div=8.0),
+    dict(B=2, T=700, H=1, K=64, V=80, seed=833, C=64, dht=True),
     # wide head: full-head forward and dh scan (V tiles, segments), per-chunk gradients
     dict(B=1, T=1024, H=2, K=256, V=192, seed=815, C=64, h0=True, dht=True, gate_div=16.0),
     # K = 200, three V tiles: the scans and the dv kernel stream the per-chunk gating (a
