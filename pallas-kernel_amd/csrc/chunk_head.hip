@@ -132,6 +132,22 @@ __device__ __forceinline__ void mma_rr(f32x4& acc, const bf16* X, int xr0, const
   const int oy = LT<WY>::at(yr0, 0) + LT<WY>::row_frag(lane);
   for (int kk = 0; kk < klen; kk += 32) mma(acc, ldr(X, ox + kk), ldr(Y, oy + kk));
 }
+// The same over K = KL columns (a compile-time depth), every fragment read before the
+// products
+template <int WX, int WY, int KL>
+__device__ __forceinline__ void mma_rr_b(f32x4& acc, const bf16* X, int xr0, const bf16* Y,
+                                         int yr0, int lane) {
+  const int ox = LT<WX>::at(xr0, 0) + LT<WX>::row_frag(lane);
+  const int oy = LT<WY>::at(yr0, 0) + LT<WY>::row_frag(lane);
+  Frag<bf16> x[KL / 32], y[KL / 32];
+#pragma unroll
+  for (int kk = 0; kk < KL / 32; ++kk) {
+    x[kk] = ldr(X, ox + kk * 32);
+    y[kk] = ldr(Y, oy + kk * 32);
+  }
+#pragma unroll
+  for (int kk = 0; kk < KL / 32; ++kk) mma(acc, x[kk], y[kk]);
+}
 // acc += X^T Y^T-rows: X stored [k][m] (columns xc0.. of a WX-wide tile, transposed
 // fragments), Y rows yr0.. of a WY-wide tile stored [n][k] (row fragments), over klen k
 template <int WX, int WY>
@@ -1323,7 +1339,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       const int mi = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
       const int ni = t - mi * (mi + 1) / 2;
       f32x4 at = zero4();
-      mma_rr<KP, KP>(at, sQg, mi * 16, sKg, ni * 16, KP, ln);
+      mma_rr_b<KP, KP, KP>(at, sQg, mi * 16, sKg, ni * 16, ln);
       const int jj = ni * 16 + (lane & 15);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
@@ -1361,23 +1377,46 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
         for (int kk = 0; kk < KP / 32; ++kk)
           fq[kk] = ldr(sQg, LT<KP>::at(it * 16, kk * 32) + LT<KP>::row_frag(ln));
       }
+      f32x4 ot[NTV];
+      if constexpr (SG) {
+#pragma unroll
+        for (int i = 0; i < NTV; ++i) {   // inter term first, scaled by 2^{G_i} (column i of o^T)
+          const int vt = vt0 + i;
+          ot[i] = zero4();
+          mma_tr<VP, KP>(ot[i], sHk, vt * 16, sQg, it * 16, KP, ln);
+          ot[i] *= exp2_hw(sG[it * 16 + (lane & 15)]);
+          mma_tr<VP, HC>(ot[i], sV, vt * 16, sA, it * 16, HC, ln);
+        }
+      } else {
+        // v^T A^T + h'^T qg^T for the wave's NTV v tiles at once: per k step the NTV
+        // transposed fragments are read together, then the NTV products (independent
+        // accumulators) issue back to back
+#pragma unroll
+        for (int i = 0; i < NTV; ++i) ot[i] = zero4();
+#pragma unroll
+        for (int kk = 0; kk < HC / 32; ++kk) {
+          Frag<bf16> x[NTV];
+#pragma unroll
+          for (int i = 0; i < NTV; ++i)
+            x[i] = ldt<VP>(sV, LT<VP>::at(kk * 32, (vt0 + i) * 16) + LT<VP>::tr_frag(ln));
+#pragma unroll
+          for (int i = 0; i < NTV; ++i) mma(ot[i], x[i], fa[kk]);
+        }
+#pragma unroll
+        for (int kk = 0; kk < KP / 32; ++kk) {
+          Frag<bf16> x[NTV];
+#pragma unroll
+          for (int i = 0; i < NTV; ++i)
+            x[i] = ldt<VP>(sHk, LT<VP>::at(kk * 32, (vt0 + i) * 16) + LT<VP>::tr_frag(ln));
+#pragma unroll
+          for (int i = 0; i < NTV; ++i) mma(ot[i], x[i], fq[kk]);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < NTV; ++i) {
         const int vt = vt0 + i;
-        f32x4 ot = zero4();
-        if constexpr (SG) {   // inter term first, scaled by 2^{G_i} (column i of o^T)
-          mma_tr<VP, KP>(ot, sHk, vt * 16, sQg, it * 16, KP, ln);
-          ot *= exp2_hw(sG[it * 16 + (lane & 15)]);
-          mma_tr<VP, HC>(ot, sV, vt * 16, sA, it * 16, HC, ln);
-        } else {   // v^T A^T + h'^T qg^T
-#pragma unroll
-          for (int kk = 0; kk < HC / 32; ++kk)
-            mma(ot, ldt<VP>(sV, LT<VP>::at(kk * 32, vt * 16) + LT<VP>::tr_frag(ln)), fa[kk]);
-#pragma unroll
-          for (int kk = 0; kk < KP / 32; ++kk)
-            mma(ot, ldt<VP>(sHk, LT<VP>::at(kk * 32, vt * 16) + LT<VP>::tr_frag(ln)), fq[kk]);
-        }
-        const uint2 ox = make_uint2(pack2_bf16(ot[0], ot[1]), pack2_bf16(ot[2], ot[3]));
+        const uint2 ox =
+            make_uint2(pack2_bf16(ot[i][0], ot[i][1]), pack2_bf16(ot[i][2], ot[i][3]));
         if constexpr (ROWS) {
           stage_tile(sStg, i, ox, ln);
         } else {
@@ -1781,9 +1820,9 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
       f32x4 at = zero4();
       if (ni <= mi) {
         if (t < 16)
-          mma_rr<KP, KP>(at, sQg, mi * 16, sKg, ni * 16, KP, lane);
+          mma_rr_b<KP, KP, KP>(at, sQg, mi * 16, sKg, ni * 16, lane);
         else
-          mma_rr<VP, VP>(at, sDo, mi * 16, sV, ni * 16, VP, lane);
+          mma_rr_b<VP, VP, VP>(at, sDo, mi * 16, sV, ni * 16, lane);
       }
       bf16* dst = t < 16 ? sA : sdA;
       const int jj = ni * 16 + (lane & 15);
@@ -1812,11 +1851,18 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         const Frag<bf16> ydh =
             ldr(sDh, LT<VP>::at((kq0 + t) * 16, f * 32) + LT<VP>::row_frag(lane));
         hdp[t] = dot8_bf16(yh.d, ydh.d, hdp[t]);
+        // the RT row fragments of do and of v read together, then the 2 RT products
+        Frag<bf16> xd[RT], xv[RT];
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
           const int o = LT<VP>::at((rt0 + i) * 16, f * 32) + LT<VP>::row_frag(lane);
-          mma(aq[t][i], ldr(sDo, o), yh);
-          mma(ak[t][i], ldr(sV, o), ydh);
+          xd[i] = ldr(sDo, o);
+          xv[i] = ldr(sV, o);
+        }
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          mma(aq[t][i], xd[i], yh);
+          mma(ak[t][i], xv[i], ydh);
         }
       }
       hdp[t] += __shfl_xor(hdp[t], 16);
@@ -1891,13 +1937,18 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         const int jt = jt0 + i;
         // dv^T = dh'^T kg^T + do^T A (scalar gates: (dh^T k^T) 2^{gamma - G_j} + do^T A)
         f32x4 avt = zero4();
+        Frag<bf16> xk[KP / 32], xa[HC / 32];   // kg rows, A^T rows of row tile jt
 #pragma unroll
         for (int kk = 0; kk < KP / 32; ++kk)
-          mma(avt, fh[kk], ldr(sKg, LT<KP>::at(jt * 16, kk * 32) + LT<KP>::row_frag(lane)));
-        if constexpr (SG) avt *= exp2_hw(gam_s - sG[jt * 16 + (lane & 15)]);
+          xk[kk] = ldr(sKg, LT<KP>::at(jt * 16, kk * 32) + LT<KP>::row_frag(lane));
 #pragma unroll
         for (int kk = 0; kk < HC / 32; ++kk)
-          mma(avt, fd[kk], ldt<HC>(sA, LT<HC>::at(kk * 32, jt * 16) + LT<HC>::tr_frag(lane)));
+          xa[kk] = ldt<HC>(sA, LT<HC>::at(kk * 32, jt * 16) + LT<HC>::tr_frag(lane));
+#pragma unroll
+        for (int kk = 0; kk < KP / 32; ++kk) mma(avt, fh[kk], xk[kk]);
+        if constexpr (SG) avt *= exp2_hw(gam_s - sG[jt * 16 + (lane & 15)]);
+#pragma unroll
+        for (int kk = 0; kk < HC / 32; ++kk) mma(avt, fd[kk], xa[kk]);
         const int jj = jt * 16 + (lane & 15);
         const int vv = vd * 16 + 4 * (lane >> 4);
         if (jj < len && vv < V) {
