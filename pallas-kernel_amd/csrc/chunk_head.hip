@@ -760,7 +760,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   };
   // Pass 1 issues a step's loads in three parts at three points of the steps before it: the
   // gates two steps ahead (after the gating), the a rows one step ahead (after the cumsum),
-  // the b rows one step ahead (after the barrier). Issued at once, a step's 12 loads per
+  // the b rows one step ahead (after the update). Issued at once, a step's 12 loads per
   // thread stall the issuing waves until the loads before them have drained, and nothing is
   // issued while the waves compute; spread out they keep the CU's memory path busy under
   // the cumsum, the gating and the update (pass 1 73 -> 55-62 us, and 24 fewer VGPRs).
@@ -867,13 +867,13 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     else
       issue(step + 2, R);
     __syncthreads();
-    if constexpr (SPLIT) issue_b(step + 1, Rn);
     if constexpr (CR == HC) {
       if (s_all)   // state entering the chunk (forward) / leaving it (reverse)
         store_state_bf16<NTV, NTK>(acc, s_all + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K,
                                    Vw, vt0, kt0, lane, V);
     }
     state_update<NTV, NTK, VP, KP, CR>(acc, sB, sA, sGam, vt0, kt0, lane);
+    if constexpr (SPLIT) issue_b(step + 1, Rn);
   };
 
   if (nsteps > 0) {
@@ -1154,9 +1154,10 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
 
   // Per-element gates: a chunk's loads go out in three parts, as in the scans' pass 1: q and
   // k one chunk ahead (after the cumsum), the gates two chunks ahead (after the gating), v
-  // one chunk ahead (after the barrier that follows the gating). All at once they stall the
-  // issuing waves until the loads before them drain, with nothing issued under the products
-  // (head_fwd 217 -> 195 us, 6 fewer VGPRs).
+  // one chunk ahead (after the barrier before the output products). All at once they stall
+  // the issuing waves until the loads before them drain, with nothing issued under the
+  // products (head_fwd 217 -> 195 us, 6 fewer VGPRs; v after the gating's barrier instead:
+  // 3 us slower, q and k after the gating: 7 us slower).
   constexpr bool SPLIT = !PRE && !SG && PF == 2;
   auto span1 = [&](int step, int& t0, int& len) {
     const int st = min(step, nsteps - 1);
@@ -1332,7 +1333,6 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     else
       issue(step + PF, R);
     __syncthreads();
-    if constexpr (SPLIT) issue_v(step + 1, Rn);
 
     // ---- (2) A (lower tiles), h' = scale 2^r h into LDS ----
     for (int t = w; t < (PRE ? 0 : 10); t += HNW) {
@@ -1362,6 +1362,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       }
     }
     __syncthreads();
+    if constexpr (SPLIT) issue_v(step + 1, Rn);
 
     // ---- (3) o^T = v^T A^T + h'^T qg^T (wave: v tiles of half w&1, row tile w>>1) ----
     {
