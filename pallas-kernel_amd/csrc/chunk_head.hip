@@ -1562,6 +1562,11 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   static_assert(Lay::NRG == NW / NKG, "row groups of the dq / dk tiles");
   constexpr int NHF = VP / 32;                      // h fragments per lane
   static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
+  // dv out as whole rows (stage_tile, rows_out): a wave takes row tile w >> 1 and the v tiles
+  // of half w & 1, staged in the v tile, which nothing reads after the A / dA products.
+  // Plain, its 32-byte pieces leave dirty L2 lines whose writeback delays the next launch
+  // (the next forward's pass 1: 11 us).
+  constexpr bool ROWS = VP == 128 && NW == 8 && NW * kStgBytes <= LT<VP>::bytes(HC);
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* sTot = reinterpret_cast<float*>(smem + Lay::tot);
   float* sSuf = reinterpret_cast<float*>(smem + Lay::suf);
@@ -1612,9 +1617,9 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 
   const int vt0 = (w & 1) * NTV, kt0 = (w >> 1) * NTK;
   const bool full_kv = K == KP && V == VP;   // no column of the tiles lies past the head
-  // dq, dk, dg stored nontemporally where their row pieces are whole 128-byte lines (dv, in
-  // the accumulator layout, goes out in 32-byte pieces: plain stores)
-  const bool ntk = K % 64 == 0;
+  // dq, dk, dg (16 lanes a row) and dv (staged as whole rows, ROWS) stored nontemporally
+  // where their row pieces are whole 128-byte lines
+  const bool ntk = K % 64 == 0, ntv = V % 64 == 0;
   int gbad = 0;          // uniform: a chunk had a factor beyond the gate-range limit
   f32x4 acc[NTV][NTK];   // dh[v][k]
   {
@@ -1923,8 +1928,55 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
         }
       }
     }
+    if constexpr (ROWS) {
+      // dv^T of row tile w >> 1 and the four v tiles of half w & 1 (independent
+      // accumulators, each k step's transposed fragments read together), staged in the v
+      // tile and stored as whole rows
+      const int jt = w >> 1;
+      Frag<bf16> fk[KP / 32], fa[HC / 32];   // kg rows, A^T rows of row tile jt
 #pragma unroll
-    for (int u = 0; u < VTW; ++u) {
+      for (int kk = 0; kk < KP / 32; ++kk)
+        fk[kk] = ldr(sKg, LT<KP>::at(jt * 16, kk * 32) + LT<KP>::row_frag(lane));
+#pragma unroll
+      for (int kk = 0; kk < HC / 32; ++kk)
+        fa[kk] = ldt<HC>(sA, LT<HC>::at(kk * 32, jt * 16) + LT<HC>::tr_frag(lane));
+      f32x4 avt[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) avt[u] = zero4();
+#pragma unroll
+      for (int kk = 0; kk < KP / 32; ++kk) {
+        Frag<bf16> x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          x[u] = ldt<VP>(sDh, LT<VP>::at(kk * 32, ((w & 1) * 4 + u) * 16) + LT<VP>::tr_frag(lane));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) mma(avt[u], x[u], fk[kk]);
+      }
+      if constexpr (SG) {
+        const float f = exp2_hw(gam_s - sG[jt * 16 + (lane & 15)]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) avt[u] *= f;
+      }
+#pragma unroll
+      for (int kk = 0; kk < HC / 32; ++kk) {
+        Frag<bf16> x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          x[u] = ldt<VP>(sDo, LT<VP>::at(kk * 32, ((w & 1) * 4 + u) * 16) + LT<VP>::tr_frag(lane));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) mma(avt[u], x[u], fa[kk]);
+      }
+      bf16* sStg = sV + w * (kStgBytes / 2);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        stage_tile(sStg, u,
+                   make_uint2(pack2_bf16(avt[u][0], avt[u][1]), pack2_bf16(avt[u][2], avt[u][3])),
+                   ln);
+      rows_out(sStg, dv + (long)(t0 + jt * 16) * rsV + (long)hh * V + (w & 1) * 64,
+               (uint32_t)rsV, len - jt * 16, V - (w & 1) * 64, ntv, ln);
+    }
+#pragma unroll
+    for (int u = 0; u < (ROWS ? 0 : VTW); ++u) {
       const int vd = vd0 + u;
       Frag<bf16> fh[KP / 32], fd[HC / 32];   // dh'^T, do^T of this v tile
 #pragma unroll
