@@ -170,6 +170,13 @@ __device__ __forceinline__ uint32_t opaque(uint32_t x) {
   return x;
 }
 
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima) as a real instruction, which the
+// compiler's wait-count tracking takes into account. Placed before a chunk loop it clears the
+// loads issued ahead of the loop: the counter is in order and counts stores as well, so a
+// wait the compiler sizes for the loop's entry, where only those loads are outstanding,
+// would otherwise also wait, on every later pass, for the stores of the pass before.
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // acc + sum of the products of 8 bf16 pairs (v_dot2c_f32_bf16: fp32 accumulation)
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float dot8_bf16(uint4 a, uint4 b, float acc) {
@@ -1676,6 +1683,10 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
 
 
   if (nsteps > 0) issue_g(0);
+  // the first gates waited for here: otherwise the loop's wait for the gates (in the
+  // cumsum), sized for this entry, counts back over the previous chunk's stores and
+  // holds every chunk until those have completed
+  vm_wait_all();
   for (int step = 0; step < nsteps; ++step) {
     int t0, len, ci;
     chunk_of(step, t0, len, ci);

@@ -152,8 +152,21 @@ __device__ __forceinline__ void put(void* p, long i, float x) {
 
 }  // namespace
 
+// Whether any block of the full-head kernels flagged (sequence seq, head hh): the pair's
+// flags (one per segment and V tile) read by the lanes of every wave at once, so that an
+// unflagged block leaves after a single load. Uniform over the block.
+__device__ __forceinline__ bool pair_flagged(const GateFlags& f, int seq, int hh, int H) {
+  int x = 0;
+  for (int i = (int)(threadIdx.x & 63); i < f.ns * f.vt; i += 64)
+    x |= f.p[((long)seq * f.ns + i / f.vt) * H * f.vt + (long)hh * f.vt + i % f.vt];
+  return __ballot(x != 0) != 0ull;
+}
+
+// One unit L = (sequence, head) x NCT + column tile of a scan, run by the whole block. The
+// LDS arrays are function-scope statics: units that one block runs in turn share them, with
+// a barrier between.
 template <typename T, typename TO, int NCG, int RPT>
-__global__ __launch_bounds__(RNT) void rec_scan_kernel(RecScanArgs p) {
+__device__ __forceinline__ void rec_scan_unit(const RecScanArgs& p, const int L) {
   using Cf = RecCfg<NCG, RPT>;
   constexpr int CB = Cf::CB, RP = Cf::RP, TB = Cf::TB, RGW = Cf::RGW;
   static_assert(RPT == 2 || RPT % 4 == 0, "rows are read as float2 / float4");
@@ -178,19 +191,9 @@ __global__ __launch_bounds__(RNT) void rec_scan_kernel(RecScanArgs p) {
   const int NCT = (C + CB - 1) / CB;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int ct = L % NCT;
   const int sh = L / NCT;
   const int seq = sh / H, hh = sh % H;
-  if (p.flags.p) {   // fallback launch: only the (sequence, head) pairs a block flagged
-    // the pair's flags (one per segment and column tile) read by the lanes of every wave
-    // at once, so an unflagged block returns after a single load
-    int f = 0;
-    for (int i = lane; i < p.flags.ns * p.flags.vt; i += 64)
-      f |= p.flags.p[((long)seq * p.flags.ns + i / p.flags.vt) * H * p.flags.vt +
-                     (long)hh * p.flags.vt + i % p.flags.vt];
-    if (__ballot(f != 0) == 0ull) return;   // uniform over the block: before any barrier
-  }
   int bos, eos;
   seq_bounds(p.si, seq, bos, eos);
   const int n = eos - bos;
@@ -479,6 +482,44 @@ __global__ __launch_bounds__(RNT) void rec_scan_kernel(RecScanArgs p) {
   }
 }
 
+template <typename T, typename TO, int NCG, int RPT>
+__global__ __launch_bounds__(RNT) void rec_scan_kernel(RecScanArgs p) {
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  if (p.flags.p) {   // fallback launch: only the (sequence, head) pairs a block flagged
+    const int NCT = (p.C + NCG * 4 - 1) / (NCG * 4);
+    if (!pair_flagged(p.flags, L / NCT / p.H, (L / NCT) % p.H, p.H)) return;
+  }
+  rec_scan_unit<T, TO, NCG, RPT>(p, L);
+}
+
+// Every column tile of one (sequence, head) pair of a scan, in turn.
+template <typename T, typename TO, int NCG, int RPT>
+__device__ __forceinline__ void rec_scan_pair(const RecScanArgs& p, int pair) {
+  const int NCT = (p.C + NCG * 4 - 1) / (NCG * 4);
+#pragma unroll 1
+  for (int ct = 0; ct < NCT; ++ct) {
+    rec_scan_unit<T, TO, NCG, RPT>(p, pair * NCT + ct);
+    __syncthreads();   // LDS reuse; the next scan's reads of this one's global writes
+  }
+}
+
+// The backward's gate-range fallback in one launch: block = (sequence, head) pair; a
+// flagged pair runs the three scans of run_recurrent_bwd in order, each over all of its
+// column tiles (the second reads the first's dq and final state, written by this block);
+// an unflagged one leaves after reading its flags. Three launches with a block per column
+// tile cost about 4 us each even when nothing is flagged.
+template <typename T, typename TO, int NCG, int RPT>
+__global__ __launch_bounds__(RNT) void rec_bwd_fallback_kernel(RecScanArgs s1, RecScanArgs s2,
+                                                               RecScanArgs s3) {
+  const int pair = xcd_remap(blockIdx.x, gridDim.x);
+  if (!pair_flagged(s1.flags, pair / s1.H, pair % s1.H, s1.H)) return;
+  // each scan named directly (an array of pointers to the arguments would copy them to
+  // scratch memory, whose set-up slows this launch and the next even when nothing is flagged)
+  rec_scan_pair<T, TO, NCG, RPT>(s1, pair);
+  rec_scan_pair<T, TO, NCG, RPT>(s2, pair);
+  rec_scan_pair<T, TO, NCG, RPT>(s3, pair);
+}
+
 namespace {
 
 template <typename T, typename TO, int NCG, int RPT>
@@ -512,6 +553,35 @@ hipError_t run_scan(const RecScanArgs& p, int dtype, int o_dtype, hipStream_t st
   if (dtype == DT_BF16 && o_dtype == DT_F32) return dispatch_scan<bf16, float>(p, st);
   if (dtype == DT_BF16 && o_dtype == DT_BF16) return dispatch_scan<bf16, bf16>(p, st);
   if (dtype == DT_F32 && o_dtype == DT_F32) return dispatch_scan<float, float>(p, st);
+  return hipErrorInvalidValue;
+}
+
+template <typename T, typename TO, int RPT>
+hipError_t launch_bwd_fallback(const RecScanArgs& s1, const RecScanArgs& s2,
+                               const RecScanArgs& s3, hipStream_t st) {
+  const long blocks = (long)s1.si.N * s1.H;
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL((rec_bwd_fallback_kernel<T, TO, 8, RPT>), dim3((unsigned)blocks), dim3(RNT),
+                     0, st, s1, s2, s3);
+  return hipGetLastError();
+}
+
+// 32-column tiles (the scans' layout for up to 512 rows) for the rows of every scan
+template <typename T, typename TO>
+hipError_t dispatch_bwd_fallback(const RecScanArgs& s1, const RecScanArgs& s2,
+                                 const RecScanArgs& s3, hipStream_t st) {
+  const int R = s1.R > s3.R ? s1.R : s3.R;
+  if (R <= 128) return launch_bwd_fallback<T, TO, 2>(s1, s2, s3, st);
+  if (R <= 256) return launch_bwd_fallback<T, TO, 4>(s1, s2, s3, st);
+  if (R <= 512) return launch_bwd_fallback<T, TO, 8>(s1, s2, s3, st);
+  return hipErrorInvalidValue;
+}
+
+hipError_t run_bwd_fallback(const RecScanArgs& s1, const RecScanArgs& s2, const RecScanArgs& s3,
+                            int dtype, int o_dtype, hipStream_t st) {
+  if (dtype == DT_BF16 && o_dtype == DT_F32) return dispatch_bwd_fallback<bf16, float>(s1, s2, s3, st);
+  if (dtype == DT_BF16 && o_dtype == DT_BF16) return dispatch_bwd_fallback<bf16, bf16>(s1, s2, s3, st);
+  if (dtype == DT_F32 && o_dtype == DT_F32) return dispatch_bwd_fallback<float, float>(s1, s2, s3, st);
   return hipErrorInvalidValue;
 }
 
@@ -567,8 +637,6 @@ hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, int o_dtype, hipStr
   s.C = p.K;
   s.dir = p.reverse ? 1 : 0;
   s.flags = p.flags;
-  hipError_t e = run(s);
-  if (e != hipSuccess) return e;
 
   // 2. dk (+ dgk) : S = dh^T, rows V, columns K, opposite direction
   RecScanArgs s2 = s;
@@ -589,8 +657,6 @@ hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, int o_dtype, hipStr
     s2.hfin = need_ht ? p.ht_ws : nullptr;
     s2.dg = p.dgk;
   }
-  e = run(s2);
-  if (e != hipSuccess) return e;
 
   // 3. dv (+ dgv, dh0) : S = dh, rows K, columns V, opposite direction
   RecScanArgs s3{};
@@ -620,7 +686,12 @@ hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, int o_dtype, hipStr
     s3.hfin = need_ht ? p.ht_ws : nullptr;
     s3.dg = p.dgv;
   }
-  return run(s3);
+  // the chunked backward's gate-range fallback: one launch for the three scans
+  if (p.flags.p) return run_bwd_fallback(s, s2, s3, dtype, o_dtype, st);
+  hipError_t e = run(s);
+  if (e == hipSuccess) e = run(s2);
+  if (e == hipSuccess) e = run(s3);
+  return e;
 }
 
 }  // namespace tops
