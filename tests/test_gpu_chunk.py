@@ -745,6 +745,10 @@ STRONG_CASES = [
          only_seq=2, h0=True, dht=True),
     # just inside the limit (ranges of about 120-130): the chunked kernels themselves
     dict(B=1, T=1024, H=2, K=128, V=128, seed=865, mul=2.4, h0=True, dht=True),
+    # no final-state gradient (the fallback's first scan keeps no final state), with and
+    # without an initial state; one strong pair among four
+    dict(B=2, T=1100, H=2, K=128, V=128, seed=866, mul=5.0, only=(0, 1), h0=True, dht=False),
+    dict(B=1, T=700, H=2, K=64, V=64, seed=867, mul=5.0, h0=False, dht=False),
 ]
 
 
@@ -777,10 +781,14 @@ def test_strong_gates(cfg):
     q, k, v, g, s0, do, dht, cu = _strong_inputs(cfg)
     K = cfg["K"]
     tq, tk, tv, tg = (to_dev(x, "bf16").requires_grad_() for x in (q, k, v, g))
-    th0 = to_dev(s0, "state").requires_grad_()
+    th0 = to_dev(s0, "state") if s0 is not None else None
+    if th0 is not None:
+        th0.requires_grad_()
     o, ht = G.chunk_gla(tq, tk, tv, tg, initial_state=th0, output_final_state=True,
                         cu_seqlens=None if cu is None else torch.tensor(cu), chunk_size=64)
-    loss = (o.float() * to_dev(do, "f32")).sum() + (ht * to_dev(dht, "state")).sum()
+    loss = (o.float() * to_dev(do, "f32")).sum()
+    if dht is not None:
+        loss = loss + (ht * to_dev(dht, "state")).sum()
     loss.backward()
     torch.cuda.synchronize()
     on, hn = orc.naive_recurrent_gla(q, k, v, g, initial_state=s0, output_final_state=True,
@@ -791,4 +799,5 @@ def test_strong_gates(cfg):
                             cu_seqlens=cu, chunk_size=16)
     for name, x, r in zip(["dq", "dk", "dv", "dg"], (tq, tk, tv, tg), ref):
         check(name, to_np(x.grad), r, "bf16")
-    check("dh0", to_np(th0.grad), ref[4], "bf16")
+    if th0 is not None:
+        check("dh0", to_np(th0.grad), ref[4], "bf16")
