@@ -497,6 +497,49 @@ def test_north_star_shape_slices():
         check("dh0", to_np(th0.grad[b:b + 1, h:h + 1]), ref[4], "bf16")
 
 
+def test_north_star_shape_all_slices_vs_torch_fp32():
+    """C4 (B4 T8192 H16 K=V=128, bf16, chunk 64) fwd+bwd, every one of the 64 (b, h) slices
+    against the float32 torch chunked GLA (``tests/torch_ref.py``, pinned to the oracle by
+    ``test_torch_ref.py``) run on the GPU from the same bf16 inputs, gradients by torch
+    autograd. Bar per slice and output: max-abs error / max |ref| of that slice <= 2e-2."""
+    from gla_cases import BF16_RTOL_MAX
+    from torch_ref import chunk_gla_torch
+
+    G = _gla()
+    B, T, H, K, V = 4, 8192, 16, 128, 128
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    mk = lambda *s: torch.randn(*s, generator=gen, device="cuda")  # noqa: E731
+    q, k, v = (mk(B, T, H, K).to(torch.bfloat16) for _ in range(3))
+    g = (torch.nn.functional.logsigmoid(mk(B, T, H, K)) / 16).to(torch.bfloat16)
+    h0 = mk(B, H, K, V) * 0.1
+    do = mk(B, T, H, V).to(torch.bfloat16)
+    dht = mk(B, H, K, V) * 0.1
+    leaves = [x.clone().requires_grad_() for x in (q, k, v, g, h0)]
+    o, ht = G.chunk_gla(*leaves[:4], initial_state=leaves[4], output_final_state=True,
+                        chunk_size=64)
+    torch.autograd.backward([o, ht], [do, dht])
+    refs = [x.float().requires_grad_() for x in (q, k, v, g, h0)]
+    ro, rht = chunk_gla_torch(*refs, chunk_size=64)
+    torch.autograd.backward([ro, rht], [do.float(), dht])
+    torch.cuda.synchronize()
+
+    def per_slice(name, got, ref, tok_major):
+        dims = (1, 3) if tok_major else (2, 3)   # [B, T, H, D] or [B, H, K, V]
+        got, ref = got.detach().float(), ref.detach().float()
+        assert torch.isfinite(got).all(), name
+        err = (got - ref).abs().amax(dim=dims)
+        scale = ref.abs().amax(dim=dims).clamp_min(1e-30)
+        worst = float((err / scale).max())
+        print(f"{name}: worst slice error/max|ref| {worst:.3e}", flush=True)
+        assert worst <= BF16_RTOL_MAX, f"{name}: worst slice error/max|ref| {worst:.3e}"
+
+    per_slice("o", o, ro, True)
+    per_slice("ht", ht, rht, False)
+    for name, x, r in zip(["dq", "dk", "dv", "dg"], leaves[:4], refs[:4]):
+        per_slice(name, x.grad, r.grad, True)
+    per_slice("dh0", leaves[4].grad, refs[4].grad, False)
+
+
 @pytest.mark.parametrize("B,T,H", [(2, 4096, 4), (1, 2412, 2), (1, 2284, 2)],
                          ids=["even", "short-last", "odd"])
 def test_segmented_scans_match_sequential(B, T, H):
