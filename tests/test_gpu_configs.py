@@ -64,6 +64,34 @@ def test_c3_chunk_gla_fwd_full_size():
         _say(f"  slice ({b}, {h}) ok")
 
 
+def test_c3_all_slices_vs_torch_fp32():
+    """C3 at full size, all 32 (b, h) slices of o and ht against the float32 torch chunked
+    GLA (``tests/torch_ref.py``, pinned to the oracle by ``test_torch_ref.py``) on the GPU from
+    the same bf16 inputs. Bar per slice: max-abs error / max |ref| <= 2e-2."""
+    import tops.ops.gla as G
+    from gla_cases import BF16_RTOL_MAX
+    from torch_ref import chunk_gla_torch, slice_errors
+
+    B, T, H, K, V = 8, 4096, 4, 256, 512
+    _say(f"C3 chunk_gla fwd B{B} T{T} H{H} K{K} V{V}, all slices vs torch fp32")
+    gen = torch.Generator(device="cuda").manual_seed(33)
+    mk = lambda *s: torch.randn(*s, generator=gen, device="cuda")  # noqa: E731
+    q, k = (mk(B, T, H, K).to(torch.bfloat16) for _ in range(2))
+    v = mk(B, T, H, V).to(torch.bfloat16)
+    g = (torch.nn.functional.logsigmoid(mk(B, T, H, K)) / 16).to(torch.bfloat16)
+    h0 = mk(B, H, K, V) * 0.1
+    o, ht = G.chunk_gla(q, k, v, g, initial_state=h0, output_final_state=True, chunk_size=64)
+    with torch.no_grad():
+        ro, rht = chunk_gla_torch(q.float(), k.float(), v.float(), g.float(), h0,
+                                  chunk_size=64)
+    torch.cuda.synchronize()
+    for name, x, r, tm in (("o", o, ro, True), ("ht", ht, rht, False)):
+        err, scale = slice_errors(x, r, tm)
+        worst = float((err / scale.clamp_min(1e-30)).max())
+        _say(f"  {name}: worst slice error/max|ref| {worst:.3e}")
+        assert worst <= BF16_RTOL_MAX, name
+
+
 def test_c5_layer_fwd_bwd_full_size():
     from oracle import layer as L
     from tops.layers import GatedLinearAttention

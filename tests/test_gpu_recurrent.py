@@ -119,6 +119,35 @@ def test_naive_recurrent(dtype):
     check("ht", to_np(ht), hn, "f32")
 
 
+def test_fused_recurrent_c2_all_slices_vs_torch_fp32():
+    """C2 at full size (B8 T2048 H4 K256 V512, bf16 inputs, h0, float32 o), all 32 (b, h)
+    slices of o and ht against the float32 torch chunked GLA (``tests/torch_ref.py``, pinned
+    to the oracle by ``test_torch_ref.py``; the same recurrence in chunk form, 16-token chunks
+    so that its gate factors stay small) on the GPU from the same inputs. Bar per slice:
+    max-abs error <= 1e-4 x max(1, max |ref|)."""
+    import tops.ops.gla as G
+    from torch_ref import chunk_gla_torch, slice_errors
+
+    B, T, H, K, V = 8, 2048, 4, 256, 512
+    gen = torch.Generator(device="cuda").manual_seed(22)
+    mk = lambda *s: torch.randn(*s, generator=gen, device="cuda")  # noqa: E731
+    q, k = (mk(B, T, H, K).to(torch.bfloat16) for _ in range(2))
+    v = mk(B, T, H, V).to(torch.bfloat16)
+    gk = (torch.nn.functional.logsigmoid(mk(B, T, H, K)) / 16).to(torch.bfloat16)
+    h0 = mk(B, H, K, V) * 0.1
+    o, ht = G.fused_recurrent_gla(q, k, v, gk=gk, initial_state=h0, output_final_state=True)
+    assert o.dtype == torch.float32
+    with torch.no_grad():
+        ro, rht = chunk_gla_torch(q.float(), k.float(), v.float(), gk.float(), h0,
+                                  chunk_size=16)
+    torch.cuda.synchronize()
+    for name, x, r, tm in (("o", o, ro, True), ("ht", ht, rht, False)):
+        err, scale = slice_errors(x, r, tm)
+        worst = float((err / scale.clamp_min(1.0)).max())
+        print(f"{name}: worst slice error/max(1, max|ref|) {worst:.3e}", flush=True)
+        assert worst <= 1e-4, name
+
+
 def test_fused_recurrent_c2_shape_slices():
     """C2 (B8 T2048 H4 K256 V512, bf16, h0, output_final_state): slices vs the oracle."""
     import tops.ops.gla as G

@@ -48,3 +48,12 @@ def chunk_gla_torch(q, k, v, g, h0=None, scale=None, chunk_size=64):
     o = torch.stack(outs, 2)                            # [B, H, NC, C, V]
     o = o.permute(0, 2, 3, 1, 4).reshape(B, NC * C, H, V)[:, :T]
     return o, h
+
+
+def slice_errors(got, ref, tok_major):
+    """Per (batch, head) slice: max |got - ref| and max |ref|, as [B, H] tensors, for outputs
+    laid out [B, T, H, D] (tok_major) or states [B, H, K, V]."""
+    dims = (1, 3) if tok_major else (2, 3)
+    got, ref = got.detach().float(), ref.detach().float()
+    assert torch.isfinite(got).all()
+    return (got - ref).abs().amax(dim=dims), ref.abs().amax(dim=dims)
