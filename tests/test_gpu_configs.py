@@ -10,7 +10,8 @@ the reference-written layer fixtures on the HIP layer.
   output and parameter gradient finite; the output on a causal prefix of 512 tokens against
   the layer oracle on the same weights; the attention core's dq / dk / dv / dg on two (b, h)
   slices against the oracle's ``chunk_gla_bwd`` given the core's own inputs and upstream
-  gradient (captured from the layer run).
+  gradient (captured from the layer run), and the core's o, dq, dk, dv, dg on all 8 slices
+  against the float32 torch chunked GLA (``tests/torch_ref.py``) from the same inputs.
 * Reference fixtures (``tests/golden/gla_layer.npz``, written by the reference's torch CPU
   layer): the float32 HIP layer's output and gradients.
 
@@ -152,6 +153,21 @@ def test_c5_layer_fwd_bwd_full_size():
             check(f"d{name}[{b},{h}]", sl(core[name].grad), r, "bf16")
         _say(f"  core slice ({b}, {h}) ok")
     assert core["q"].shape == (B, T, H, K) and core["v"].shape == (B, T, H, V)
+    # the core's output and gradients on all 8 (b, h) slices against the float32 torch
+    # chunked GLA (tests/torch_ref.py) from the same inputs and upstream gradient
+    from gla_cases import BF16_RTOL_MAX
+    from torch_ref import chunk_gla_torch, slice_errors
+
+    refs = [core[n].detach().float().requires_grad_() for n in ("q", "k", "v", "g")]
+    ro, _ = chunk_gla_torch(*refs, chunk_size=64)
+    ro.backward(core["o"].grad.float())
+    pairs = [("o", core["o"], ro)] + [(f"d{n}", core[n].grad, r.grad)
+                                      for n, r in zip(("q", "k", "v", "g"), refs)]
+    for name, got, r in pairs:
+        err, scale = slice_errors(got, r, True)
+        worst = float((err / scale.clamp_min(1e-30)).max())
+        _say(f"  core {name}, all slices: worst error/max|ref| {worst:.3e}")
+        assert worst <= BF16_RTOL_MAX, name
 
 
 def _layer_cases():
