@@ -295,7 +295,7 @@ def _c4_stages(x, simple, B, T, H, K, V, C, gamma, reps=10):
     ht, dh0 = torch.empty_like(x["h0"]), torch.empty_like(x["h0"])
     q, k, v, g, h0, do, dht = (x[n] for n in ("q", "k", "v", "g", "h0", "do", "dht"))
     lay = (B, T, H, K, V, C, *seq.args(), _lib.BF16, st)
-    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, False, torch.bfloat16, dev)
+    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, False, torch.bfloat16, dev, backward=True)
     gs = torch.from_numpy(gamma).to(dev)
     if simple:
         runs = [("simple_chunk_fwd", KT_HEAD_FWD, lambda: call(

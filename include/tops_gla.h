@@ -111,28 +111,32 @@ int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void
                          void* stream);
 
 /*
- * Bytes of the optional workspace (`seg_ws`) of tops_gla_chunk_fwd and tops_gla_chunk_bwd
- * for this problem (0: the call does not use one); N = sequences (B, or the number of
- * cu_seqlens sequences with varlen = 1). Parts, each 256-byte aligned, in this order:
- *  - sequence segments (fixed length): the inter-chunk scans run as parallel segments
- *    (local states, then all segments at once, each folding its entry state from them)
- *    instead of one chunk after another;
- *  - gate-range flags: the full-head kernels factor e^{g~_i - g~_j} per element as
+ * Bytes of the optional workspace (`seg_ws`) of tops_gla_chunk_fwd (backward = 0) or
+ * tops_gla_chunk_bwd (backward = 1) for this problem (0: the call does not use one); N =
+ * sequences (B, or the number of cu_seqlens sequences with varlen = 1). Parts, each
+ * 256-byte aligned, in this order:
+ *  - sequence segments (full-head kernels, fixed length): the inter-chunk scans run as
+ *    parallel segments (local states, then all segments at once, each folding its entry
+ *    state from them) instead of one chunk after another;
+ *  - gate-range flags (K <= 512): the chunk kernels factor e^{g~_i - g~_j} per element as
  *    e^{g~_i - r} e^{r - g~_j} about each column's chunk midpoint r, which holds while
- *    |g~ - r| <= 100 log(2) (a chunk's gate range up to about 138 in natural log units);
- *    every block records whether one of its chunks goes beyond, and the recurrent scans
- *    (exact for any decay) then recompute the flagged sequences and heads (o and ht in the
- *    forward; dq, dk, dv, dg and dh0 in the fused backward). Without this part a gate range
- *    beyond the limit gives non-finite or inaccurate values. Wide heads (K > 128) that
- *    stream the gating workspace, and their backward, are not checked;
+ *    |g~ - r| <= 100 log(2) (a chunk's gate range up to about 138 in natural log units).
+ *    Every chunk is checked (by the full-head kernels as they gate it, by the wide heads'
+ *    gating kernel, or by a check kernel on the other paths), and the recurrent scans
+ *    (exact for any decay) then recompute the flagged sequences and heads: o and ht in the
+ *    forward; dq, dk, dv, dg and dh0 in the backward (K and V <= 512). Without this part a
+ *    gate range beyond the limit gives non-finite or inaccurate values;
  *  - wide heads (K = 256, three or more 64-column V tiles, fixed length): the per-chunk
  *    gating that the scans, the forward and the dv kernel then stream;
- *  - the backward fallback's final states (f32 [N, H, K, V], K and V <= 128).
- * A shorter workspace drops the later parts.
+ *  - backward only: the fallback's final states (f32 [N, H, K, V], K and V <= 512; without
+ *    it a call with dht is not checked).
+ * A shorter workspace drops the later parts. The per-chunk states h_ws that the forward
+ * stores for flagged pairs are not meaningful (the backward recomputes those pairs).
  * No counterpart in the reference (its scans are sequential grid axes, chunk_h.py:252-271).
  */
 int64_t tops_gla_chunk_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
-                                int chunk_size, int64_t N, int varlen, int dtype);
+                                int chunk_size, int64_t N, int varlen, int dtype,
+                                int backward);
 
 /*
  * 1 when the full-head kernels run this shape (16-byte aligned buffers assumed): the
@@ -166,7 +170,8 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
  * 24 MiB per GPU (held by each GPU the library runs on until the process ends), whose
  * address is taken once per device on the first call with that device current; a shape
  * that needs more returns TOPS_GLA_EINVAL (the segment part never exceeds 17.04 MB; the
- * flags take 4 bytes per sequence, head, segment and V tile). The wide heads' per-chunk
+ * flags take 4 bytes per chunk and head, or per sequence, head, segment and V tile where
+ * that is more). The wide heads' per-chunk
  * gating workspace is not used. Nothing here calls hipMalloc or hipFree.
  * Every call on one GPU shares that array: calls that overlap on one GPU (other streams,
  * other threads) race and must be serialized by the caller. Each call writes every part of

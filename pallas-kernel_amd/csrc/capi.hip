@@ -133,11 +133,16 @@ bool use_head(int dtype, int chunk, int64_t K, int64_t V, bool g_is_cumsum,
   return true;
 }
 
-// Workspace of the full-head paths of tops_gla_chunk_fwd / _bwd, each part 256-byte aligned:
-//   [segment states, decays (NS > 1)] [gate-range flags, int32 per block]
-//   [wide heads' per-chunk gating (fixed length)] [fallback final states f32 [N, H, K, V]]
-// A workspace that ends early leaves the later parts out: no flags (no gate-range fallback),
-// no gating workspace (every V tile's block gates its chunks), no backward fallback.
+// Workspace of tops_gla_chunk_fwd / _bwd, each part 256-byte aligned:
+//   [segment states, decays (full-head, NS > 1)] [gate-range flags, int32]
+//   [wide heads' per-chunk gating (full-head, fixed length)]
+//   [backward only: fallback final states f32 [N, H, K, V]]
+// The flags part holds the full-head kernels' per-block flags or the per-chunk flags [NC, H]
+// of the other paths (its size is the larger of the two, NC bounded by N ceil(T / C), or
+// ceil(T / C) + N for varlen). Flags exist when the recurrent fallback runs the shape (K <=
+// 512; the backward's also V <= 512). A workspace that ends early leaves the later parts
+// out: no flags (no gate-range fallback), no gating workspace (every V tile's block gates its
+// chunks), no backward fallback when dht is given.
 long align256(long x) { return (x + 255) / 256 * 256; }
 
 struct WsLayout {
@@ -146,14 +151,20 @@ struct WsLayout {
   long off_flags = 0, off_gate = 0, off_ht = 0, total = 0;
 };
 
-WsLayout ws_layout(int N, int T, int H, int K, int V, int C, bool varlen) {
+WsLayout ws_layout(int N, int T, int H, int K, int V, int C, bool varlen, bool head,
+                   bool backward) {
   WsLayout w;
-  w.VT = tops::head_vtiles(K, V);
-  tops::head_seg_plan(N, H, T, C, varlen, w.NS, w.SL, w.VT);
-  w.seg = align256(tops::head_seg_ws_bytes(N, w.NS, H, K, V));
-  w.flags = align256((long)N * w.NS * H * w.VT * 4);
-  w.gate = varlen ? 0 : align256(tops::head_gate_ws_bytes(N, T, H, K, V));
-  w.ht = tops::head_bwd_supported(K, V) ? align256((long)N * H * K * V * 4) : 0;
+  long nflag = (varlen ? (long)(T + C - 1) / C + N : (long)N * ((T + C - 1) / C)) * H;
+  if (head) {
+    w.VT = tops::head_vtiles(K, V);
+    tops::head_seg_plan(N, H, T, C, varlen, w.NS, w.SL, w.VT);
+    w.seg = align256(tops::head_seg_ws_bytes(N, w.NS, H, K, V));
+    w.gate = varlen ? 0 : align256(tops::head_gate_ws_bytes(N, T, H, K, V));
+    const long nblk = (long)N * w.NS * H * w.VT;
+    if (nblk > nflag) nflag = nblk;
+  }
+  w.flags = K <= 512 ? align256(nflag * 4) : 0;
+  w.ht = backward && tops::recurrent_supported(K, V) ? align256((long)N * H * K * V * 4) : 0;
   w.off_flags = w.seg;
   w.off_gate = w.off_flags + w.flags;
   w.off_ht = w.off_gate + w.gate;
@@ -161,8 +172,8 @@ WsLayout ws_layout(int N, int T, int H, int K, int V, int C, bool varlen) {
   return w;
 }
 
-// The full-head kernels' workspace pointers from the caller's workspace (NULL parts are
-// absent; NS = 1 without the segment part).
+// The workspace pointers of one call from the caller's workspace (NULL parts are absent; NS
+// = 1 without the segment part). `head`: the full-head kernels run the call.
 struct WsParts {
   int NS = 1, SL = 0, VT = 1;
   float *st = nullptr, *gm = nullptr;
@@ -172,8 +183,9 @@ struct WsParts {
 };
 
 WsParts ws_parts(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void* ws,
-                 int64_t ws_bytes) {
-  const WsLayout w = ws_layout(si.N, si.T, (int)H, (int)K, (int)V, si.C, si.cu != nullptr);
+                 int64_t ws_bytes, bool head, bool backward) {
+  const WsLayout w = ws_layout(si.N, si.T, (int)H, (int)K, (int)V, si.C, si.cu != nullptr,
+                               head, backward);
   WsParts p;
   p.VT = w.VT;
   const bool usable = ws != nullptr && ((uintptr_t)ws & 255u) == 0;
@@ -185,10 +197,24 @@ WsParts ws_parts(const tops::SeqInfo& si, int64_t H, int64_t K, int64_t V, void*
     p.st = (float*)b;
     p.gm = (float*)(b + (long)si.N * w.NS * H * K * V * 4);
   }
-  if (ws_bytes >= w.off_gate) p.flags = (int*)(b + w.off_flags);
+  if (w.flags > 0 && ws_bytes >= w.off_gate) p.flags = (int*)(b + w.off_flags);
   if (w.gate > 0 && ws_bytes >= w.off_ht) p.gate = b + w.off_gate;
   if (w.ht > 0 && ws_bytes >= w.total) p.ht = (float*)(b + w.off_ht);
   return p;
+}
+
+// Per-chunk flags [NC, H] in the recurrent fallback's layout.
+tops::GateFlags chunk_flags(int* f, const tops::SeqInfo& si) {
+  tops::GateFlags g = {};
+  g.p = f;
+  g.vt = 1;
+  if (si.cu) {
+    g.ns = 0;
+    g.co = si.chunk_cu;
+  } else {
+    g.ns = (si.T + si.C - 1) / si.C;
+  }
+  return g;
 }
 
 }  // namespace
@@ -264,11 +290,14 @@ int tops_gla_full_head(int64_t K, int64_t V, int chunk_size, int dtype, int back
 }
 
 int64_t tops_gla_chunk_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
-                                int chunk_size, int64_t N, int varlen, int dtype) {
-  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || K > 256 || V > (1 << 20)) return 0;
-  if (N <= 0 || N > kMaxInt || (!varlen && N != B)) return 0;
-  if (!tops::head_supported(dtype, chunk_size, (int)K, (int)V, false)) return 0;
-  return ws_layout((int)N, (int)T, (int)H, (int)K, (int)V, chunk_size, varlen != 0).total;
+                                int chunk_size, int64_t N, int varlen, int dtype,
+                                int backward) {
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || K > 512 || V > (1 << 20)) return 0;
+  if (N <= 0 || N > kMaxInt || (!varlen && N != B) || B * T > kMaxInt) return 0;
+  if (!dtype_ok(dtype) || chunk_size <= 0 || chunk_size > 64) return 0;
+  const bool head = tops::head_supported(dtype, chunk_size, (int)K, (int)V, false);
+  return ws_layout((int)N, (int)T, (int)H, (int)K, (int)V, chunk_size, varlen != 0, head,
+                   backward != 0).total;
 }
 
 int tops_gla_chunk_local_cumsum(const void* g, void* out, int64_t B, int64_t T, int64_t H,
@@ -342,7 +371,7 @@ int tops_gla_chunk_fwd_h(const void* k, const void* v, const void* g, int g_is_c
     s.s_all = h;
     s.s_final = ht;
     {
-      const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+      const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes, true, false);
       s.NS = w.NS;
       s.SL = w.SL;
       s.seg_state = w.st;
@@ -412,7 +441,7 @@ int tops_gla_chunk_bwd_dh(const void* q, const void* g, int g_is_cumsum, const v
     s.s_all = dh;
     s.s_final = dh0;
     {
-      const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+      const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes, true, false);
       s.NS = w.NS;
       s.SL = w.SL;
       s.seg_state = w.st;
@@ -481,69 +510,15 @@ int tops_gla_chunk_fwd_o(const void* q, const void* k, const void* v, const void
   return hip_status(tops::run_chunk_fwd_o(p, dtype, (hipStream_t)stream), "chunk_fwd_o");
 }
 
-int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* g,
-                       const float* h0, void* o, float* ht, void* h_ws, void* seg_ws,
-                       int64_t seg_ws_bytes, float scale, int64_t B, int64_t T, int64_t H,
-                       int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
-                       const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
-                       void* stream) {
-  int rc = check_mfma_common(K, V, chunk_size, dtype);
-  if (rc) return rc;
-  tops::SeqInfo si;
-  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
-  if (rc) return rc;
-  if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || g == nullptr ||
-                    o == nullptr))
-    return fail(TOPS_GLA_EINVAL, "q, k, v, g and o must not be NULL");
-  hipStream_t st = (hipStream_t)stream;
-  const bool head = use_head(dtype, chunk_size, K, V, false, {q, k, v, g, h0, o, ht, h_ws});
-  if (!head && h_ws == nullptr && B * T > 0)
-    return fail(TOPS_GLA_EINVAL, "h_ws must not be NULL off the full-head path");
-  if (head) {
-    tops::HeadFwdArgs f = {};
-    f.q = q;
-    f.k = k;
-    f.v = v;
-    f.g = g;
-    f.h0 = h0;
-    f.o = o;
-    f.h_out = h_ws;
-    f.ht = ht;
-    const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
-    f.NS = w.NS;
-    f.SL = w.SL;
-    f.seg_state = w.st;
-    f.seg_gam = w.gm;
-    f.gate_ws = w.gate;
-    // the gate-range check runs where the forward gates its own chunks (wide heads that
-    // stream the gating workspace are left out)
-    f.flags = (K > 128 && w.gate) ? nullptr : w.flags;
-    f.scale = scale;
-    f.H = (int)H;
-    f.K = (int)K;
-    f.V = (int)V;
-    f.si = si;
-    rc = hip_status(tops::run_head_fwd(f, st), "chunk_fwd (full-head)");
-    if (rc || f.flags == nullptr) return rc;
-    // sequences and heads with a chunk beyond the factoring's range: the recurrent forward
-    // (exact for any decay) rewrites their o and final state; the other blocks return at once
-    tops::RecArgs r = {};
-    r.q = q;
-    r.k = k;
-    r.v = v;
-    r.gk = g;
-    r.h0 = h0;
-    r.o = o;
-    r.ht = ht;
-    r.scale = scale;
-    r.H = (int)H;
-    r.K = (int)K;
-    r.V = (int)V;
-    r.si = si;
-    r.flags = {f.flags, w.NS, w.VT};
-    return hip_status(tops::run_recurrent_fwd(r, dtype, dtype, st),
-                      "chunk_fwd (gate-range fallback)");
-  }
+namespace {
+
+// tops_gla_chunk_fwd off the full-head path: the fused float32 forward, or the state scan
+// and the per-chunk output kernel.
+int chunk_fwd_other(const void* q, const void* k, const void* v, const void* g, const float* h0,
+                    void* o, float* ht, void* h_ws, float scale, int64_t H, int64_t K,
+                    int64_t V, int chunk_size, const tops::SeqInfo& si, int dtype,
+                    hipStream_t st) {
+  int rc;
   if (tops::fused_fwd_supported(dtype, chunk_size, (int)K)) {
     tops::FusedFwdArgs f = {};
     f.q = q;
@@ -597,6 +572,120 @@ int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* 
   p.si = si;
   return hip_status(tops::run_chunk_fwd_o(p, dtype, st), "chunk_fwd (output)");
 }
+
+// Per-chunk gate-range flags [NC, H] of the raw gates g (into `flags`).
+int gate_check(const void* g, int* flags, int64_t H, int64_t K, const tops::SeqInfo& si,
+               int dtype, hipStream_t st) {
+  tops::GateCheckArgs c = {};
+  c.g = g;
+  c.flags = flags;
+  c.H = (int)H;
+  c.K = (int)K;
+  c.si = si;
+  return hip_status(tops::run_gate_range(c, dtype, st), "gate-range check");
+}
+
+// The forward's fallback off the full-head path: check every chunk, then the recurrent
+// forward over the flagged pairs.
+int gate_fallback_fwd(const void* q, const void* k, const void* v, const void* g,
+                      const float* h0, void* o, float* ht, float scale, int64_t H, int64_t K,
+                      int64_t V, const tops::SeqInfo& si, int* flags, int dtype,
+                      hipStream_t st) {
+  int rc = gate_check(g, flags, H, K, si, dtype, st);
+  if (rc) return rc;
+  tops::RecArgs r = {};
+  r.q = q;
+  r.k = k;
+  r.v = v;
+  r.gk = g;
+  r.h0 = h0;
+  r.o = o;
+  r.ht = ht;
+  r.scale = scale;
+  r.H = (int)H;
+  r.K = (int)K;
+  r.V = (int)V;
+  r.si = si;
+  r.flags = chunk_flags(flags, si);
+  return hip_status(tops::run_recurrent_fwd(r, dtype, dtype, st),
+                    "chunk_fwd (gate-range fallback)");
+}
+
+}  // namespace
+
+int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const void* g,
+                       const float* h0, void* o, float* ht, void* h_ws, void* seg_ws,
+                       int64_t seg_ws_bytes, float scale, int64_t B, int64_t T, int64_t H,
+                       int64_t K, int64_t V, int chunk_size, const int32_t* cu_seqlens,
+                       const int32_t* chunk_offsets, int64_t N, int64_t NC, int dtype,
+                       void* stream) {
+  int rc = check_mfma_common(K, V, chunk_size, dtype);
+  if (rc) return rc;
+  tops::SeqInfo si;
+  rc = make_seq(B, T, H, chunk_size, cu_seqlens, chunk_offsets, N, NC, true, &si);
+  if (rc) return rc;
+  if (B * T > 0 && (q == nullptr || k == nullptr || v == nullptr || g == nullptr ||
+                    o == nullptr))
+    return fail(TOPS_GLA_EINVAL, "q, k, v, g and o must not be NULL");
+  hipStream_t st = (hipStream_t)stream;
+  const bool head = use_head(dtype, chunk_size, K, V, false, {q, k, v, g, h0, o, ht, h_ws});
+  if (!head && h_ws == nullptr && B * T > 0)
+    return fail(TOPS_GLA_EINVAL, "h_ws must not be NULL off the full-head path");
+  if (head) {
+    tops::HeadFwdArgs f = {};
+    f.q = q;
+    f.k = k;
+    f.v = v;
+    f.g = g;
+    f.h0 = h0;
+    f.o = o;
+    f.h_out = h_ws;
+    f.ht = ht;
+    const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes, true, false);
+    f.NS = w.NS;
+    f.SL = w.SL;
+    f.seg_state = w.st;
+    f.seg_gam = w.gm;
+    f.gate_ws = w.gate;
+    // gate-range flags: per block where the forward gates its own chunks, per chunk from the
+    // gating kernel where wide heads stream the gating workspace
+    f.flags = w.flags;
+    f.scale = scale;
+    f.H = (int)H;
+    f.K = (int)K;
+    f.V = (int)V;
+    f.si = si;
+    rc = hip_status(tops::run_head_fwd(f, st), "chunk_fwd (full-head)");
+    if (rc || f.flags == nullptr) return rc;
+    const bool per_chunk = K > 128 && w.gate != nullptr;
+    // sequences and heads with a chunk beyond the factoring's range: the recurrent forward
+    // (exact for any decay) rewrites their o and final state; the other blocks return at once
+    tops::RecArgs r = {};
+    r.q = q;
+    r.k = k;
+    r.v = v;
+    r.gk = g;
+    r.h0 = h0;
+    r.o = o;
+    r.ht = ht;
+    r.scale = scale;
+    r.H = (int)H;
+    r.K = (int)K;
+    r.V = (int)V;
+    r.si = si;
+    r.flags = per_chunk ? chunk_flags(f.flags, si) : tops::GateFlags{f.flags, w.NS, w.VT};
+    return hip_status(tops::run_recurrent_fwd(r, dtype, dtype, st),
+                      "chunk_fwd (gate-range fallback)");
+  }
+  rc = chunk_fwd_other(q, k, v, g, h0, o, ht, h_ws, scale, H, K, V, chunk_size, si, dtype, st);
+  if (rc) return rc;
+  // the gate-range check of the per-chunk kernels, and the recurrent forward for the flagged
+  // (sequence, head) pairs (o and the final state rewritten)
+  const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes, false, false);
+  if (w.flags == nullptr || B * T == 0) return rc;
+  return gate_fallback_fwd(q, k, v, g, h0, o, ht, scale, H, K, V, si, w.flags, dtype, st);
+}
+
 
 // ---------------------------------------------------------------------------
 // tops_gla_chunk_fwd without a caller workspace: the segment workspace lives in one
@@ -662,12 +751,15 @@ int tops_gla_chunk_fwd_noalloc(const void* q, const void* k, const void* v, cons
   if (B <= 0 || T <= 0 || H <= 0)   // nothing to segment: no scratch needed
     return tops_gla_chunk_fwd(q, k, v, g, h0, o, ht, h_ws, nullptr, 0, scale, B, T, H, K, V,
                               chunk_size, cu_seqlens, chunk_offsets, N, NC, dtype, stream);
-  long need = 0;   // the segment part and the gate-range flags
-  if (K <= 256 && tops::head_supported(dtype, chunk_size, (int)K, (int)V, false))
-    need = ws_layout(si.N, si.T, (int)H, (int)K, (int)V, chunk_size, si.cu != nullptr).off_gate;
+  // the segment part (full-head shapes) and the gate-range flags
+  const bool head = tops::head_supported(dtype, chunk_size, (int)K, (int)V, false);
+  const long need = K <= 512 ? ws_layout(si.N, si.T, (int)H, (int)K, (int)V, chunk_size,
+                                         si.cu != nullptr, head, false).off_gate
+                             : 0;
   if (need > kScratchBytes)
     return fail(TOPS_GLA_EINVAL,
-                "the segment workspace needs %ld bytes, the static scratch holds %ld; call "
+                "the workspace (segment part, gate-range flags) needs %ld bytes, the static "
+                "scratch holds %ld; call "
                 "tops_gla_chunk_fwd with a workspace",
                 need, kScratchBytes);
   void* ws = nullptr;
@@ -710,9 +802,8 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   int NS = 1, SL = 0;
   float *seg_st = nullptr, *seg_gm = nullptr;
   void* gate = nullptr;   // per-chunk gating of wide heads (when the workspace holds it)
-  WsParts wp;
+  const WsParts wp = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes, head, true);
   if (head) {
-    wp = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
     NS = wp.NS;
     SL = wp.SL;
     seg_st = wp.st;
@@ -720,6 +811,12 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     gate = wp.gate;
   }
   if (head_bwd) gate = nullptr;
+  // the recurrent fallback's needs: K, V <= 512 and, with dht, its final-state part
+  const bool rec_ok = tops::recurrent_supported((int)K, (int)V) && B * T > 0 &&
+                      (dht == nullptr || wp.ht != nullptr);
+  // per-chunk gate-range flags of the paths below the fused backward: from the gating
+  // kernel (wide heads with the gating workspace) or the check kernel
+  int* cflags = (!head_bwd && rec_ok) ? wp.flags : nullptr;
   if (gate) {   // gated q, k, A and the column factors once per (chunk, head): the scans and
                 // the dv kernel stream them
     tops::HeadFwdArgs a = {};
@@ -727,12 +824,16 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
     a.k = k;
     a.g = g;
     a.gate_ws = gate;
+    a.flags = cflags;
     a.scale = scale;
     a.H = (int)H;
     a.K = (int)K;
     a.V = (int)V;
     a.si = si;
     rc = hip_status(tops::run_head_gate(a, st), "chunk_bwd (gating)");
+    if (rc) return rc;
+  } else if (cflags) {
+    rc = gate_check(g, cflags, H, K, si, dtype, st);
     if (rc) return rc;
   }
   auto head_scan = [&](bool rev, const void* a, const void* b, const float* s_init, void* s_all,
@@ -875,7 +976,32 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   p.V = (int)V;
   p.vec = vec_ok(dtype, K, V, {q, k, v, g, dout, h, dh_ws, dq, dk, dv, dg});
   p.si = si;
-  return hip_status(tops::run_chunk_bwd(p, dtype, st), "chunk_bwd (gradients)");
+  rc = hip_status(tops::run_chunk_bwd(p, dtype, st), "chunk_bwd (gradients)");
+  if (rc || cflags == nullptr) return rc;
+  // sequences and heads with a chunk beyond the factoring's range: the recurrent backward
+  // (exact for any decay) rewrites their dq, dk, dv, dg and dh0
+  tops::RecBwdArgs r = {};
+  r.q = q;
+  r.k = k;
+  r.v = v;
+  r.gk = g;
+  r.dout = dout;
+  r.h0 = h0;
+  r.dht = dht;
+  r.dq = dq;
+  r.dk = dk;
+  r.dv = dv;
+  r.dgk = dg;
+  r.dh0 = dh0;
+  r.ht_ws = wp.ht;
+  r.scale = scale;
+  r.H = (int)H;
+  r.K = (int)K;
+  r.V = (int)V;
+  r.si = si;
+  r.flags = chunk_flags(cflags, si);
+  return hip_status(tops::run_recurrent_bwd(r, dtype, dtype, st),
+                    "chunk_bwd (gate-range fallback)");
 }
 
 // ---------------------------------------------------------------------------
@@ -921,7 +1047,7 @@ int tops_gla_simple_chunk_fwd(const void* q, const void* k, const void* v, const
   f.h_out = h_ws;
   f.ht = ht;
   {
-    const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+    const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes, true, false);
     f.NS = w.NS;
     f.SL = w.SL;
     f.seg_state = w.st;
@@ -964,7 +1090,7 @@ int tops_gla_simple_chunk_bwd(const void* q, const void* k, const void* v, const
   int NS = 1, SL = 0;
   float *seg_st = nullptr, *seg_gm = nullptr;
   {
-    const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes);
+    const WsParts w = ws_parts(si, H, K, V, seg_ws, seg_ws_bytes, true, false);
     NS = w.NS;
     SL = w.SL;
     seg_st = w.st;

@@ -970,6 +970,15 @@ __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
   float r[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) r[e] = 0.5f * (first[e] + gam[e]);
+  if (p.flags) {   // uniform: the chunk's gate-range flag, per chunk [NC, H], always written
+    float dmax = 0.f;   // rows past the chunk hold gam, columns past K zeros: both in range
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dmax = fmaxf(dmax, fabsf(gt[j][e] - r[e]));
+    const int bad = __syncthreads_or(dmax > kGateLimit2 ? 1 : 0);
+    if (tid == 0) p.flags[(long)(c0 + ci) * H + hh] = bad ? 1 : 0;
+  }
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int row = rs * RPT + j;
@@ -2322,9 +2331,11 @@ static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
       e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP, false, true>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
       if (e != hipSuccess) return e;
+      HeadFwdArgs q = p;
+      q.flags = nullptr;   // the gating kernel wrote the per-chunk flags
       ktimer_mark(KT_HEAD_FWD, false, st);
       hipLaunchKernelGGL((head_fwd_kernel<KP, VP, false, true>), dim3((unsigned)blocks),
-                         dim3(HNT), Lay::bytes, st, p);
+                         dim3(HNT), Lay::bytes, st, q);
       ktimer_mark(KT_HEAD_FWD, true, st);
       return hipGetLastError();
     }

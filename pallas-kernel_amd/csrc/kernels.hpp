@@ -98,16 +98,30 @@ struct CumsumArgs {
 hipError_t run_cumsum(const CumsumArgs& p, int in_dtype, int out_dtype, hipStream_t st);
 
 // Fused recurrent forward (recurrent.hip).
-// Per-block flags of the full-head kernels: 1 when one of the block's chunks has a gate
-// range beyond what the per-element factoring holds (|g~ - r| > kGateLimit2 in base 2),
-// written unconditionally by every block (no clearing). The block of (sequence seq, segment
-// s, head h, V tile t) writes at ((seq * ns + s) * H + h) * vt + t. The recurrent fallback
-// (exact for any decay) then recomputes the flagged (sequence, head) pairs.
+// Gate-range flags: 1 when a chunk has a gate range beyond what the per-element factoring
+// holds (|g~ - r| > kGateLimit2 in base 2), written unconditionally (no clearing). Two
+// layouts, both ((seq * ns + s) * H + h) * vt + t:
+// * per block of the full-head kernels: s = segment, t = V tile;
+// * per chunk (gate_range_kernel, head_gate_kernel; vt = 1): s = the sequence's chunk, i.e.
+//   [NC, H]; with varlen sequences `co` (chunk offsets [N + 1]) gives each sequence's chunk
+//   range instead of ns chunks from seq * ns.
+// The recurrent fallback (exact for any decay) then recomputes the flagged (sequence, head)
+// pairs.
 struct GateFlags {
-  int* p;      // nullable: no check, no fallback
-  int ns, vt;  // segments and V tiles per (sequence, head) in the flags' layout
+  int* p;         // nullable: no check, no fallback
+  int ns, vt;     // segments (or chunks) and V tiles per (sequence, head)
+  const int* co;  // nullable: per-chunk flags of varlen sequences (ns unused)
 };
 constexpr float kGateLimit2 = 100.f;
+
+// Per-chunk gate-range check (gate_range.hip): flags[c * H + h] for every chunk c and head h.
+struct GateCheckArgs {
+  const void* g;   // raw log-gates [tokens, H, K]
+  int* flags;      // [NC, H]
+  int H, K;
+  SeqInfo si;
+};
+hipError_t run_gate_range(const GateCheckArgs& p, int dtype, hipStream_t st);
 
 struct RecArgs {
   const void *q, *k, *v, *gk, *gv;  // gk / gv nullable
@@ -141,6 +155,11 @@ struct RecScanArgs {
   const void* gx;
   const void* gxf;   // out dtype, or float when gxf_f32
   int gxf_f32;
+  // bf16 outputs read back by a later scan's epilogue: `out_lo` (nullable, out dtype, out's
+  // layout) receives out's rounding residual (out - bf16(out)), and a `gxf_lo` given with
+  // gxf adds it back, so the epilogue sees out to about 16 significant bits
+  void* out_lo;
+  const void* gxf_lo;
   const void* gy;
   const float* hfin;
   void* dg;          // out dtype
@@ -260,10 +279,13 @@ struct HeadFwdArgs {
   float scale;
   int H, K, V;
   SeqInfo si;
-  int* flags;             // nullable: per-block gate-range flags (GateFlags, vt = V tiles)
+  // nullable: gate-range flags. head_fwd_kernel: per block (GateFlags, vt = V tiles); with
+  // a gating workspace (K = 256) the gating kernel's per-chunk flags [NC, H] instead
+  int* flags;
 };
 hipError_t run_head_fwd(const HeadFwdArgs& p, hipStream_t st);
-// Per-chunk gating of wide heads (K = 256) into p.gate_ws (q, k, g, scale, H, K, si read).
+// Per-chunk gating of wide heads (K = 256) into p.gate_ws (q, k, g, scale, H, K, si read;
+// per-chunk gate-range flags [NC, H] into p.flags when given).
 hipError_t run_head_gate(const HeadFwdArgs& p, hipStream_t st);
 
 struct HeadBwdArgs {

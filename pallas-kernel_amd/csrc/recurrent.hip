@@ -152,13 +152,19 @@ __device__ __forceinline__ void put(void* p, long i, float x) {
 
 }  // namespace
 
-// Whether any block of the full-head kernels flagged (sequence seq, head hh): the pair's
-// flags (one per segment and V tile) read by the lanes of every wave at once, so that an
-// unflagged block leaves after a single load. Uniform over the block.
+// Whether (sequence seq, head hh) is flagged: the pair's flags (one per segment or chunk and
+// V tile) read by the lanes of every wave at once, so that an unflagged block leaves after a
+// few loads. Uniform over the block.
 __device__ __forceinline__ bool pair_flagged(const GateFlags& f, int seq, int hh, int H) {
+  long s0 = (long)seq * f.ns;
+  int n = f.ns * f.vt;
+  if (f.co) {   // per-chunk flags of varlen sequences
+    s0 = f.co[seq];
+    n = (f.co[seq + 1] - f.co[seq]) * f.vt;
+  }
   int x = 0;
-  for (int i = (int)(threadIdx.x & 63); i < f.ns * f.vt; i += 64)
-    x |= f.p[((long)seq * f.ns + i / f.vt) * H * f.vt + (long)hh * f.vt + i % f.vt];
+  for (int i = (int)(threadIdx.x & 63); i < n; i += 64)
+    x |= f.p[((s0 + i / f.vt) * H + hh) * f.vt + i % f.vt];
   return __ballot(x != 0) != 0ull;
 }
 
@@ -301,8 +307,9 @@ __device__ __forceinline__ void rec_scan_unit(const RecScanArgs& p, const int L)
         pgc[k] = (cin && gi >= 0) ? y : 0.f;
       }
       if (grad) {
-        const float xf = p.gxf_f32 ? static_cast<const float*>(p.gxf)[co]
-                                   : to_f32(static_cast<const TO*>(p.gxf)[co]);
+        float xf = p.gxf_f32 ? static_cast<const float*>(p.gxf)[co]
+                             : to_f32(static_cast<const TO*>(p.gxf)[co]);
+        if (p.gxf_lo) xf += to_f32(static_cast<const TO*>(p.gxf_lo)[co]);
         const float xd = to_f32(gx[co]) * xf, xy = to_f32(gy[co]);
         pxd[k] = cin ? xd : 0.f;
         py[k] = cin ? xy : 0.f;
@@ -424,7 +431,10 @@ __device__ __forceinline__ void rec_scan_unit(const RecScanArgs& p, const int L)
         float val = 0.f;
 #pragma unroll
         for (int ww = 0; ww < RNW; ++ww) val += sO[(ww * TB + s) * CB + c];
-        put<TO>(p.out, (long)tok(b0 + s) * rsC + (long)hh * C + cbase + c, val);
+        const long oi = (long)tok(b0 + s) * rsC + (long)hh * C + cbase + c;
+        put<TO>(p.out, oi, val);
+        if constexpr (!std::is_same<TO, float>::value)
+          if (p.out_lo) put<TO>(p.out_lo, oi, val - to_f32(from_f32<TO>(val)));
         if (grad) sXD[i] -= sY[i] * val;   // this step's term of the gate gradient
       } else if (grad) {
         sXD[i] = 0.f;
@@ -656,6 +666,13 @@ hipError_t run_recurrent_bwd(const RecBwdArgs& p, int dtype, int o_dtype, hipStr
     s2.gy = p.k;
     s2.hfin = need_ht ? p.ht_ws : nullptr;
     s2.dg = p.dgk;
+    if (o_dtype != DT_F32) {
+      // bf16 dq: its rounding residual goes into dgk (same layout), where the dk scan reads
+      // a token's residual before it writes that token's gate gradient, so the q dq terms of
+      // the reverse cumsum keep their float32 accuracy over long sequences
+      s.out_lo = p.dgk;
+      s2.gxf_lo = p.dgk;
+    }
   }
 
   // 3. dv (+ dgv, dh0) : S = dh, rows K, columns V, opposite direction

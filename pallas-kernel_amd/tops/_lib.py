@@ -36,7 +36,7 @@ _SIGS = {
                               _I64, _I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_chunk_fwd_o": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64,
                              _I64, _I, _P, _P, _I64, _I64, _I, _P],
-    "tops_gla_chunk_ws_bytes": [_I64, _I64, _I64, _I64, _I64, _I, _I64, _I, _I],
+    "tops_gla_chunk_ws_bytes": [_I64, _I64, _I64, _I64, _I64, _I, _I64, _I, _I, _I],
     "tops_gla_chunk_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _F, _I64, _I64, _I64, _I64,
                            _I64, _I, _P, _P, _I64, _I64, _I, _P],
     "tops_gla_chunk_fwd_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64,
@@ -141,14 +141,15 @@ def full_head(K, V, chunk, dtype, backward):
     return bool(load().tops_gla_full_head(K, V, chunk, dtype_code(dtype), int(bool(backward))))
 
 
-def seg_workspace(B, T, H, K, V, chunk, varlen, dtype, device, N=None):
-    """Workspace of tops_gla_chunk_fwd / _bwd (sequence segments, gate-range flags, wide
-    heads' gating, the backward fallback's states): (tensor or None, bytes). ``varlen``: the
-    cu_seqlens list (or a true value with ``N`` given), else falsy."""
+def seg_workspace(B, T, H, K, V, chunk, varlen, dtype, device, N=None, backward=False):
+    """Workspace of tops_gla_chunk_fwd (``backward`` false) or tops_gla_chunk_bwd (true):
+    sequence segments, gate-range flags, wide heads' gating, and for the backward the
+    fallback's final states. Returns (tensor or None, bytes). ``varlen``: the cu_seqlens list
+    (or a true value with ``N`` given), else falsy."""
     if N is None:
         N = len(varlen) - 1 if isinstance(varlen, (list, tuple)) else B
     n = int(load().tops_gla_chunk_ws_bytes(B, T, H, K, V, chunk, N, int(bool(varlen)),
-                                           dtype_code(dtype)))
+                                           dtype_code(dtype), int(bool(backward))))
     if n <= 0:
         return None, 0
     return torch.empty(n, dtype=torch.uint8, device=device), n

@@ -178,7 +178,8 @@ class _ChunkGLAFunction(torch.autograd.Function):
         dh_ws = (None if _full_head(K, V, chunk, q.dtype, True, q, k, v, g, h0, h_ws, do, dht,
                                     dq, dk, dv, dg, dh0)
                  else torch.empty(seq.NC, H, K, V, dtype=q.dtype, device=dev))
-        ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list, q.dtype, dev)
+        ws, nws = _lib.seg_workspace(B, T, H, K, V, chunk, cu_list, q.dtype, dev,
+                                     backward=True)
         call("tops_gla_chunk_bwd", ptr(q), ptr(k), ptr(v), ptr(g), ptr(h0), ptr(h_ws), ptr(do),
              ptr(dht), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), None, ptr(dh_ws), ptr(ws),
              nws, scale, B, T, H, K, V, chunk, *seq.args(), dtype_code(q.dtype),
@@ -576,7 +577,7 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
     h_ws = None if h is not None else torch.empty(seq.NC, H, K, V, dtype=cdt, device=dev)
     dh_ws = (None if _full_head(K, V, C, cdt, True, qq, kk, vv, gg, dd, h, dht, initial_state)
              else torch.empty(seq.NC, H, K, V, dtype=cdt, device=dev))
-    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list, cdt, dev)
+    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, cu_list, cdt, dev, backward=True)
     call("tops_gla_chunk_bwd", ptr(qq), ptr(kk), ptr(vv), ptr(gg),
          ptr(_c(initial_state, torch.float32)), ptr(h), ptr(dd), ptr(_c(dht, torch.float32)),
          ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(dh0), ptr(h_ws), ptr(dh_ws), ptr(ws), nws,

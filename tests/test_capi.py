@@ -174,8 +174,9 @@ def test_seq_layout_chunk_offsets():
 
 
 def test_segment_workspace_query():
-    """Host-only: the workspace = segment states [N, NS, H, K, V] f32 + decays, the per-block
-    gate-range flags (int32), the wide heads' gating, the backward fallback's final states
+    """Host-only: the workspace = segment states [N, NS, H, K, V] f32 + decays (full-head
+    kernels), the gate-range flags (int32: per chunk and head, or per full-head block where
+    that is more), the wide heads' gating, and for the backward the fallback's final states
     [N, H, K, V] f32; each part 256-byte aligned."""
     lib = _lib.load()
     q = lib.tops_gla_chunk_ws_bytes
@@ -184,21 +185,28 @@ def test_segment_workspace_query():
     # -> 4 segments of 32 chunks (one block per CU of 256)
     st = 4 * 4 * 16 * 128 * 128 * 4
     gm = 4 * 4 * 16 * 128 * 4
-    flags = a(4 * 4 * 16 * 4)
+    flags = a(4 * 128 * 16 * 4)          # per chunk and head (more than the 256 blocks)
     ht = 4 * 16 * 128 * 128 * 4
-    assert q(4, 8192, 16, 128, 128, 64, 4, 0, 1) == a(st + a(gm)) + flags + ht
-    # varlen (3 sequences): unsegmented, flags and fallback states only
-    assert q(1, 8192, 16, 128, 128, 64, 3, 1, 1) == a(3 * 16 * 4) + 3 * 16 * 128 * 128 * 4
-    assert q(4, 8192, 16, 128, 128, 64, 3, 0, 1) == 0    # fixed length needs N == B
-    assert q(4, 8192, 16, 128, 128, 64, 4, 0, 0) == 0    # float32: other kernels
-    assert q(4, 8192, 16, 128, 128, 32, 4, 0, 1) == 0    # chunk 32: other kernels
+    assert q(4, 8192, 16, 128, 128, 64, 4, 0, 1, 1) == a(st + a(gm)) + flags + ht
+    assert q(4, 8192, 16, 128, 128, 64, 4, 0, 1, 0) == a(st + a(gm)) + flags   # forward
+    # varlen (3 sequences): unsegmented; flags for at most 8192 / 64 + 3 chunks per head
+    assert q(1, 8192, 16, 128, 128, 64, 3, 1, 1, 1) == a(131 * 16 * 4) + 3 * 16 * 128 * 128 * 4
+    assert q(4, 8192, 16, 128, 128, 64, 3, 0, 1, 1) == 0    # fixed length needs N == B
+    # float32 and chunk 32 (the per-chunk kernels): flags and fallback states only
+    assert q(4, 8192, 16, 128, 128, 64, 4, 0, 0, 1) == flags + ht
+    assert q(4, 8192, 16, 128, 128, 32, 4, 0, 1, 1) == a(4 * 256 * 16 * 4) + ht
+    assert q(4, 8192, 16, 128, 128, 32, 4, 0, 1, 0) == a(4 * 256 * 16 * 4)
     # 4 chunks: too short to split; flags and fallback states
-    assert q(1, 256, 2, 64, 64, 64, 1, 0, 1) == a(2 * 4) + 2 * 64 * 64 * 4
-    # K = 256: V tiles of 64 columns (2 per head) -> 2 segments of 64 chunks; no fused
-    # backward, so no fallback states
+    assert q(1, 256, 2, 64, 64, 64, 1, 0, 1, 1) == a(4 * 2 * 4) + 2 * 64 * 64 * 4
+    # K = 256: V tiles of 64 columns (2 per head) -> 2 segments of 64 chunks; the fallback's
+    # states for the per-chunk backward
     st2, gm2 = 4 * 2 * 16 * 256 * 128 * 4, 4 * 2 * 16 * 256 * 4
-    assert q(4, 8192, 16, 256, 128, 64, 4, 0, 1) == a(st2 + a(gm2)) + a(4 * 2 * 16 * 2 * 4)
-    assert q(4, 8192, 16, 320, 128, 64, 4, 0, 1) == 0    # K > 256: other kernels
+    assert q(4, 8192, 16, 256, 128, 64, 4, 0, 1, 1) == (a(st2 + a(gm2)) + flags
+                                                        + 4 * 16 * 256 * 128 * 4)
+    # K = 320 (per-chunk kernels): flags and states; K or V past 512: no fallback states
+    assert q(4, 8192, 16, 320, 128, 64, 4, 0, 1, 1) == flags + 4 * 16 * 320 * 128 * 4
+    assert q(4, 8192, 16, 128, 640, 64, 4, 0, 1, 1) == flags
+    assert q(4, 8192, 16, 640, 128, 64, 4, 0, 1, 1) == 0    # K > 512: nothing checked
 
 
 def test_kernel_timer_without_launches():

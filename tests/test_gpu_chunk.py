@@ -560,7 +560,7 @@ def test_segmented_scans_match_sequential(B, T, H):
     dev = q.device
     seq = SeqLayout(B, T, C, None, dev)
     st = stream_of(dev)
-    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, False, torch.bfloat16, dev)
+    ws, nws = _lib.seg_workspace(B, T, H, K, V, C, False, torch.bfloat16, dev, backward=True)
     assert nws > 0, "this shape is expected to use sequence segments"
     outs = []
     for w, n in ((None, 0), (ws, nws)):
@@ -792,6 +792,26 @@ STRONG_CASES = [
     # without an initial state; one strong pair among four
     dict(B=2, T=1100, H=2, K=128, V=128, seed=866, mul=5.0, only=(0, 1), h0=True, dht=False),
     dict(B=1, T=700, H=2, K=64, V=64, seed=867, mul=5.0, h0=False, dht=False),
+    # float32 inputs: the per-chunk float32 kernels (fused forward / state scan + output,
+    # per-chunk backward), checked per chunk by the gate-range kernel
+    dict(B=1, T=600, H=2, K=64, V=64, seed=868, mul=5.0, h0=True, dht=True, dtype="f32"),
+    dict(B=2, T=400, H=2, K=128, V=128, seed=869, mul=4.0, only=(1, 1), h0=True, dht=True,
+         dtype="f32"),
+    dict(B=1, T=500, H=2, K=128, V=96, seed=870, mul=4.0, cu=[0, 130, 330, 500], only_seq=1,
+         h0=True, dht=False, dtype="f32"),
+    # wide heads, fixed length: K = 256, V = 512 (eight 64-column V tiles: the gating kernel's
+    # per-chunk flags; the per-chunk backward checked by the same kernel)
+    dict(B=1, T=512, H=2, K=256, V=512, seed=871, mul=4.0, h0=True, dht=True),
+    dict(B=2, T=320, H=2, K=256, V=512, seed=872, mul=4.0, only=(0, 1), h0=True, dht=True),
+    # wide heads, varlen (no gating workspace: the forward's blocks flag themselves)
+    dict(B=1, T=450, H=2, K=256, V=192, seed=873, mul=4.0, cu=[0, 200, 450], only_seq=0,
+         h0=True, dht=True),
+    # K <= 128 with V > 128: full-head forward, per-chunk backward (checked per chunk)
+    dict(B=1, T=640, H=2, K=128, V=256, seed=874, mul=5.0, h0=True, dht=True),
+    dict(B=2, T=300, H=2, K=64, V=384, seed=875, mul=5.0, only=(1, 0), h0=True, dht=False),
+    # a long sequence through the fallback (bf16 dq read back with its rounding residual by
+    # the gate gradient's reverse cumsum over 8192 steps)
+    dict(B=1, T=8192, H=1, K=64, V=64, seed=876, mul=5.0, h0=True, dht=True),
 ]
 
 
@@ -810,20 +830,25 @@ def _strong_inputs(cfg):
         mul[:, cu[i]:cu[i + 1]] = cfg["mul"]
     else:
         mul[:] = cfg["mul"]
-    q, k, v, g, do = (round_bf16(x) for x in (q, k, v, g * mul, do))
+    g = g * mul
+    if cfg.get("dtype", "bf16") == "bf16":
+        q, k, v, g, do = (round_bf16(x) for x in (q, k, v, g, do))
     return q, k, v, g, s0, do, dht, cu
 
 
 @pytest.mark.parametrize("cfg", STRONG_CASES, ids=[f"s{c['seed']}" for c in STRONG_CASES])
 def test_strong_gates(cfg):
-    """bf16 chunk_gla forward and backward with per-token decays of about 4 (chunk gate
-    ranges beyond the full-head kernels' per-element factoring): the flagged (sequence,
+    """chunk_gla forward and backward with per-token decays of 3-5 (chunk gate ranges beyond
+    the kernels' per-element factoring), on every chunked path: the full-head kernels, the
+    wide heads' gating kernel, the per-chunk bf16 and float32 kernels. The flagged (sequence,
     head) pairs are recomputed by the recurrent scans; everything matches the float64
-    oracle at the bf16 bar, and stays finite."""
+    oracle at the dtype's bar (float32: max-abs error 1e-4), and stays finite."""
     G = _gla()
     q, k, v, g, s0, do, dht, cu = _strong_inputs(cfg)
     K = cfg["K"]
-    tq, tk, tv, tg = (to_dev(x, "bf16").requires_grad_() for x in (q, k, v, g))
+    dt = cfg.get("dtype", "bf16")
+    print(f"strong gates {cfg}", flush=True)
+    tq, tk, tv, tg = (to_dev(x, dt).requires_grad_() for x in (q, k, v, g))
     th0 = to_dev(s0, "state") if s0 is not None else None
     if th0 is not None:
         th0.requires_grad_()
@@ -836,11 +861,12 @@ def test_strong_gates(cfg):
     torch.cuda.synchronize()
     on, hn = orc.naive_recurrent_gla(q, k, v, g, initial_state=s0, output_final_state=True,
                                      cu_seqlens=cu)
-    check("o", to_np(o), on, "bf16")
-    check("ht", to_np(ht), hn, "bf16")
+    errs = {"o": check("o", to_np(o), on, dt), "ht": check("ht", to_np(ht), hn, dt)}
     ref = orc.chunk_gla_bwd(q, k, v, g, None, None, K ** -0.5, s0, None, None, do, dht,
                             cu_seqlens=cu, chunk_size=16)
     for name, x, r in zip(["dq", "dk", "dv", "dg"], (tq, tk, tv, tg), ref):
-        check(name, to_np(x.grad), r, "bf16")
+        errs[name] = check(name, to_np(x.grad), r, dt)
     if th0 is not None:
-        check("dh0", to_np(th0.grad), ref[4], "bf16")
+        errs["dh0"] = check("dh0", to_np(th0.grad), ref[4], dt)
+    print(f"  {'max-abs' if dt == 'f32' else 'max-abs / max|ref|'} errors: "
+          + ", ".join(f"{n} {e:.2e}" for n, e in errs.items()), flush=True)
