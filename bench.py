@@ -16,6 +16,12 @@ Other legs (``--op``; not the headline, same JSON fields):
                     sum(out * probe) (flops / bytes: the GLA core, as BASELINE.md counts it);
   simple_gla      : the C4 shape with a per-head constant log-decay (chunk_gla(g_gamma=...)).
 
+The default run (``--op chunk_gla``) first measures the other configurations, C2, C3 and C5
+(the legs above, fixed warmup and step counts each), and reports them compactly under
+``legs`` in the headline's line: ms per step, tokens/s, the step's HBM fraction, and the
+dominant kernel's roofline fraction (C2: fp32 VALU, with its HBM fraction beside it). They
+run before the headline's warmup, so its timed steps also start at the GPU's steady clocks.
+
 The JSON line carries the driver's fields plus
   tflops, mfma_frac   : BASELINE.md section 2 flops of the step / time, / bf16 dense peak;
   step_hbm_frac       : BASELINE.md section 2 algorithmic bytes of the step / time / 8 TB/s;
@@ -275,7 +281,7 @@ LEGS = {"chunk_gla": leg_chunk_gla, "simple_gla": lambda d: leg_chunk_gla(d, sim
 # ---------------------------------------------------------------------------
 
 
-def _c4_stages(x, simple, B, T, H, K, V, C, gamma, reps=10):
+def _c4_stages(x, simple, B, T, H, K, V, C, gamma, reps=25):
     """tops_gla_chunk_fwd / _bwd (or the scalar-gate pair) called back to back through the C
     ABI: whole entry point timed with torch events on the launch stream, the fused kernel
     with the library's HIP events; their difference is the segment preparation."""
@@ -409,86 +415,63 @@ def _measured_traffic(kernel, op):
     return d.get(op, {}).get(kernel)
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    # the GPU reaches its steady clocks after about 40 ms of this load: 5 warmup steps leave
-    # the timed steps 6 % slower than 50 or 200 do
-    ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--op", choices=tuple(LEGS), default="chunk_gla")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-kernel-profile", action="store_true")
-    ap.add_argument("--cpu-procs", type=int, default=0, help="cap on CPU-baseline processes")
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="also run a 512 MiB device copy (HBM counter calibration point)")
-    a = ap.parse_args()
-    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the GLA path shards over batch and "
-              "heads with no communication); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
+def _measure(leg, steps, warmup, timing):
+    """W untimed steps, then K steps timed with torch events on the launch stream (bracketed
+    by synchronizations); with ``timing`` the library's HIP events around every launch of the
+    leg's timed kernels during those K steps. Returns (ms per step, {kernel: ms})."""
     import torch
 
     from tops import _lib
 
     dev = torch.device("cuda:0")
-    leg = LEGS[a.op](dev)
     step = leg["step"]
-    for _ in range(a.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize(dev)
     cur = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    timing = not a.no_kernel_profile
     if timing:   # HIP events around every timed-kernel launch of the timed steps
         _lib.call("tops_gla_kernel_timing", 1)
     e0.record(cur)
-    for _ in range(a.steps):
+    for _ in range(steps):
         step()
     e1.record(cur)
     torch.cuda.synchronize(dev)
-    ms = e0.elapsed_time(e1) / a.steps
-    kernels = {}
+    ms = e0.elapsed_time(e1) / steps
+    kms = {}
     if timing:
         lib = _lib.load()
         for name, kd in leg["kernels"].items():
-            kms = float(lib.tops_gla_kernel_ms(kd["slot"]))
-            if kms <= 0:
-                continue
-            kernels[name] = dict(ms=round(kms, 4), bytes=int(kd["bytes"]),
-                                 gbs=round(kd["bytes"] / (kms * 1e-3) / 1e9, 1))
-            if kd.get("residual"):
-                kernels[name]["residual_bytes"] = int(kd["residual"])
+            x = float(lib.tops_gla_kernel_ms(kd["slot"]))
+            if x > 0:
+                kms[name] = x
         _lib.call("tops_gla_kernel_timing", 0)
+    return ms, kms
+
+
+def _report(leg, ms, kms, op):
+    """The leg's figures: throughput, flop and byte fractions, the dominant kernel's
+    roofline (or the step's, where the work is split over kernels)."""
     sec = ms * 1e-3
-    out = {
-        "metric": leg["metric"],
-        "value": round(leg["tokens"] / sec, 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
-        "ms_per_step": round(ms, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": leg["config"],
-    }
+    out = {"value": round(leg["tokens"] / sec, 1), "ms_per_step": round(ms, 4)}
     if leg["flops"]:
         out["tflops"] = round(leg["flops"] / sec / 1e12, 2)
         out["mfma_frac"] = round(leg["flops"] / sec / MFMA_BF16_PEAK, 4)
     out["step_hbm_frac"] = round(leg["bytes"] / sec / 1e9 / HBM_PEAK_GBS, 4)
     out["step_algorithmic_bytes"] = int(leg["bytes"])
+    kernels = {}
+    for name, x in kms.items():
+        kd = leg["kernels"][name]
+        kernels[name] = dict(ms=round(x, 4), bytes=int(kd["bytes"]),
+                             gbs=round(kd["bytes"] / (x * 1e-3) / 1e9, 1))
+        if kd.get("residual"):
+            kernels[name]["residual_bytes"] = int(kd["residual"])
     if kernels and leg.get("roofline_on_step"):
         gbs = leg["bytes"] / sec / 1e9
         out["roofline"] = {
             "bound": "hbm", "kernel": "step (every kernel of the op)", "achieved": round(gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None}
-        out["kernels"] = kernels
     elif kernels:
         dom = max(kernels, key=lambda n: kernels[n]["ms"])
         d, kd = kernels[dom], leg["kernels"][dom]
@@ -499,17 +482,108 @@ def main():
                 "bound": "valu", "kernel": dom, "achieved": round(achieved, 2),
                 "peak": round(peak, 2), "unit": "T fp32 lane-ops/s (non-packed)",
                 "frac": round(achieved / peak, 4),
-                "traffic": _measured_traffic(dom, a.op),
+                "traffic": _measured_traffic(dom, op),
                 "hbm_achieved_gbs": d["gbs"], "hbm_frac": round(d["gbs"] / HBM_PEAK_GBS, 4)}
         else:
             out["roofline"] = {
                 "bound": "hbm", "kernel": dom, "achieved": d["gbs"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
-                "traffic": _measured_traffic(dom, a.op),
+                "traffic": _measured_traffic(dom, op),
                 "residual_bytes": int(kd.get("residual", 0))}
+    if kernels:
         out["kernels"] = kernels
-        if leg["stages"] is not None:
-            out["stages"] = leg["stages"]()
+    return out
+
+
+# the other BASELINE configurations, measured before the headline leg and reported in its
+# line (compact), in this order: (key, leg name, warmup, timed steps). Every leg's inputs are
+# made first, so the measurements follow one another with the GPU busy throughout (C5's ten
+# warmup steps, about 60 ms, bring it to its steady clocks).
+SIDE_LEGS = (("C5", "layer_c5", 10, 10), ("C3", "chunk_fwd_c3", 5, 20),
+             ("C2", "fused_recurrent", 5, 20))
+
+
+def _side_leg(leg, op, warmup, steps, timing):
+    """One BASELINE configuration other than the headline's, as a compact dict."""
+    ms, kms = _measure(leg, steps, warmup, timing)
+    r = _report(leg, ms, kms, op)
+    d = {"ms_per_step": r["ms_per_step"], "tokens_per_s": r["value"], "steps": steps,
+         "warmup": warmup, "step_hbm_frac": r["step_hbm_frac"]}
+    if "tflops" in r:
+        d["tflops"] = r["tflops"]
+    rf = r.get("roofline")
+    if rf:
+        d["roofline"] = {"kernel": rf["kernel"], "bound": rf["bound"], "frac": rf["frac"]}
+        if rf["bound"] == "valu":
+            d["roofline"]["hbm_frac"] = rf["hbm_frac"]
+        if rf["kernel"] in r.get("kernels", {}):
+            d["roofline"]["kernel_ms"] = r["kernels"][rf["kernel"]]["ms"]
+    return d
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    # the GPU reaches its steady clocks after about 40 ms of this load: 5 warmup steps alone
+    # leave the timed steps 6 % slower than 50 or 200 do (the other configurations' legs,
+    # which run first by default, are such a load as well)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--op", choices=tuple(LEGS), default="chunk_gla")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernel-profile", action="store_true")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the C2 / C3 / C5 legs the default headline run reports")
+    ap.add_argument("--cpu-procs", type=int, default=0, help="cap on CPU-baseline processes")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 512 MiB device copy (HBM counter calibration point)")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the GLA path shards over batch and "
+              "heads with no communication); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    # torch.autograd.grad with grad_outputs imports this module (and sympy) on its first call,
+    # about 0.2 s of host time; imported here, the first step does not leave the GPU idle
+    # between the measurements (after such a gap the step time settles over ~50 steps)
+    import torch.fx.experimental.symbolic_shapes  # noqa: F401
+
+    dev = torch.device("cuda:0")
+    timing = not a.no_kernel_profile
+    leg = LEGS[a.op](dev)
+    legs = {}
+    if a.op == "chunk_gla" and not a.no_legs:
+        side = [(key, op, w, k, LEGS[op](dev)) for key, op, w, k in SIDE_LEGS]
+        for key, op, w, k, sl in side:
+            legs[key] = _side_leg(sl, op, w, k, timing)
+        order = [key for key, *_ in SIDE_LEGS]
+        legs = {key: legs[key] for key in sorted(order)}
+    # the C4 entry points timed on their own: a measurement of the same work, made right before
+    # the headline's warmup (the step time falls for about 30 steps of this work after other
+    # work or idle: measured, 0.69-0.87 -> 0.64 ms)
+    stages = leg["stages"]() if timing and leg["stages"] is not None else None
+    ms, kms = _measure(leg, a.steps, a.warmup, timing)
+    out = {
+        "metric": leg["metric"],
+        "value": None,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": leg["config"],
+    }
+    out.update(_report(leg, ms, kms, a.op))
+    if stages is not None:
+        out["stages"] = stages
+    if legs:
+        out["legs"] = legs
     if a.calibrate_copy:
         n = 512 * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
