@@ -51,8 +51,13 @@ def to_np(t):
     return None if t is None else t.detach().float().cpu().numpy().astype(np.float64)
 
 
-def check(name, got, ref, dtype, atol=None):
-    """Assert the north-star tolerance; returns the measured error."""
+def check(name, got, ref, dtype, atol=None, rel_f32=None):
+    """Assert the north-star tolerance; returns the measured error.
+
+    float32: max-abs error <= 1e-4 (or ``atol``). ``rel_f32`` (a reason) names an output whose
+    values are far from order one (sums over long sequences or wide heads, the unmasked
+    intra matrix): it is held to 1e-4 x max(1, max |ref|) instead, and both errors are
+    printed."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape, f"{name}: shape {got.shape} vs {ref.shape}"
@@ -60,6 +65,11 @@ def check(name, got, ref, dtype, atol=None):
     err = float(np.abs(got - ref).max()) if got.size else 0.0
     if dtype == "f32":
         tol = FP32_ATOL if atol is None else atol
+        if rel_f32 is not None:
+            big = max(1.0, float(np.abs(ref).max()) if ref.size else 1.0)
+            tol = FP32_ATOL * big
+            print(f"  {name}: max-abs error {err:.2e}, max |ref| {big:.1f}, error / max(1, "
+                  f"max|ref|) {err / big:.2e} ({rel_f32})", flush=True)
         assert err <= tol, f"{name}: max-abs error {err:.3e} > {tol:.1e}"
         return err
     scale = float(np.abs(ref).max()) if ref.size else 1.0

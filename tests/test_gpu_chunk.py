@@ -261,14 +261,19 @@ def _run_bwd(cfg, dtype):
 @pytest.mark.parametrize("cfg", BWD_CASES, ids=[_cid(c) for c in BWD_CASES])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_chunk_gla_bwd(cfg, dtype):
+    """Every gradient against the float64 oracle; float32 at the north-star bar, max-abs
+    error 1e-4 (absolute), bf16 at error / max |ref| 2e-2."""
     got, ref = _run_bwd(cfg, dtype)
+    errs = {}
+    # wide heads (K = 256, V = 512): dq / dk / dv sum up to 512 + 64 products per element,
+    # values up to ~10^2, where float32 rounding alone reaches 1e-4
+    wide = "sums over wide heads" if cfg["K"] * cfg["V"] > 128 * 128 else None
     for name, a, b in zip(["dq", "dk", "dv", "dg", "dh0"], got, ref):
         if a is None:
             continue
-        # float32: the 1e-4 bar applies to values of order one; gradients summed over long
-        # chunks (dg, dh0) are compared relative to max(1, max|ref|)
-        atol = 1e-4 * max(1.0, float(np.abs(b).max())) if dtype == "f32" else None
-        check(name, a, b, dtype, atol=atol)
+        errs[name] = check(name, a, b, dtype, rel_f32=wide)
+    print(f"  {dtype} errors: " + ", ".join(f"{n} {e:.2e}" for n, e in errs.items()),
+          flush=True)
 
 
 # ---------------------------------------------------------------------------
@@ -310,7 +315,7 @@ def test_fwd_subfunctions_compose():
     check("ht", to_np(ht), ht_ref, "f32")
     A = G.chunk_gla_fwd_intra_gk(d(q), d(k), gc, K ** -0.5, chunk_size=C)
     A_ref = orc.chunk_gla_fwd_intra_gk(q, k, gc_ref, K ** -0.5, C)
-    check("A", to_np(A), A_ref, "f32", atol=1e-4 * max(1.0, np.abs(A_ref).max()))
+    check("A", to_np(A), A_ref, "f32")
     o = G.chunk_gla_fwd_o_gk(d(q), d(v), gc, A, h, K ** -0.5, chunk_size=C)
     o_ref = orc.chunk_gla_fwd_o_gk(q, v, gc_ref, A_ref, h_ref, K ** -0.5, C)
     check("o", to_np(o), o_ref, "f32")
@@ -350,15 +355,17 @@ def test_small_chunk_forward_subfunctions(cfg, dtype):
     q, k, v, g, s0, do, dht = make_inputs(B, T, H, K, V, cfg["seed"], h0=cfg.get("h0", False),
                                           dht=True, N=N, dtype=dtype)
     d = lambda x: to_dev(x, dtype)  # noqa: E731
-    tol = (lambda ref: 1e-4 * max(1.0, float(np.abs(ref).max()))) if dtype == "f32" \
-        else (lambda ref: None)  # noqa: E731
+    tol = (lambda ref: 1e-4) if dtype == "f32" else (lambda ref: None)  # noqa: E731
     scale = K ** -0.5
     out = G.chunk_gla_fwd(d(q), d(k), d(v), d(g), None, None, scale,
                           to_dev(s0, "state"), True, cu_seqlens=cu, chunk_size=C)
     ref = orc.chunk_gla_fwd(q, k, v, g, None, None, scale, s0, True, cu_seqlens=cu,
                             chunk_size=C)
+    # the intra matrix is unmasked, as the reference returns it: its upper triangle grows as
+    # e^{g~_i - g~_j} with i < j (values up to ~10^3 here)
+    unmasked = "unmasked intra matrix" if dtype == "f32" else None
     for name, a, b in zip(["g_cumsum", "A", "h", "ht", "o"], out, ref):
-        check(name, to_np(a), b, dtype, atol=tol(b))
+        check(name, to_np(a), b, dtype, atol=tol(b), rel_f32=unmasked if name == "A" else None)
     if T % C or cu is not None:
         return   # the pieces below take chunk-aligned, fixed-length inputs
     gc_ref = ref[0]
@@ -367,7 +374,7 @@ def test_small_chunk_forward_subfunctions(cfg, dtype):
     check("h", to_np(h), ref[2], dtype, atol=tol(ref[2]))
     check("ht", to_np(ht), ref[3], dtype, atol=tol(ref[3]))
     A = G.chunk_gla_fwd_intra_gk(d(q), d(k), gc, scale, chunk_size=C)
-    check("A", to_np(A), ref[1], dtype, atol=tol(ref[1]))
+    check("A", to_np(A), ref[1], dtype, atol=tol(ref[1]), rel_f32=unmasked)
     o = G.chunk_gla_fwd_o_gk(d(q), d(v), gc, A, h, scale, chunk_size=C)
     check("o", to_np(o), ref[4], dtype, atol=tol(ref[4]))
     dh_ref, dh0_ref = orc.chunk_bwd_dh(q, gc_ref, do, s0, dht, scale, chunk_size=C)
@@ -388,14 +395,14 @@ def test_chunk_gla_fwd_and_bwd_orchestrators_padded():
     ref = orc.chunk_gla_fwd(q, k, v, g, None, None, K ** -0.5, s0, True, cu_seqlens=cu,
                             chunk_size=C)
     for name, a, b in zip(["g_cumsum", "A", "h", "ht", "o"], out, ref):
-        check(name, to_np(a), b, "f32", atol=1e-4 * max(1.0, np.abs(b).max()))
+        check(name, to_np(a), b, "f32")
     grads = G.chunk_gla_bwd(d(q), d(k), d(v), d(g), None, None, K ** -0.5, to_dev(s0, "state"),
                             out[2], None, d(do), to_dev(dht, "state"), cu_seqlens=cu,
                             chunk_size=C)
     gref = orc.chunk_gla_bwd(q, k, v, g, None, None, K ** -0.5, s0, None, None, do, dht,
                              cu_seqlens=cu, chunk_size=C)
     for name, a, b in zip(["dq", "dk", "dv", "dg", "dh0"], grads, gref):
-        check(name, to_np(a), b, "f32", atol=1e-4 * max(1.0, np.abs(b).max()))
+        check(name, to_np(a), b, "f32")
 
 
 @pytest.mark.parametrize("cfg", [
@@ -423,8 +430,7 @@ def test_chunk_gla_bwd_orchestrator_small_chunks(cfg, dtype):
         if b is None:
             assert a is None, name
             continue
-        atol = 1e-4 * max(1.0, float(np.abs(b).max())) if dtype == "f32" else None
-        check(name, to_np(a), b, dtype, atol=atol)
+        check(name, to_np(a), b, dtype)   # float32: max-abs error 1e-4
 
 
 def test_g_gamma_gradient_reduced():
@@ -440,7 +446,7 @@ def test_g_gamma_gradient_reduced():
     check("o", to_np(o), o_ref, "f32")
     _, _, _, dg_ref, _ = orc.chunk_gla_bwd(q, k, v, None, gg, None, K ** -0.5, None, None, None,
                                            do, None, chunk_size=16)
-    check("dg_gamma", to_np(tgg.grad), dg_ref, "f32", atol=1e-4 * max(1, np.abs(dg_ref).max()))
+    check("dg_gamma", to_np(tgg.grad), dg_ref, "f32")
 
 
 def test_deterministic():
@@ -642,7 +648,7 @@ def test_bwd_parts(cfg):
     dq0, dk0 = r.standard_normal((2, B, T, H, K))
     scale = K ** -0.5
     d = lambda x: to_dev(x, "f32")  # noqa: E731
-    tol = lambda ref: 1e-4 * max(1.0, float(np.abs(ref).max()))  # noqa: E731
+    tol = lambda ref: 1e-4  # noqa: E731
 
     got = G.chunk_gla_bwd_dA_ref(d(v), d(do), scale, chunk_size=C)
     ref = orc.chunk_gla_bwd_dA(v, do, scale, C)
@@ -686,7 +692,7 @@ def test_bwd_parts_compose_to_the_fused_backward():
     ref = orc.chunk_gla_bwd(q, k, v, g, None, None, scale, s0, None, None, do, dht,
                             chunk_size=C)
     for name, a, b in zip(("dq", "dk", "dv", "dg"), (dq, dk, dv, dg), ref):
-        check(name, to_np(a), b, "f32", atol=1e-4 * max(1.0, float(np.abs(b).max())))
+        check(name, to_np(a), b, "f32")
 
 
 # tops.ops.common.chunk_h (reference tops/ops/common/chunk_h.py:137-697): state scans with
@@ -747,7 +753,7 @@ def test_common_chunk_h(cfg):
     d = lambda x: to_dev(x, "f32")  # noqa: E731
     dkw = {name: d(x) for name, x in kw.items()}
     cut = None if cu is None else torch.tensor(cu)
-    tol = lambda ref: 1e-4 * max(1.0, float(np.abs(ref).max()))  # noqa: E731
+    tol = lambda ref: 1e-4  # noqa: E731
 
     h_ref, ht_ref = orc.chunk_fwd_h(k, v, gfull, h0, True, cu_seqlens=cu, chunk_size=C)
     h, ht = CH.chunk_fwd_h_kernel(d(k), d(v), h0=d(h0), output_final_state=True,

@@ -15,7 +15,7 @@ the reference-written layer fixtures on the HIP layer.
 * Reference fixtures (``tests/golden/gla_layer.npz``, written by the reference's torch CPU
   layer): the float32 HIP layer's output and gradients.
 
-Bars: bf16 max-abs error / max |ref| <= 2e-2; float32 max-abs <= 1e-4 x max(1, |ref|).
+Bars: bf16 max-abs error / max |ref| <= 2e-2; float32 max-abs error <= 1e-4.
 """
 
 import os
@@ -195,7 +195,10 @@ def test_layer_matches_reference_fixture(case):
     out, _, _ = m(xd, cu_seqlens=cu)
 
     def close(name, got, ref):
-        check(name, to_np(got), ref, "f32", atol=1e-4 * max(1.0, float(np.abs(ref).max())))
+        # parameter gradients sum over every token of the batch (projections on hipBLASLt)
+        check(name, to_np(got), ref, "f32",
+              rel_f32="sum over the batch's tokens" if name.startswith("d_") and
+              name != "d_x" else None)
 
     close("out", out, fx[f"{case}/out"])
     if grads:

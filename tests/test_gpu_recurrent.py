@@ -99,8 +99,8 @@ def test_fused_recurrent(cfg, dtype):
                                      reverse=cfg.get("reverse", False), cu_seqlens=cu)
     # the recurrent kernel computes in fp32 from the (bf16-rounded) inputs: hold both dtypes
     # to the fp32 bar, relative to the output magnitude for long accumulations
-    check("o", to_np(o), on, "f32", atol=1e-4 * max(1.0, float(np.abs(on).max())))
-    check("ht", to_np(ht), hn, "f32", atol=1e-4 * max(1.0, float(np.abs(hn).max())))
+    check("o", to_np(o), on, "f32")
+    check("ht", to_np(ht), hn, "f32")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -124,7 +124,7 @@ def test_fused_recurrent_c2_all_slices_vs_torch_fp32():
     slices of o and ht against the float32 torch chunked GLA (``tests/torch_ref.py``, pinned
     to the oracle by ``test_torch_ref.py``; the same recurrence in chunk form, 16-token chunks
     so that its gate factors stay small) on the GPU from the same inputs. Bar per slice:
-    max-abs error <= 1e-4 x max(1, max |ref|)."""
+    max-abs error <= 1e-4."""
     import tops.ops.gla as G
     from torch_ref import chunk_gla_torch, slice_errors
 
@@ -143,8 +143,9 @@ def test_fused_recurrent_c2_all_slices_vs_torch_fp32():
     torch.cuda.synchronize()
     for name, x, r, tm in (("o", o, ro, True), ("ht", ht, rht, False)):
         err, scale = slice_errors(x, r, tm)
-        worst = float((err / scale.clamp_min(1.0)).max())
-        print(f"{name}: worst slice error/max(1, max|ref|) {worst:.3e}", flush=True)
+        worst = float(err.max())
+        print(f"{name}: worst slice max-abs error {worst:.3e} (max |ref| "
+              f"{float(scale.max()):.2f})", flush=True)
         assert worst <= 1e-4, name
 
 
@@ -167,7 +168,7 @@ def test_fused_recurrent_c2_shape_slices():
         on, _ = orc.fused_recurrent_gla(sl(q), sl(k), sl(v), gk=sl(gk),
                                         initial_state=to_np(h0[b:b + 1, h:h + 1]),
                                         output_final_state=False)
-        check("o[:256]", sl(o), on, "f32", atol=1e-4 * max(1.0, float(np.abs(on).max())))
+        check("o[:256]", sl(o), on, "f32")
 
 
 # ---------------------------------------------------------------------------
@@ -245,7 +246,7 @@ def _close(name, got, ref):
         assert got is None, f"{name}: expected None"
         return
     assert got is not None and got.dtype == torch.float32, name
-    check(name, to_np(got), ref, "f32", atol=1e-4 * max(1.0, float(np.abs(ref).max())))
+    check(name, to_np(got), ref, "f32")
 
 
 def _bwd_id(c):
@@ -323,7 +324,9 @@ def test_fused_recurrent_bwd_c2_shape_slices():
         for name, g_, r_ in zip(("dq", "dk", "dv", "dgk", "dgv", "dh0"), got, ref):
             if r_ is not None:
                 gs = st(g_) if name == "dh0" else sl(g_)
-                check(name, gs, r_, "f32", atol=1e-4 * max(1.0, float(np.abs(r_).max())))
+                # dgk: a reverse cumsum over 2048 steps of terms of order 10
+                check(name, gs, r_, "f32",
+                      rel_f32="reverse cumsum over 2048 steps" if name == "dgk" else None)
 
 
 def test_non_contiguous_inputs():
@@ -346,5 +349,5 @@ def test_non_contiguous_inputs():
                                   output_final_state=True)
     torch.cuda.synchronize()
     on, hn = orc.fused_recurrent_gla(q, k, v, gk=gk, initial_state=s0, output_final_state=True)
-    check("o", to_np(o), on, "f32", atol=1e-4 * max(1.0, float(np.abs(on).max())))
-    check("ht", to_np(ht), hn, "f32", atol=1e-4 * max(1.0, float(np.abs(hn).max())))
+    check("o", to_np(o), on, "f32")
+    check("ht", to_np(ht), hn, "f32")
