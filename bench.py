@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmarks of the GLA hot path on one MI355X.
+"""Benchmarks of the GLA hot path on one MI355X (the headline configurations C1-C5).
 
 Default (the headline metric, configs[3], "C4"): ``chunk_gla`` forward + backward, B=4 T=8192
 H=16 K=V=128, bf16, chunk 64, h0 and dht. One step = forward (o, ht) + backward (dq, dk, dv,
@@ -13,23 +13,28 @@ Other legs (``--op``; not the headline, same JSON fields):
   chunk_fwd_c3    : configs[2] "C3", chunk_gla forward, B8 T4096 H4 K256 V512 bf16, h0;
   layer_c5        : configs[4] "C5", GatedLinearAttention forward + backward, bf16, B2
                     T16384 hidden 2048, 4 heads (K 256, V 512), weights ~ N(0, 0.02), loss =
-                    sum(out * probe) (flops / bytes: the GLA core, as BASELINE.md counts it);
-  simple_gla      : the C4 shape with a per-head constant log-decay (chunk_gla(g_gamma=...)).
+                    sum(out * probe) (flops / bytes: the GLA core's);
+  simple_gla      : the C4 shape with a per-head constant log-decay (chunk_gla(g_gamma=...));
+  decode_t1 / _t64: fused_recurrent_gla forward at a decode shape, B64 H16 K=V=128, T = 1 / 64:
+                    the recurrent kernel where HBM, not VALU, bounds it.
 
-The default run (``--op chunk_gla``) first measures the other configurations, C2, C3 and C5
-(the legs above, fixed warmup and step counts each), and reports them compactly under
+The default run (``--op chunk_gla``) first measures the other configurations, C2, C3 and C5,
+and the two decode shapes (the legs above, fixed warmup and step counts each), and reports
+them compactly under
 ``legs`` in the headline's line: ms per step, tokens/s, the step's HBM fraction, and the
 dominant kernel's roofline fraction (C2: fp32 VALU, with its HBM fraction beside it). They
 run before the headline's warmup, so its timed steps also start at the GPU's steady clocks.
 
 The JSON line carries the driver's fields plus
-  tflops, mfma_frac   : BASELINE.md section 2 flops of the step / time, / bf16 dense peak;
-  step_hbm_frac       : BASELINE.md section 2 algorithmic bytes of the step / time / 8 TB/s;
+  tflops, mfma_frac   : the step's flops (per token-head: forward 4KV + 2C(K+V), backward
+                        twice that) / time, / bf16 dense peak;
+  step_hbm_frac       : the step's algorithmic bytes (every input read once, every output
+                        written once) / time / 8 TB/s;
   roofline            : the dominant kernel of the step, timed inside the timed steps with
                         HIP events the library records on the launch stream (torch's current
                         stream) around every launch of it, against its binding roofline with
                         its algorithmic bytes (every input read once, every output written
-                        once, BASELINE.md section 2; the per-chunk state residual h / dh is
+                        once; the per-chunk state residual h / dh is
                         implementation traffic, reported apart) -- or, for the recurrent
                         kernel, its fp32 VALU lane-ops against the non-packed VALU peak with
                         the HBM fraction beside it; ``traffic`` = its HBM bytes per launch
@@ -67,7 +72,8 @@ KT_HEAD_FWD, KT_HEAD_BWD, KT_REC_FWD, KT_BWD_DQKG = 0, 1, 2, 3
 
 
 def _flops(T_tok, H, K, V, C, fwd=True, bwd=False):
-    """per token-head fwd 4KV + 2C(K+V), bwd twice that."""
+    """Flops per token-head: forward 4KV + 2C(K+V) (state and chunk products), backward
+    twice that."""
     per = (4 * K * V + 2 * C * (K + V)) * (int(fwd) + 2 * int(bwd))
     return T_tok * H * per
 
@@ -195,6 +201,37 @@ def leg_fused_recurrent(dev):
     )
 
 
+def leg_recurrent_decode(dev, T):
+    """fused_recurrent_gla forward at a decode shape: B64 H16 K=V=128,
+    T = 1 or 64 tokens, bf16 inputs, h0 and the final state fp32, o fp32 -- the shape where
+    the recurrent kernel is bound by HBM (state in and out) rather than by its VALU work."""
+    import torch
+
+    import tops.ops.gla as G
+
+    B, H, K, V = 64, 16, 128, 128
+    raw = _rng_inputs((B, T, H, K), V, 6 + T)
+    x = _to_dev(raw, dev)
+
+    def step():
+        with torch.no_grad():
+            return G.fused_recurrent_gla(x["q"], x["k"], x["v"], gk=x["g"],
+                                         initial_state=x["h0"], output_final_state=True)
+
+    tok = B * T * H
+    nbytes = tok * (3 * K + V) * BF + tok * V * F4 + 2 * B * H * K * V * F4
+    return dict(
+        metric=f"fused_recurrent_gla fwd (decode) tokens/s, B64 T{T} H16 K=V=128",
+        tokens=B * T, flops=None, bytes=nbytes, step=step,
+        config={"workload": f"fused_recurrent_gla fwd + final state, decode shape T={T}",
+                "B": B, "T": T, "H": H, "K": K, "V": V, "h0": True, "o_dtype": "f32",
+                "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
+        kernels={"rec_scan_kernel": dict(slot=KT_REC_FWD, bytes=nbytes, residual=0,
+                                         lane_ops=3 * tok * K * V)},
+        bound="hbm", cpu=None, stages=None,
+    )
+
+
 def leg_chunk_fwd_c3(dev):
     """C3: chunk_gla forward, wide heads."""
     import torch
@@ -265,15 +302,16 @@ def leg_layer_c5(dev):
                 "global_batch": B, "seq_len": T, "parallelism": "single-gpu",
                 "counted": "GLA core flops/bytes (projections are hipBLASLt GEMMs, not counted)"},
         kernels={"head_fwd_kernel": dict(slot=KT_HEAD_FWD, bytes=fwd_b, residual=resid // 2),
-                 "chunk_bwd_dqkg_kernel": dict(slot=KT_BWD_DQKG, bytes=dqkg_b,
-                                               residual=resid)},
+                 "head_dqkg_kernel": dict(slot=KT_BWD_DQKG, bytes=dqkg_b, residual=resid)},
         bound="hbm", cpu=None, stages=None,
     )
 
 
 LEGS = {"chunk_gla": leg_chunk_gla, "simple_gla": lambda d: leg_chunk_gla(d, simple=True),
         "fused_recurrent": leg_fused_recurrent, "chunk_fwd_c3": leg_chunk_fwd_c3,
-        "layer_c5": leg_layer_c5}
+        "layer_c5": leg_layer_c5,
+        "decode_t1": lambda d: leg_recurrent_decode(d, 1),
+        "decode_t64": lambda d: leg_recurrent_decode(d, 64)}
 
 
 # ---------------------------------------------------------------------------
@@ -485,11 +523,15 @@ def _report(leg, ms, kms, op):
                 "traffic": _measured_traffic(dom, op),
                 "hbm_achieved_gbs": d["gbs"], "hbm_frac": round(d["gbs"] / HBM_PEAK_GBS, 4)}
         else:
+            res = int(kd.get("residual", 0))
             out["roofline"] = {
                 "bound": "hbm", "kernel": dom, "achieved": d["gbs"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
                 "traffic": _measured_traffic(dom, op),
-                "residual_bytes": int(kd.get("residual", 0))}
+                "residual_bytes": res,
+                # the same launch with its per-chunk state traffic counted as well
+                "frac_with_residual": round((kd["bytes"] + res) / (d["ms"] * 1e-3) / 1e9 /
+                                            HBM_PEAK_GBS, 4)}
     if kernels:
         out["kernels"] = kernels
     return out
@@ -499,7 +541,8 @@ def _report(leg, ms, kms, op):
 # line (compact), in this order: (key, leg name, warmup, timed steps). Every leg's inputs are
 # made first, so the measurements follow one another with the GPU busy throughout (C5's ten
 # warmup steps, about 60 ms, bring it to its steady clocks).
-SIDE_LEGS = (("C5", "layer_c5", 10, 10), ("C3", "chunk_fwd_c3", 5, 20),
+SIDE_LEGS = (("D1", "decode_t1", 5, 50), ("D64", "decode_t64", 5, 50),
+             ("C5", "layer_c5", 10, 10), ("C3", "chunk_fwd_c3", 5, 20),
              ("C2", "fused_recurrent", 5, 20))
 
 
@@ -516,6 +559,10 @@ def _side_leg(leg, op, warmup, steps, timing):
         d["roofline"] = {"kernel": rf["kernel"], "bound": rf["bound"], "frac": rf["frac"]}
         if rf["bound"] == "valu":
             d["roofline"]["hbm_frac"] = rf["hbm_frac"]
+        if rf.get("residual_bytes"):
+            d["roofline"]["frac_with_residual"] = rf["frac_with_residual"]
+        if rf["bound"] == "hbm" and rf["unit"] == "GB/s" and rf["kernel"] in r.get("kernels", {}):
+            d["roofline"]["gbs"] = rf["achieved"]
         if rf["kernel"] in r.get("kernels", {}):
             d["roofline"]["kernel_ms"] = r["kernels"][rf["kernel"]]["ms"]
     return d

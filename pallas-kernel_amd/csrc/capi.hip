@@ -976,7 +976,13 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const void* 
   p.V = (int)V;
   p.vec = vec_ok(dtype, K, V, {q, k, v, g, dout, h, dh_ws, dq, dk, dv, dg});
   p.si = si;
-  rc = hip_status(tops::run_chunk_bwd(p, dtype, st), "chunk_bwd (gradients)");
+  if (head && tops::head_dqkg_supported((int)K, (int)V)) {
+    // dq, dk, dg one block per (chunk, head) over every V tile; dv by the per-chunk kernel
+    rc = hip_status(tops::run_head_dqkg(p, st), "chunk_bwd (dq, dk, dg)");
+    if (!rc) rc = hip_status(tops::run_chunk_bwd(p, dtype, st, 2), "chunk_bwd (dv)");
+  } else {
+    rc = hip_status(tops::run_chunk_bwd(p, dtype, st), "chunk_bwd (gradients)");
+  }
   if (rc || cflags == nullptr) return rc;
   // sequences and heads with a chunk beyond the factoring's range: the recurrent backward
   // (exact for any decay) rewrites their dq, dk, dv, dg and dh0

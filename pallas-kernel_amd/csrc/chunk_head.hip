@@ -1029,6 +1029,410 @@ __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Per-chunk dq, dk, dg of heads wider than 64 on the per-chunk backward (bf16, chunk 64, K in
+// (64, 256], any V): one 256-thread block per (chunk, head, 128-column key slice), streaming
+// V in 64-column tiles. With G the base-2 chunk-local cumsum of the gates, R = (G_first +
+// Gamma) / 2 per column, Gamma its last row, h the state entering the chunk and dh the
+// gradient of the state leaving it:
+//   qg = q 2^{G-R}, kg = k 2^{R-G}, dA = scale tril(do v^T)
+//   Xq = dA kg + scale 2^R (do h^T),  Xm = 2^{Gamma-R} (v dh^T),  Xk = dA^T qg + Xm
+//   dq = 2^{G-R} Xq,  dk = 2^{R-G} Xk
+//   dg = revcumsum_rows(qg Xq - kg Xk) + 2^Gamma sum_v h dh + sum_rows kg Xm
+// Every product is formed transposed ([k x i] tiles): an accumulator lane then holds four
+// consecutive key columns of one chunk row, i.e. 8-byte row pieces of dq, dk, dg, qg and kg.
+// Wave w owns key tiles KTW w .. KTW w + KTW - 1 of the slice over all 64 rows, so the chunk
+// cumsum of the gates and dg's reverse cumsum over the rows run inside the wave (DPP row
+// shifts over the 16 lanes of a row group, a running total over the four row tiles): no
+// block-wide exchange. do and v tiles are staged in LDS; h and dh fragments are read straight
+// from HBM (16 bytes a lane), each by the one wave that uses it, one V tile ahead; dA is formed
+// once per slice. Two blocks share a CU (61.5 KB of LDS, two waves per SIMD), so one block's
+// gating and epilogue run under the other's V loop; the two slices of a K = 256 head are
+// adjacent blocks (one XCD), whose do / v reads meet in its L2. Replaces a grid of (chunk,
+// head, 64-column key tile) blocks, each of which read all of do and v and formed dA again.
+// ---------------------------------------------------------------------------
+constexpr int DKB = 128;   // key columns per block
+constexpr int DNW = 4;     // waves per block
+// LDS of the V loop (do, v: 64 x 64; h, dh: the slice's KB key rows x 64), then, over the
+// same bytes, of the epilogue (q -> qg, k -> kg, g: 64 x KB; dA 64 x 64)
+template <int KB>
+struct HDLayout {
+  static constexpr int TB = LT<64>::bytes(HC);
+  static constexpr int HB = LT<64>::bytes(KB);
+  static constexpr int GB = LT<KB>::bytes(HC);
+  static constexpr int dout = 0, v = TB, h = 2 * TB, dh = 2 * TB + HB;
+  static constexpr int loop_end = 2 * TB + 2 * HB;
+  static constexpr int qg = 0, kg = GB, g = 2 * GB, da = 3 * GB;
+  static constexpr int after_end = 3 * GB + TB;
+  static constexpr int bytes = loop_end > after_end ? loop_end : after_end;
+};
+
+// x + the value `SH` lanes below (row_shr) or above (row_shl) within each 16-lane row, zero
+// past the row's end (bound_ctrl)
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __uint_as_float(
+                 __builtin_amdgcn_update_dpp(0u, __float_as_uint(x), CTRL, 0xF, 0xF, true));
+}
+// inclusive prefix / suffix over the 16 lanes of each row
+__device__ __forceinline__ float row16_prefix(float x) {
+  x = dpp_add<0x111>(x);
+  x = dpp_add<0x112>(x);
+  x = dpp_add<0x114>(x);
+  return dpp_add<0x118>(x);
+}
+__device__ __forceinline__ float row16_suffix(float x) {
+  x = dpp_add<0x101>(x);
+  x = dpp_add<0x102>(x);
+  x = dpp_add<0x104>(x);
+  return dpp_add<0x108>(x);
+}
+
+// 4 bf16 (8 bytes) <-> floats
+__device__ __forceinline__ void unpack4(const uint2& u, float (&x)[4]) {
+  x[0] = bf16_lo(u.x); x[1] = bf16_hi(u.x);
+  x[2] = bf16_lo(u.y); x[3] = bf16_hi(u.y);
+}
+__device__ __forceinline__ uint2 pack4(const float (&x)[4]) {
+  return make_uint2(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]));
+}
+
+// Base-2 chunk cumsum of one key tile in the transposed accumulator layout: x[mi][r] holds the
+// raw gate of row 16 mi + (lane & 15), column 4 (lane >> 4) + r (rows past the chunk zero);
+// on return G (base 2, inclusive over the rows), R = (G_first + Gamma) / 2 and Gamma.
+__device__ __forceinline__ void acc_cumsum(float (&x)[4][4], float (&R)[4], float (&Gm)[4],
+                                           int lane) {
+  float run[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pre = row16_prefix(x[mi][r] * kLog2e);
+      const float tot = __shfl(pre, lane | 15);   // the row group's total
+      x[mi][r] = run[r] + pre;
+      run[r] += tot;
+    }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float first = __shfl(x[0][r], lane & 0x30);   // row 0
+    Gm[r] = run[r];
+    R[r] = 0.5f * (first + run[r]);
+  }
+}
+
+template <int KB, int NW>
+__global__ __launch_bounds__(NW * 64) void head_dqkg_kernel(BwdArgs p) {
+  using Lay = HDLayout<KB>;
+  constexpr int NT = NW * 64;
+  constexpr int KTW = KB / 16 / NW;   // key tiles per wave
+  static_assert(KTW >= 1 && KTW * 16 * NW == KB, "key tiles over the waves");
+  // 16-byte pieces per thread: a 64 x 64 tile, a KB x 64 slice of h / dh, a 64 x KB slice of
+  // q / k / g (8 or KB / 8 pieces a row)
+  constexpr int P64 = 64 * 8 / NT, PH = KB * 8 / NT, PK = 64 * (KB / 8) / NT;
+  static_assert(P64 * NT == 512 && PH * NT == KB * 8 && PK * NT == 8 * KB, "staging map");
+  constexpr int NDA = 16 / NW;        // dA tiles (lower and upper) per wave
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  bf16* sDo = reinterpret_cast<bf16*>(smem + Lay::dout);
+  bf16* sV = reinterpret_cast<bf16*>(smem + Lay::v);
+  bf16* sH = reinterpret_cast<bf16*>(smem + Lay::h);
+  bf16* sDh = reinterpret_cast<bf16*>(smem + Lay::dh);
+  bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
+  bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
+  bf16* sG = reinterpret_cast<bf16*>(smem + Lay::g);
+  bf16* sdA = reinterpret_cast<bf16*>(smem + Lay::da);
+
+  const int H = p.H, K = p.K, V = p.V;
+  const int KS = (K + KB - 1) / KB;   // key slices per head
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int kb = (L % KS) * KB;       // the slice's first key column
+  const int c = (L / KS) / H, hh = (L / KS) % H;
+  int seq, t0, len;
+  chunk_range(p.si, c, seq, t0, len);
+  (void)seq;
+  const uint32_t rsK = (uint32_t)(H * K), rsV = (uint32_t)(H * V);
+  const long oK = (long)t0 * rsK + (long)hh * K, oV = (long)t0 * rsV + (long)hh * V;
+  const bf16* __restrict__ q = (const bf16*)p.q + oK;
+  const bf16* __restrict__ k = (const bf16*)p.k + oK;
+  const bf16* __restrict__ g = (const bf16*)p.g + oK;
+  const bf16* __restrict__ v = (const bf16*)p.v + oV;
+  const bf16* __restrict__ dout = (const bf16*)p.dout + oV;
+  const long KV = (long)K * V;
+  const bf16* __restrict__ hc = (const bf16*)p.h + ((long)c * H + hh) * KV;
+  const bf16* __restrict__ dhc = (const bf16*)p.dh + ((long)c * H + hh) * KV;
+  const float scale = p.scale;
+  const int VT = (V + 63) >> 6;
+  const int kt0 = w * KTW;   // this wave's first key tile in the slice
+  const int ri = lane & 15;
+
+  // ---- staging: whole 128-byte row pieces (8 lanes a row), rows / columns past the chunk
+  // or the head as zeros ----
+  // V tile vt of do, v (rows: chunk rows) and of h, dh (rows: the slice's key rows)
+  auto ld_v = [&](int vt, uint4 (&rd)[P64], uint4 (&rv)[P64], uint4 (&rh)[PH],
+                  uint4 (&rdh)[PH]) {
+#pragma unroll
+    for (int e = 0; e < P64; ++e) {
+      const int pc = tid + NT * e, row = pc >> 3, col = vt * 64 + 8 * (pc & 7);
+      const uint32_t off = ((uint32_t)min(row, len - 1) * rsV + (uint32_t)min(col, V - 8)) * 2u;
+      rd[e] = ld16(dout, off);
+      rv[e] = ld16(v, off);
+      if (row >= len || col >= V) rd[e] = rv[e] = make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < PH; ++e) {
+      const int pc = tid + NT * e, row = kb + (pc >> 3), col = vt * 64 + 8 * (pc & 7);
+      const uint32_t off = ((uint32_t)min(row, K - 1) * (uint32_t)V +
+                            (uint32_t)min(col, V - 8)) * 2u;
+      rh[e] = ld16(hc, off);
+      rdh[e] = ld16(dhc, off);
+      if (row >= K || col >= V) rh[e] = rdh[e] = make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto st_v = [&](const uint4 (&rd)[P64], const uint4 (&rv)[P64], const uint4 (&rh)[PH],
+                  const uint4 (&rdh)[PH]) {
+#pragma unroll
+    for (int e = 0; e < P64; ++e) {
+      const int pc = tid + NT * e;
+      const int o = LT<64>::off(pc >> 3, 8 * (pc & 7));
+      *reinterpret_cast<uint4*>(sDo + o) = rd[e];
+      *reinterpret_cast<uint4*>(sV + o) = rv[e];
+    }
+#pragma unroll
+    for (int e = 0; e < PH; ++e) {
+      const int pc = tid + NT * e;
+      const int o = LT<64>::off(pc >> 3, 8 * (pc & 7));
+      *reinterpret_cast<uint4*>(sH + o) = rh[e];
+      *reinterpret_cast<uint4*>(sDh + o) = rdh[e];
+    }
+  };
+  // the chunk's q, k, g over the slice's key columns
+  auto ld_k = [&](uint4 (&rq)[PK], uint4 (&rk)[PK], uint4 (&rg)[PK]) {
+#pragma unroll
+    for (int e = 0; e < PK; ++e) {
+      const int pc = tid + NT * e, row = pc / (KB / 8), col = kb + 8 * (pc % (KB / 8));
+      const uint32_t off = ((uint32_t)min(row, len - 1) * rsK + (uint32_t)min(col, K - 8)) * 2u;
+      rq[e] = ld16(q, off);
+      rk[e] = ld16(k, off);
+      rg[e] = ld16(g, off);
+      if (row >= len || col >= K) rq[e] = rk[e] = rg[e] = make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto st_k = [&](const uint4 (&rq)[PK], const uint4 (&rk)[PK], const uint4 (&rg)[PK]) {
+#pragma unroll
+    for (int e = 0; e < PK; ++e) {
+      const int pc = tid + NT * e;
+      const int o = LT<KB>::off(pc / (KB / 8), 8 * (pc % (KB / 8)));
+      *reinterpret_cast<uint4*>(sQg + o) = rq[e];
+      *reinterpret_cast<uint4*>(sKg + o) = rk[e];
+      *reinterpret_cast<uint4*>(sG + o) = rg[e];
+    }
+  };
+
+  // dA tiles (as [j x i] products): wave w takes tiles w + NW e, e < 16 / NW; tiles 0..9 are
+  // the lower ones (j tile <= i tile; tile u: mi with mi (mi + 1) / 2 <= u, nj = u - mi (mi +
+  // 1) / 2), 10..15 the upper ones, written as zeros (rows 0, 0, 0, 1, 1, 2, columns 1, 2, 3,
+  // 2, 3, 3). Arithmetic, not a table: the values are uniform.
+  int dmi[NDA], dnj[NDA];
+#pragma unroll
+  for (int e = 0; e < NDA; ++e) {
+    const int u = w + NW * e;
+    if (u < 10) {
+      dmi[e] = (u >= 1) + (u >= 3) + (u >= 6);
+      dnj[e] = u - dmi[e] * (dmi[e] + 1) / 2;
+    } else {
+      const int x = u - 10;
+      dmi[e] = (x >= 3) + (x >= 5);
+      dnj[e] = dmi[e] == 0 ? x + 1 : dmi[e] == 1 ? x - 1 : 3;
+    }
+  }
+
+  // ---- V loop: do h^T, v dh^T (all key tiles of the wave), dA, sum_v h dh ----
+  f32x4 Mq[KTW][4], M2[KTW][4], dA[NDA];
+#pragma unroll
+  for (int t = 0; t < KTW; ++t)
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) Mq[t][mi] = M2[t][mi] = zero4();
+#pragma unroll
+  for (int e = 0; e < NDA; ++e) dA[e] = zero4();
+  float hd[KTW];
+#pragma unroll
+  for (int t = 0; t < KTW; ++t) hd[t] = 0.f;
+  const int rf = LT<64>::row_frag(lane);
+
+  uint4 rd[P64], rv[P64], rh[PH], rdh[PH];
+  ld_v(0, rd, rv, rh, rdh);
+#pragma unroll 1
+  for (int vt = 0; vt < VT; ++vt) {
+    st_v(rd, rv, rh, rdh);
+    __syncthreads();   // this V tile in LDS
+    if (vt + 1 < VT) ld_v(vt + 1, rd, rv, rh, rdh);
+#pragma unroll
+    for (int t = 0; t < KTW; ++t) {
+      Frag<bf16> fh[2], fdh[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int o = LT<64>::at((kt0 + t) * 16, 32 * s) + rf;
+        fh[s] = ldr(sH, o);
+        fdh[s] = ldr(sDh, o);
+        hd[t] = dot8_bf16(fh[s].d, fdh[s].d, hd[t]);
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const int o = LT<64>::at(16 * mi, 32 * s) + rf;
+          mma(Mq[t][mi], fh[s], ldr(sDo, o));
+          mma(M2[t][mi], fdh[s], ldr(sV, o));
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < NDA; ++e) {
+      if (w + NW * e < 10) {   // uniform
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          mma(dA[e], ldr(sV, LT<64>::at(16 * dnj[e], 32 * s) + rf),
+              ldr(sDo, LT<64>::at(16 * dmi[e], 32 * s) + rf));
+      }
+    }
+    __syncthreads();   // this tile's readers are done
+  }
+
+  // ---- q, k, g of the slice into LDS (over the V loop's tiles), dA, the gating ----
+  {
+    uint4 rq[PK], rk[PK], rg[PK];
+    ld_k(rq, rk, rg);
+    st_k(rq, rk, rg);
+  }
+  const int o0 = LT<64>::acc_pos(lane);
+#pragma unroll
+  for (int e = 0; e < NDA; ++e) {
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+    if (w + NW * e < 10) {
+      const int i = 16 * dmi[e] + ri;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * dnj[e] + 4 * (lane >> 4) + r;
+        x[r] = j <= i ? dA[e][r] * scale : 0.f;
+      }
+    }
+    *reinterpret_cast<uint2*>(sdA + LT<64>::at(16 * dmi[e], 16 * dnj[e]) + o0) = pack4(x);
+  }
+  __syncthreads();   // q, k, g, dA in LDS
+  // the lane's piece of a [k x i] tile of the slice: row 16 mi + (lane & 15), key columns
+  // kc + 4 (lane >> 4) .. + 3 (the accumulator position of a transposed product)
+  auto piece = [&](const bf16* t_, int mi, int kc, float (&x)[4]) {
+    unpack4(*reinterpret_cast<const uint2*>(t_ + LT<KB>::at(16 * mi, kc) + LT<KB>::acc_pos(lane)),
+            x);
+  };
+  // gating of the wave's own key tiles, in place (q -> qg, k -> kg): the wave reads and writes
+  // only its own columns, each lane only its own pieces
+  float G[KTW][4][4], R[KTW][4], Gm[KTW][4];
+#pragma unroll
+  for (int t = 0; t < KTW; ++t) {
+    const int kc = (kt0 + t) * 16;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) piece(sG, mi, kc, G[t][mi]);
+    acc_cumsum(G[t], R[t], Gm[t], lane);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      float xq[4], xk[4];
+      piece(sQg, mi, kc, xq);
+      piece(sKg, mi, kc, xk);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float d = G[t][mi][r] - R[t][r];
+        xq[r] *= exp2_hw(d);
+        xk[r] *= exp2_hw(-d);
+      }
+      const int o = LT<KB>::at(16 * mi, kc) + LT<KB>::acc_pos(lane);
+      *reinterpret_cast<uint2*>(sQg + o) = pack4(xq);
+      *reinterpret_cast<uint2*>(sKg + o) = pack4(xk);
+    }
+  }
+
+  // ---- per key tile: the chunk products, then dq, dk, dg ----
+  bf16* __restrict__ dq = (bf16*)p.dq + oK;
+  bf16* __restrict__ dk = (bf16*)p.dk + oK;
+  bf16* __restrict__ dg = (bf16*)p.dg + oK;
+  const int tf = LT<KB>::tr_frag(lane), tf64 = LT<64>::tr_frag(lane);
+#pragma unroll
+  for (int t = 0; t < KTW; ++t) {
+    const int kc = (kt0 + t) * 16;
+    f32x4 Mqi[4], Mk1[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      Mqi[mi] = Mk1[mi] = zero4();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        // Xq: sum_j kg[j][k] dA[i][j]; Xk: sum_i qg[i][k] dA[i][j] (row tile mi as j)
+        mma(Mqi[mi], ldt<KB>(sKg, LT<KB>::at(32 * s, kc) + tf),
+            ldr(sdA, LT<64>::at(16 * mi, 32 * s) + rf));
+        mma(Mk1[mi], ldt<KB>(sQg, LT<KB>::at(32 * s, kc) + tf),
+            ldt<64>(sdA, LT<64>::at(32 * s, 16 * mi) + tf64));
+      }
+    }
+    // sum_v h dh: lane (lane & 15) of every row group holds row kc + (lane & 15) after the
+    // sum over the four column groups; taken for rows kc + 4 (lane >> 4) + r
+    float hs = hd[t];
+    hs += __shfl_xor(hs, 16);
+    hs += __shfl_xor(hs, 32);
+    float fr[4], fe[4], hdp[4], y[4][4], dkc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      hdp[r] = __shfl(hs, 4 * (lane >> 4) + r);
+      fr[r] = scale * exp2_hw(R[t][r]);
+      fe[r] = exp2_hw(Gm[t][r] - R[t][r]);
+      dkc[r] = 0.f;
+    }
+    const int k4 = kb + kc + 4 * (lane >> 4);
+    const bool kin = k4 < K;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      const int i = 16 * mi + ri;
+      float qv[4], kv[4], vq[4], vk[4];
+      piece(sQg, mi, kc, qv);
+      piece(sKg, mi, kc, kv);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float xq = Mqi[mi][r] + fr[r] * Mq[t][mi][r];
+        const float xm = fe[r] * M2[t][mi][r];
+        const float xk = Mk1[mi][r] + xm;
+        const float d = G[t][mi][r] - R[t][r];
+        vq[r] = exp2_hw(d) * xq;
+        vk[r] = exp2_hw(-d) * xk;
+        y[mi][r] = qv[r] * xq - kv[r] * xk;
+        dkc[r] += kv[r] * xm;
+      }
+      if (i < len && kin) {
+        const uint32_t off = ((uint32_t)i * rsK + (uint32_t)k4) * 2u;
+        st8(dq, off, pack4(vq));
+        st8(dk, off, pack4(vk));
+      }
+    }
+    // dg = suffix over the rows of y + 2^Gamma sum_v h dh + sum_rows kg Xm
+    float add[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float tot = __shfl(row16_prefix(dkc[r]), lane | 15);
+      add[r] = exp2_hw(Gm[t][r]) * hdp[r] + tot;
+    }
+    float run[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mi = 3; mi >= 0; --mi) {
+      const int i = 16 * mi + ri;
+      float x[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float suf = row16_suffix(y[mi][r]);
+        x[r] = suf + run[r] + add[r];
+        run[r] += __shfl(suf, lane & 0x30);   // the row group's total (its row 0)
+      }
+      if (i < len && kin) st8(dg, ((uint32_t)i * rsK + (uint32_t)k4) * 2u, pack4(x));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Fused forward: per chunk (base-2 gates, r = (g~_first + gamma) / 2 per column)
 //   qg = q 2^{g~-r}, kg = k 2^{r-g~}, kd = kg 2^{gamma-r}, A = scale tril(qg kg^T),
 //   o = A v + qg (scale 2^r h), h <- 2^{gamma} h + kd^T v.
@@ -2318,6 +2722,30 @@ hipError_t run_head_gate(const HeadFwdArgs& p, hipStream_t st) {
   hipLaunchKernelGGL((head_gate_kernel<256>), dim3((unsigned)(nt * p.H), (unsigned)p.si.N),
                      dim3(HNT), GL::bytes, st, p);
   return hipGetLastError();
+}
+
+static hipError_t launch_head_dqkg(const BwdArgs& p, hipStream_t st) {
+  const long blocks = (long)p.si.NC * p.H * ((p.K + DKB - 1) / DKB);
+  if (blocks == 0) return hipSuccess;
+  if (blocks > 2147483647L) return hipErrorInvalidValue;
+  using Lay = HDLayout<DKB>;
+  static_assert(2 * Lay::bytes <= 163840, "two blocks per CU");
+  hipError_t e = hipFuncSetAttribute((const void*)head_dqkg_kernel<DKB, DNW>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
+  if (e != hipSuccess) return e;
+  ktimer_mark(KT_BWD_DQKG, false, st);
+  hipLaunchKernelGGL((head_dqkg_kernel<DKB, DNW>), dim3((unsigned)blocks), dim3(DNW * 64),
+                     Lay::bytes, st, p);
+  ktimer_mark(KT_BWD_DQKG, true, st);
+  return hipGetLastError();
+}
+
+bool head_dqkg_supported(int K, int V) { return K > 64 && K <= 256 && V >= 8; }
+
+hipError_t run_head_dqkg(const BwdArgs& p, hipStream_t st) {
+  if (!head_dqkg_supported(p.K, p.V) || p.K % 8 || p.V % 8 || p.si.C != HC)
+    return hipErrorInvalidValue;
+  return launch_head_dqkg(p, st);
 }
 
 template <int KP, int VP>

@@ -306,6 +306,12 @@ struct HeadBwdArgs {
 };
 hipError_t run_head_bwd(const HeadBwdArgs& p, hipStream_t st);
 
+// Per-chunk dq, dk, dg of the per-chunk backward for bf16 heads of K in (64, 256] (any V,
+// multiples of 8), chunk 64: one block per (chunk, head), V streamed in 64-column tiles
+// (chunk_head.hip). p.gate_ws, p.dv and p.vec are not used.
+bool head_dqkg_supported(int K, int V);
+hipError_t run_head_dqkg(const BwdArgs& p, hipStream_t st);
+
 // Optional HIP-event timing of the fused full-head kernels (a measurement hook): when
 // enabled, an event is recorded on the launch stream right before and after the kernel.
 enum { KT_HEAD_FWD = 0, KT_HEAD_BWD = 1, KT_REC_FWD = 2, KT_BWD_DQKG = 3, KT_COUNT = 4 };

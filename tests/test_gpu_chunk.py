@@ -220,6 +220,11 @@ BWD_CASES = [
     # varlen wide head (no gating workspace)
     dict(B=1, T=400, H=2, K=256, V=192, seed=818, C=64, h0=True, dht=True, cu=[0, 70, 256, 400],
          gate_div=8.0),
+    # per-chunk dq / dk / dg with K <= 128 and V > 128 (128-wide key tiles): a partial last
+    # chunk, V = 136 (a partial last 64-column V tile), K = 96 (a partial key tile), varlen
+    dict(B=2, T=130, H=3, K=128, V=256, seed=831, C=64, h0=True, dht=True, gate_div=4.0),
+    dict(B=1, T=250, H=2, K=96, V=136, seed=832, C=64, dht=True, cu=[0, 40, 250],
+         gate_div=4.0),
     # varlen on the main shape (full-head kernels): unaligned sequences, one of a single token
     dict(B=1, T=700, H=2, K=128, V=128, seed=819, C=64, h0=True, dht=True,
          cu=[0, 130, 131, 500, 700], gate_div=8.0),
@@ -315,7 +320,7 @@ def test_fwd_subfunctions_compose():
     check("ht", to_np(ht), ht_ref, "f32")
     A = G.chunk_gla_fwd_intra_gk(d(q), d(k), gc, K ** -0.5, chunk_size=C)
     A_ref = orc.chunk_gla_fwd_intra_gk(q, k, gc_ref, K ** -0.5, C)
-    check("A", to_np(A), A_ref, "f32")
+    check("A", to_np(A), A_ref, "f32", rel_f32="unmasked intra matrix")
     o = G.chunk_gla_fwd_o_gk(d(q), d(v), gc, A, h, K ** -0.5, chunk_size=C)
     o_ref = orc.chunk_gla_fwd_o_gk(q, v, gc_ref, A_ref, h_ref, K ** -0.5, C)
     check("o", to_np(o), o_ref, "f32")
@@ -395,7 +400,8 @@ def test_chunk_gla_fwd_and_bwd_orchestrators_padded():
     ref = orc.chunk_gla_fwd(q, k, v, g, None, None, K ** -0.5, s0, True, cu_seqlens=cu,
                             chunk_size=C)
     for name, a, b in zip(["g_cumsum", "A", "h", "ht", "o"], out, ref):
-        check(name, to_np(a), b, "f32")
+        check(name, to_np(a), b, "f32",
+              rel_f32="unmasked intra matrix" if name == "A" else None)
     grads = G.chunk_gla_bwd(d(q), d(k), d(v), d(g), None, None, K ** -0.5, to_dev(s0, "state"),
                             out[2], None, d(do), to_dev(dht, "state"), cu_seqlens=cu,
                             chunk_size=C)
@@ -446,7 +452,8 @@ def test_g_gamma_gradient_reduced():
     check("o", to_np(o), o_ref, "f32")
     _, _, _, dg_ref, _ = orc.chunk_gla_bwd(q, k, v, None, gg, None, K ** -0.5, None, None, None,
                                            do, None, chunk_size=16)
-    check("dg_gamma", to_np(tgg.grad), dg_ref, "f32")
+    # the gradient of a per-head decay sums dg over every token and key column of the head
+    check("dg_gamma", to_np(tgg.grad), dg_ref, "f32", rel_f32="sum over a head's tokens")
 
 
 def test_deterministic():
