@@ -48,6 +48,14 @@ CASES = [
     dict(B=1, T=200, H=2, K=64, V=64, seed=141, gate_mul=5.0, h0=True),
     dict(B=1, T=100, H=2, K=32, V=64, seed=142, gate="gv", gate_mul=8.0, h0=True),
     dict(B=1, T=100, H=2, K=32, V=64, seed=143, gate_mul=8.0, h0=True, reverse=True),
+    # short scans (fixed length, T <= 64, K <= 128, 256+ blocks: the short-scan kernel): the
+    # decode shape B64 T1 H16 K=V=128; partial tiles (K = 96, V = 200, a partial 64-column
+    # tile), both gates; unaligned columns (V = 130), reverse, gv only; K = 20 (rows past K
+    # in the last row groups), no gate, custom scale
+    dict(B=64, T=1, H=16, K=128, V=128, seed=150, h0=True, gate_div=16.0),
+    dict(B=16, T=37, H=8, K=96, V=200, seed=151, h0=True, gate="gk+gv"),
+    dict(B=32, T=64, H=4, K=64, V=130, seed=152, reverse=True, gate="gv", h0=True),
+    dict(B=16, T=5, H=16, K=20, V=64, seed=153, gate="none", scale=0.3),
 ]
 
 
