@@ -171,6 +171,54 @@ __device__ __forceinline__ bool pair_flagged(const GateFlags& f, int seq, int hh
 // One unit L = (sequence, head) x NCT + column tile of a scan, run by the whole block. The
 // LDS arrays are function-scope statics: units that one block runs in turn share them, with
 // a barrier between.
+// Elements as stored, for loads whose conversion waits until the data is needed: ld_bits
+// one element (bf16 in the low half of the word), ld_raw N aligned elements in one load
+// (raw_words: bf16 two a word, element 2i in the low half of word i; N == 1: the low half),
+// and their fp32 values (bits_f32, cvt_raw).
+__device__ __forceinline__ uint32_t ld_bits(const float* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
+__device__ __forceinline__ uint32_t ld_bits(const bf16* p) {
+  return *reinterpret_cast<const uint16_t*>(p);
+}
+template <typename T>
+__device__ __forceinline__ float bits_f32(uint32_t x) {
+  return sizeof(T) == 4 ? __uint_as_float(x) : __uint_as_float(x << 16);
+}
+template <typename T, int N>
+constexpr int raw_words() { return sizeof(T) == 4 ? N : (N + 1) / 2; }
+template <typename T, int N>
+__device__ __forceinline__ void ld_raw(const T* p, uint32_t (&x)[raw_words<T, N>()]) {
+  constexpr int W = raw_words<T, N>();
+  if constexpr (sizeof(T) == 2 && N == 1) {
+    x[0] = *reinterpret_cast<const uint16_t*>(p);
+  } else if constexpr (W == 1) {
+    x[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else if constexpr (W == 2) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    x[0] = u.x; x[1] = u.y;
+  } else {
+    static_assert(W % 4 == 0, "words");
+#pragma unroll
+    for (int i = 0; i < W; i += 4) {
+      const uint4 u = reinterpret_cast<const uint4*>(p)[i / 4];
+      x[i] = u.x; x[i + 1] = u.y; x[i + 2] = u.z; x[i + 3] = u.w;
+    }
+  }
+}
+template <typename T, int N>
+__device__ __forceinline__ void cvt_raw(const uint32_t (&x)[raw_words<T, N>()], float (&y)[N]) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) y[i] = __uint_as_float(x[i]);
+  } else if constexpr (N == 1) {
+    y[0] = __uint_as_float(x[0] << 16);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) bf2(x[i], y[2 * i], y[2 * i + 1]);
+  }
+}
+
 template <typename T, typename TO, int NCG, int RPT>
 __device__ __forceinline__ void rec_scan_unit(const RecScanArgs& p, const int L) {
   using Cf = RecCfg<NCG, RPT>;
@@ -276,84 +324,93 @@ __device__ __forceinline__ void rec_scan_unit(const RecScanArgs& p, const int L)
 
   // Staging: wave w loads steps w and w + 8 of a stage, so each load has a wave-uniform
   // token; lane l loads rows l*RL .. l*RL+RL-1 (one vector load per array when the rows are
-  // whole and aligned) and column cbase + l of the column side.
+  // whole and aligned) and column cbase + l of the column side. issue() only issues the
+  // loads, into registers as stored; commit() converts, masks and stores them to LDS a stage
+  // later (converted or masked at issue, every stage would wait there for its own loads).
   constexpr int RL = RP / 64;     // rows per lane
   constexpr int SPW = TB / RNW;   // steps per wave per stage
   static_assert(RL * 64 == RP && SPW * RNW == TB, "staging map");
   const int row0 = lane * RL;
   const bool vrow = row0 + RL <= R && R % RL == 0 &&
                     (((uintptr_t)a | (uintptr_t)orow | (uintptr_t)ga) % (RL * sizeof(T))) == 0;
-  auto ld_rows = [&](const T* src, long off, float (&x)[RL]) {
+  // a row piece as stored (bf16 two a word): vrow, RL elements in one load; else element by
+  // element, rows clamped into the state (that path packs the halves, so it waits there)
+  constexpr int RW = sizeof(T) == 4 ? RL : (RL + 1) / 2;   // words of a row piece
+  auto ld_rows = [&](const T* src, long off, uint32_t (&x)[RW]) {
     if (vrow) {
-      ld_vec<T, RL>(src + off + row0, x);
+      ld_raw<T, RL>(src + off + row0, x);
+    } else if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int i = 0; i < RL; ++i) x[i] = ld_bits(src + off + min(row0 + i, R - 1));
     } else {
 #pragma unroll
-      for (int i = 0; i < RL; ++i) {
-        const float y = to_f32(src[off + min(row0 + i, R - 1)]);
-        x[i] = row0 + i < R ? y : 0.f;
+      for (int i = 0; i < RW; ++i) {
+        const uint32_t lo = ld_bits(src + off + min(row0 + 2 * i, R - 1));
+        const uint32_t hi = 2 * i + 1 < RL ? ld_bits(src + off + min(row0 + 2 * i + 1, R - 1)) : 0u;
+        x[i] = lo | (hi << 16);
       }
     }
   };
-  float pa[SPW][RL], po[SPW][RL], pg[SPW][RL], pb[SPW], pgc[SPW], pxd[SPW], py[SPW];
+  auto cvt_rows = [&](const uint32_t (&x)[RW], float (&y)[RL]) {
+    cvt_raw<T, RL>(x, y);
+    if (!vrow) {
+#pragma unroll
+      for (int i = 0; i < RL; ++i) y[i] = row0 + i < R ? y[i] : 0.f;
+    }
+  };
+  uint32_t ua[SPW][RW], uo[SPW][RW], ug[SPW][RW];   // row side, as stored
+  uint32_t ub[SPW], ugc[SPW];                      // column side, as stored
+  float pxd[SPW], py[SPW];   // gate-gradient inputs (backward scans): converted at issue
   auto issue = [&](int b0) {
-    const int nb = min(TB, n - b0);
 #pragma unroll
     for (int k = 0; k < SPW; ++k) {
       const int s = w + k * RNW;   // wave-uniform
-      const bool in = s < nb;
       const int gi = b0 + s - p.shift;
-      const bool gin = in && gi >= 0;
       const int t = tok(min(b0 + s, n - 1)), tg = tok(max(min(gi, n - 1), 0));
       const long ro = (long)t * rsR + (long)hh * R, rgo = (long)tg * rsR + (long)hh * R;
-      ld_rows(a, ro, pa[k]);
-      ld_rows(orow, ro, po[k]);
-      if (has_ga) ld_rows(ga, rgo, pg[k]);
-#pragma unroll
-      for (int i = 0; i < RL; ++i) {
-        pa[k][i] = in ? pa[k][i] : 0.f;
-        po[k][i] = in ? po[k][i] : 0.f;
-        pg[k][i] = (has_ga && gin) ? pg[k][i] : 0.f;   // log gate; 0 -> factor 1
-      }
+      ld_rows(a, ro, ua[k]);
+      ld_rows(orow, ro, uo[k]);
+      if (has_ga) ld_rows(ga, rgo, ug[k]);
       const int c = cbase + lane;
-      const bool cin = in && lane < CB && c < C;
       const long co = (long)t * rsC + (long)hh * C + min(c, C - 1);
-      const float xb = to_f32(b[co]);
-      pb[k] = cin ? xb : 0.f;
-      pgc[k] = 0.f;
-      if (has_gb) {
-        const float y = to_f32(gb[(long)tg * rsC + (long)hh * C + min(c, C - 1)]);
-        pgc[k] = (cin && gi >= 0) ? y : 0.f;
-      }
+      ub[k] = ld_bits(b + co);
+      if (has_gb) ugc[k] = ld_bits(gb + (long)tg * rsC + (long)hh * C + min(c, C - 1));
       if (grad) {
         float xf = p.gxf_f32 ? static_cast<const float*>(p.gxf)[co]
                              : to_f32(static_cast<const TO*>(p.gxf)[co]);
         if (p.gxf_lo) xf += to_f32(static_cast<const TO*>(p.gxf_lo)[co]);
-        const float xd = to_f32(gx[co]) * xf, xy = to_f32(gy[co]);
-        pxd[k] = cin ? xd : 0.f;
-        py[k] = cin ? xy : 0.f;
+        pxd[k] = to_f32(gx[co]) * xf;
+        py[k] = to_f32(gy[co]);
       }
     }
   };
-  auto commit = [&]() {
+  auto commit = [&](int b0) {
+    const int nb = min(TB, n - b0);
 #pragma unroll
     for (int k = 0; k < SPW; ++k) {
       const int s = w + k * RNW;
+      const bool in = s < nb;
+      const bool gin = in && b0 + s - p.shift >= 0;
       float xa[RL], xo[RL], xg[RL];
+      cvt_rows(ua[k], xa);
+      cvt_rows(uo[k], xo);
+      if (has_ga) cvt_rows(ug[k], xg);
 #pragma unroll
       for (int i = 0; i < RL; ++i) {
-        xa[i] = p.sa * pa[k][i];
-        xo[i] = p.so * po[k][i];
-        xg[i] = has_ga ? gexp<T>(pg[k][i]) : 1.f;
+        xa[i] = in ? p.sa * xa[i] : 0.f;
+        xo[i] = in ? p.so * xo[i] : 0.f;
+        xg[i] = (has_ga && gin) ? gexp<T>(xg[i]) : 1.f;   // absent gate: factor 1
       }
       st_vec<RL>(sA + s * RP + row0, xa);
       st_vec<RL>(sOR + s * RP + row0, xo);
       st_vec<RL>(sGR + s * RP + row0, xg);
       if (lane < CB) {
-        sB[s * CB + lane] = pb[k];
-        sGC[s * CB + lane] = has_gb ? gexp<T>(pgc[k]) : 1.f;
+        const bool cin = in && cbase + lane < C;
+        sB[s * CB + lane] = cin ? bits_f32<T>(ub[k]) : 0.f;
+        sGC[s * CB + lane] = (has_gb && cin && gin) ? gexp<T>(bits_f32<T>(ugc[k])) : 1.f;
         if (grad) {
-          sXD[s * CB + lane] = pxd[k];
-          sY[s * CB + lane] = py[k];
+          sXD[s * CB + lane] = cin ? pxd[k] : 0.f;
+          sY[s * CB + lane] = cin ? py[k] : 0.f;
         }
       }
     }
@@ -363,7 +420,7 @@ __device__ __forceinline__ void rec_scan_unit(const RecScanArgs& p, const int L)
   for (int b0 = 0; b0 < n; b0 += TB) {
     const int nb = min(TB, n - b0);
     __syncthreads();  // the previous stage's reads of the staged arrays and sO are done
-    commit();
+    commit(b0);
     __syncthreads();
     if (b0 + TB < n) issue(b0 + TB);
     // The column gate's presence is uniform: one copy of the step loop for each case.
@@ -421,13 +478,31 @@ __device__ __forceinline__ void rec_scan_unit(const RecScanArgs& p, const int L)
       const float cs = wave_colsum<NCG>(x);
       if (lane_writes<NCG>(lane)) sO[(w * TB + s) * CB + lane_col<NCG>(lane)] = cs;
     };
-    // Which gates exist is uniform: one copy of the step loop for each case.
+    // Which gates exist is uniform: one copy of the step loop for each case. With 8 state
+    // rows a thread (256 VGPRs), a step's LDS operands are read while the step before it
+    // computes (two register sets, two steps a trip; the read past the stage's last step is
+    // of a staged row that is not used); the 4-wave variants have no registers for that.
     auto steps = [&](auto gac, auto gbc) {
+      if constexpr (RPT < 8) {
 #pragma unroll 1
-      for (int s = 0; s < nb; ++s) {
-        StepIn in;
-        load_step(gac, gbc, s, in);
-        step(gac, gbc, s, in);
+        for (int s = 0; s < nb; ++s) {
+          StepIn in;
+          load_step(gac, gbc, s, in);
+          step(gac, gbc, s, in);
+        }
+        return;
+      }
+      StepIn x0, x1;
+      load_step(gac, gbc, 0, x0);
+#pragma unroll 1
+      for (int s = 0; s < nb; s += 2) {
+        load_step(gac, gbc, min(s + 1, TB - 1), x1);
+        __builtin_amdgcn_sched_barrier(0);   // the reads issue before the step's products
+        step(gac, gbc, s, x0);
+        if (s + 1 >= nb) break;
+        load_step(gac, gbc, min(s + 2, TB - 1), x0);
+        __builtin_amdgcn_sched_barrier(0);
+        step(gac, gbc, s + 1, x1);
       }
     };
     using yes = std::integral_constant<bool, true>;
