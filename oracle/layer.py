@@ -96,9 +96,11 @@ def recurrence(q, k, v, gk, scale, initial_state=None, cu_seqlens=None):
     return o, torch.stack(finals)
 
 
-def gla_layer(params, x, cfg, cu_seqlens=None, initial_state=None):
+def gla_layer(params, x, cfg, cu_seqlens=None, initial_state=None, recurrence_fn=None):
     """The layer's forward (``gla.py:224-345``) for config ``cfg`` (the constructor's keyword
-    arguments). Returns (o [B, T, hidden], final recurrent state)."""
+    arguments). Returns (o [B, T, hidden], final recurrent state). ``recurrence_fn`` (same
+    arguments and results as ``recurrence``) replaces the step recurrence, e.g. by a chunked
+    form for full-length sequences on the GPU."""
     hidden = cfg.get("hidden_size", 1024)
     H = cfg.get("num_heads", 4)
     Hkv = cfg.get("num_kv_heads") or H
@@ -128,7 +130,7 @@ def gla_layer(params, x, cfg, cu_seqlens=None, initial_state=None):
     fm = cfg.get("feature_map")
     if fm is not None:
         q, k = ACT[fm](q), ACT[fm](k)
-    o, ht = recurrence(q, k, v, gk, dk ** -0.5, initial_state, cu_seqlens)
+    o, ht = (recurrence_fn or recurrence)(q, k, v, gk, dk ** -0.5, initial_state, cu_seqlens)
     eps = cfg.get("norm_eps", 1e-5)
     affine = cfg.get("elementwise_affine", True)
     use_gate = cfg.get("use_output_gate", True)

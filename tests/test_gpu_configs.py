@@ -11,7 +11,10 @@ the reference-written layer fixtures on the HIP layer.
   the layer oracle on the same weights; the attention core's dq / dk / dv / dg on two (b, h)
   slices against the oracle's ``chunk_gla_bwd`` given the core's own inputs and upstream
   gradient (captured from the layer run), and the core's o, dq, dk, dv, dg on all 8 slices
-  against the float32 torch chunked GLA (``tests/torch_ref.py``) from the same inputs.
+  against the float32 torch chunked GLA (``tests/torch_ref.py``) from the same inputs; the
+  whole layer at full size (output, input gradient and every parameter gradient) against
+  a float32 reference on the GPU: the layer oracle's composition (``oracle/layer.py``) with
+  the chunked torch recurrence in place of its step loop, from the same bf16 weights.
 * Reference fixtures (``tests/golden/gla_layer.npz``, written by the reference's torch CPU
   layer): the float32 HIP layer's output and gradients.
 
@@ -168,6 +171,26 @@ def test_c5_layer_fwd_bwd_full_size():
         worst = float((err / scale.clamp_min(1e-30)).max())
         _say(f"  core {name}, all slices: worst error/max|ref| {worst:.3e}")
         assert worst <= BF16_RTOL_MAX, name
+    del refs, ro, pairs
+    # the whole layer at full size against a float32 reference on the GPU (the oracle's
+    # composition with the chunked torch recurrence, pinned by tests/test_torch_ref.py):
+    # output, input gradient and every parameter gradient, each at the bf16 bar
+    def chunk_recurrence(q, k, v, g, scale, initial_state=None, cu_seqlens=None):
+        assert cu_seqlens is None
+        return chunk_gla_torch(q, k, v, g, initial_state, scale=scale, chunk_size=64)
+
+    refp = {n: p.detach().float().requires_grad_() for n, p in m.named_parameters()}
+    xr = x.detach().float().requires_grad_()
+    oref_full, _ = L.gla_layer(refp, xr, cfg, recurrence_fn=chunk_recurrence)
+    (oref_full * probe).sum().backward()
+    torch.cuda.synchronize()
+    full = [("out", out, oref_full), ("d_x", xd.grad, xr.grad)] + [
+        (f"d_{n}", p.grad, refp[n].grad) for n, p in m.named_parameters()]
+    for name, got, r in full:
+        err = float((got.detach().float() - r.detach()).abs().max())
+        scale = float(r.detach().abs().max())
+        _say(f"  full layer {name}: error/max|ref| {err / max(scale, 1e-30):.3e}")
+        assert err <= BF16_RTOL_MAX * scale, name
 
 
 def _layer_cases():
