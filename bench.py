@@ -455,8 +455,10 @@ def _measured_traffic(kernel, op):
 
 def _measure(leg, steps, warmup, timing):
     """W untimed steps, then K steps timed with torch events on the launch stream (bracketed
-    by synchronizations); with ``timing`` the library's HIP events around every launch of the
-    leg's timed kernels during those K steps. Returns (ms per step, {kernel: ms})."""
+    by synchronizations); with ``timing`` another K steps follow with the library's HIP events
+    around every launch of the leg's timed kernels. Those events cost host time per launch
+    (measured: a short step such as the T = 1 decode, 27 -> 33 us), so they stay out of the
+    step's own timed region. Returns (ms per step, {kernel: ms})."""
     import torch
 
     from tops import _lib
@@ -468,8 +470,6 @@ def _measure(leg, steps, warmup, timing):
     torch.cuda.synchronize(dev)
     cur = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    if timing:   # HIP events around every timed-kernel launch of the timed steps
-        _lib.call("tops_gla_kernel_timing", 1)
     e0.record(cur)
     for _ in range(steps):
         step()
@@ -477,7 +477,11 @@ def _measure(leg, steps, warmup, timing):
     torch.cuda.synchronize(dev)
     ms = e0.elapsed_time(e1) / steps
     kms = {}
-    if timing:
+    if timing:   # HIP events around every timed-kernel launch of K more steps
+        _lib.call("tops_gla_kernel_timing", 1)
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize(dev)
         lib = _lib.load()
         for name, kd in leg["kernels"].items():
             x = float(lib.tops_gla_kernel_ms(kd["slot"]))

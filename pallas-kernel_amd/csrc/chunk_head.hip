@@ -1602,6 +1602,25 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     hload<VRPT>(R.v, v + (long)t0 * rsV + (long)hh * V + cv, (uint32_t)rsV, vrs * VRPT, len,
                 vg * 8, Vw);
   };
+  // PRE: the next chunk's gating-workspace loads in two parts (qg, A and the factors once
+  // this chunk's tiles are in LDS, kg and v after the barrier before the output products):
+  // all eleven at once queue behind each other and stall the issuing waves (the later four
+  // waves of a block ~2000 cycles each chunk)
+  auto pre_entry = [&](int step) {
+    const int st = min(step, nsteps - 1);
+    return (const bf16*)((const unsigned char*)p.gate_ws +
+                         ((long)(sg.c0 + sg.cb + st) * H + hh) * gate_ws_entry(K));
+  };
+  auto issue_pq = [&](int step, Regs& R) {
+    const bf16* gq = pre_entry(step);
+    hload<RPT>(R.q, gq, (uint32_t)K, rs * RPT, HC, cg * 8, K);
+    R.a = ld16(gq + 2 * HC * K, (uint32_t)tid * 16u);
+    R.f = ld16(gq + 2 * HC * K + HC * HC, (uint32_t)min(tid, 3 * K / 4 - 1) * 16u);
+  };
+  auto issue_pk = [&](int step, Regs& R) {
+    hload<RPT>(R.k, pre_entry(step) + HC * K, (uint32_t)K, rs * RPT, HC, cg * 8, K);
+    issue_v(step, R);
+  };
   // R: this chunk's registers; Rn: the next chunk's (SPLIT: its q, k and v issued here)
   auto body = [&](int step, Regs& R, Regs& Rn) {
     // lane taken through opaque() every chunk: the per-lane LDS offsets are recomputed in
@@ -1750,6 +1769,8 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     }
     if constexpr (SPLIT)
       issue_g(step + 2, R);
+    else if constexpr (PRE && PF == 1)
+      issue_pq(step + 1, R);
     else
       issue(step + PF, R);
     __syncthreads();
@@ -1783,6 +1804,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     }
     __syncthreads();
     if constexpr (SPLIT) issue_v(step + 1, Rn);
+    if constexpr (PRE && PF == 1) issue_pk(step + 1, R);
 
     // ---- (3) o^T = v^T A^T + h'^T qg^T (wave: v tiles of half w&1, row tile w>>1) ----
     {
