@@ -650,7 +650,8 @@ struct HSLayout {
   static constexpr int b = a + LT<KP>::bytes(CR);
   static constexpr int tot = b + LT<VP>::bytes(CR);
   static constexpr int gam = tot + (NT / 64) * KP * 4;
-  static constexpr int bytes = gam + KP * 4;
+  static constexpr int post = gam + KP * 4;   // PRE: the per-column factor after the update
+  static constexpr int bytes = post + KP * 4;
 };
 
 // CR = HC: one step per chunk (every pass). CR = 2 HC (pass 1 only, which needs the
@@ -658,8 +659,12 @@ struct HSLayout {
 // chunks, a 128-row tile with its own cumsum; the recurrence is the same row by row, so the
 // final state is unchanged, and every factor stays <= 1.
 // PRE (wide heads with the per-chunk gating workspace): the gated rows come from there --
-// qg (scale 2^r) for the reverse scan, kg (2^{gamma-r}) for the forward one -- with the
-// chunk decays, so a step has no cumsum and no per-element exp2.
+// qg for the reverse scan, kg for the forward one -- with their column factors, so a step
+// has no cumsum and no per-element exp2. The factor f (reverse: scale 2^r, forward:
+// 2^{gamma-r}) goes on the state instead of the rows: s <- f (.) (s 2^gamma / f + a^T b),
+// 2^gamma / f being the workspace's 2^{gamma-r} / scale (reverse) or 2^r (forward); one
+// thread per column group loads them (all 16 row groups loading the same 64 bytes doubled
+// the bytes a step moves through the CU's vector memory path).
 template <int KP, int VP, bool REV, int NT, bool SG, int CR = HC, bool PRE = false>
 __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   static_assert(!PRE || (!SG && CR == HC && HMap<KP, NT, CR>::RPT >= 4), "gated-tile scan");
@@ -675,6 +680,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   bf16* sB = reinterpret_cast<bf16*>(smem + Lay::b);
   float* sTot = reinterpret_cast<float*>(smem + Lay::tot);
   float* sGam = reinterpret_cast<float*>(smem + Lay::gam);
+  float* sPost = reinterpret_cast<float*>(smem + Lay::post);
 
   const bf16* __restrict__ a = (const bf16*)p.a;
   const bf16* __restrict__ b = (const bf16*)p.b;
@@ -720,6 +726,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   struct Regs {
     uint4 a[RPT], g[RPT], b[VRPT];
     float gs[RPT];
+    uint4 gx[2];   // PRE: the chunk gate sums gamma of the thread's 8 columns
   };
   // rows [t0, t0 + len) of step `step`; ci = its first chunk. Pairs of chunks (CR = 2 HC)
   // are taken in flow order, so an odd count leaves the segment's last chunk in flow order
@@ -742,18 +749,22 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     span(min(step, nsteps - 1), t0, len, ci);
     const long oa = (long)t0 * rsK + (long)hh * K;
     if constexpr (PRE) {
-      // gated rows (zeros past the chunk); g[0..1] = this thread's 8 column factors
-      // (reverse: scale 2^r, forward: 2^{gamma-r}), g[2..3] = their chunk gate sums gamma
+      // gated rows (zeros past the chunk); row group 0 only: g[0..1] = the 8 column
+      // factors f, g[2..3] = 2^gamma / f, gx = the chunk gate sums gamma
       const unsigned char* ent =
           (const unsigned char*)p.gate_ws + ((long)(sg.c0 + ci) * H + hh) * gate_ws_entry(K);
       hload<RPT>(R.a, (const bf16*)ent + (REV ? 0 : HC * K), (uint32_t)K, rs * RPT, HC, cg * 8,
                  K);
-      const float* fac = (const float*)(ent + 2L * HC * K * 2 + HC * HC * 2);
-      const uint32_t co = (uint32_t)min(cg * 8, K - 8) * 4u;
-      R.g[0] = ld16(fac + (REV ? 0 : 2 * K), co);
-      R.g[1] = ld16(fac + (REV ? 0 : 2 * K), co + 16u);
-      R.g[2] = ld16(fac + 3 * K, co);
-      R.g[3] = ld16(fac + 3 * K, co + 16u);
+      if (rs == 0) {
+        const float* fac = (const float*)(ent + 2L * HC * K * 2 + HC * HC * 2);
+        const uint32_t co = (uint32_t)min(cg * 8, K - 8) * 4u;
+        R.g[0] = ld16(fac + (REV ? 0 : 2 * K), co);
+        R.g[1] = ld16(fac + (REV ? 0 : 2 * K), co + 16u);
+        R.g[2] = ld16(fac + (REV ? 2 * K : K), co);
+        R.g[3] = ld16(fac + (REV ? 2 * K : K), co + 16u);
+        R.gx[0] = ld16(fac + 3 * K, co);
+        R.gx[1] = ld16(fac + 3 * K, co + 16u);
+      }
     } else {
       hload<RPT>(R.a, a + oa, (uint32_t)rsK, rs * RPT, len, cg * 8, K);
     }
@@ -793,6 +804,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
                 vg * 8, Vw);
   };
 
+  const float inv_scale = 1.f / p.scale;   // PRE reverse: 2^gamma / f = 2^{gamma-r} / scale
   float gsum[8];   // pass 1: total base-2 decay of the segment
 #pragma unroll
   for (int e = 0; e < 8; ++e) gsum[e] = 0.f;
@@ -813,22 +825,29 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     float gt[RPT][8], gam[8];
     if constexpr (PRE) {
       __syncthreads();   // the previous step's reads of the tiles are done
-      float fa[8], gs[8];
-      *reinterpret_cast<uint4*>(fa) = R.g[0];
-      *reinterpret_cast<uint4*>(fa + 4) = R.g[1];
-      *reinterpret_cast<uint4*>(gs) = R.g[2];
-      *reinterpret_cast<uint4*>(gs + 4) = R.g[3];
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
         const int row = rs * RPT + j;
-        float x[8];
-        unpack8(mask16(R.a[j], colA ? ~0u : 0u), x);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] *= fa[e];
-        *reinterpret_cast<uint4*>(sA + LT<KP>::off(row, cg * 8)) = pack8(x);
+        *reinterpret_cast<uint4*>(sA + LT<KP>::off(row, cg * 8)) =
+            mask16(R.a[j], colA ? ~0u : 0u);
       }
+      if (rs == 0) {
+        float f[8], d[8];
+        *reinterpret_cast<uint4*>(f) = R.g[0];
+        *reinterpret_cast<uint4*>(f + 4) = R.g[1];
+        *reinterpret_cast<uint4*>(d) = R.g[2];
+        *reinterpret_cast<uint4*>(d + 4) = R.g[3];
+        *reinterpret_cast<uint4*>(gam) = R.gx[0];
+        *reinterpret_cast<uint4*>(gam + 4) = R.gx[1];
+        if constexpr (REV) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) gam[e] = gs[e];
+          for (int e = 0; e < 8; ++e) d[e] *= inv_scale;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gsum[e] += gam[e];
+        st_f8(sPost + cg * 8, f);
+        st_f8(sGam + cg * 8, d);
+      }
     } else if constexpr (SG) {
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
@@ -860,7 +879,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
       const int row = vrs * VRPT + j;
       *reinterpret_cast<uint4*>(sB + LT<VP>::off(row, vg * 8)) = R.b[j];
     }
-    if (rs == TRS) {
+    if (!PRE && rs == TRS) {
       float eg[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -879,7 +898,8 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
         store_state_bf16<NTV, NTK>(acc, s_all + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K,
                                    Vw, vt0, kt0, lane, V);
     }
-    state_update<NTV, NTK, VP, KP, CR>(acc, sB, sA, sGam, vt0, kt0, lane);
+    state_update<NTV, NTK, VP, KP, CR>(acc, sB, sA, sGam, vt0, kt0, lane,
+                                       PRE ? sPost : nullptr);
     if constexpr (SPLIT) issue_b(step + 1, Rn);
   };
 
