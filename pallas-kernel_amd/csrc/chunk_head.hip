@@ -659,12 +659,11 @@ struct HSLayout {
 // chunks, a 128-row tile with its own cumsum; the recurrence is the same row by row, so the
 // final state is unchanged, and every factor stays <= 1.
 // PRE (wide heads with the per-chunk gating workspace): the gated rows come from there --
-// qg for the reverse scan, kg for the forward one -- with their column factors, so a step
-// has no cumsum and no per-element exp2. The factor f (reverse: scale 2^r, forward:
-// 2^{gamma-r}) goes on the state instead of the rows: s <- f (.) (s 2^gamma / f + a^T b),
-// 2^gamma / f being the workspace's 2^{gamma-r} / scale (reverse) or 2^r (forward); one
-// thread per column group loads them (all 16 row groups loading the same 64 bytes doubled
-// the bytes a step moves through the CU's vector memory path).
+// qs = scale q 2^{g~} for the reverse scan (s <- 2^gamma s + qs^T b), kg for the forward
+// one -- with the chunk decays, so a step has no cumsum and no per-element exp2. kg's column
+// factor f = 2^{gamma-r} goes on the state instead of the rows: s <- f (.) (s 2^r + kg^T b).
+// One thread per column group loads the factors (all 16 row groups loading the same 64
+// bytes doubled the bytes a step moves through the CU's vector memory path).
 template <int KP, int VP, bool REV, int NT, bool SG, int CR = HC, bool PRE = false>
 __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   static_assert(!PRE || (!SG && CR == HC && HMap<KP, NT, CR>::RPT >= 4), "gated-tile scan");
@@ -749,8 +748,8 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     span(min(step, nsteps - 1), t0, len, ci);
     const long oa = (long)t0 * rsK + (long)hh * K;
     if constexpr (PRE) {
-      // gated rows (zeros past the chunk); row group 0 only: g[0..1] = the 8 column
-      // factors f, g[2..3] = 2^gamma / f, gx = the chunk gate sums gamma
+      // gated rows (zeros past the chunk); row group 0 only: gx = the 8 columns' chunk gate
+      // sums gamma, forward also g[0..1] = their factors f = 2^{gamma-r}, g[2..3] = 2^r
       const unsigned char* ent =
           (const unsigned char*)p.gate_ws + ((long)(sg.c0 + ci) * H + hh) * gate_ws_entry(K);
       hload<RPT>(R.a, (const bf16*)ent + (REV ? 0 : HC * K), (uint32_t)K, rs * RPT, HC, cg * 8,
@@ -758,10 +757,12 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
       if (rs == 0) {
         const float* fac = (const float*)(ent + 2L * HC * K * 2 + HC * HC * 2);
         const uint32_t co = (uint32_t)min(cg * 8, K - 8) * 4u;
-        R.g[0] = ld16(fac + (REV ? 0 : 2 * K), co);
-        R.g[1] = ld16(fac + (REV ? 0 : 2 * K), co + 16u);
-        R.g[2] = ld16(fac + (REV ? 2 * K : K), co);
-        R.g[3] = ld16(fac + (REV ? 2 * K : K), co + 16u);
+        if constexpr (!REV) {
+          R.g[0] = ld16(fac + 2 * K, co);
+          R.g[1] = ld16(fac + 2 * K, co + 16u);
+          R.g[2] = ld16(fac + K, co);
+          R.g[3] = ld16(fac + K, co + 16u);
+        }
         R.gx[0] = ld16(fac + 3 * K, co);
         R.gx[1] = ld16(fac + 3 * K, co + 16u);
       }
@@ -804,7 +805,6 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
                 vg * 8, Vw);
   };
 
-  const float inv_scale = 1.f / p.scale;   // PRE reverse: 2^gamma / f = 2^{gamma-r} / scale
   float gsum[8];   // pass 1: total base-2 decay of the segment
 #pragma unroll
   for (int e = 0; e < 8; ++e) gsum[e] = 0.f;
@@ -832,20 +832,22 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
             mask16(R.a[j], colA ? ~0u : 0u);
       }
       if (rs == 0) {
-        float f[8], d[8];
-        *reinterpret_cast<uint4*>(f) = R.g[0];
-        *reinterpret_cast<uint4*>(f + 4) = R.g[1];
-        *reinterpret_cast<uint4*>(d) = R.g[2];
-        *reinterpret_cast<uint4*>(d + 4) = R.g[3];
+        float d[8];
         *reinterpret_cast<uint4*>(gam) = R.gx[0];
         *reinterpret_cast<uint4*>(gam + 4) = R.gx[1];
         if constexpr (REV) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) d[e] *= inv_scale;
+          for (int e = 0; e < 8; ++e) d[e] = exp2_hw(gam[e]);
+        } else {
+          float f[8];
+          *reinterpret_cast<uint4*>(f) = R.g[0];
+          *reinterpret_cast<uint4*>(f + 4) = R.g[1];
+          *reinterpret_cast<uint4*>(d) = R.g[2];
+          *reinterpret_cast<uint4*>(d + 4) = R.g[3];
+          st_f8(sPost + cg * 8, f);
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) gsum[e] += gam[e];
-        st_f8(sPost + cg * 8, f);
         st_f8(sGam + cg * 8, d);
       }
     } else if constexpr (SG) {
@@ -899,7 +901,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
                                    Vw, vt0, kt0, lane, V);
     }
     state_update<NTV, NTK, VP, KP, CR>(acc, sB, sA, sGam, vt0, kt0, lane,
-                                       PRE ? sPost : nullptr);
+                                       PRE && !REV ? sPost : nullptr);
     if constexpr (SPLIT) issue_b(step + 1, Rn);
   };
 
@@ -938,7 +940,8 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 // the fused forward needs the same gated tiles, intra matrix and column factors of a chunk;
 // this kernel makes them once per (chunk, head) into a caller workspace, and the forward's
 // PRE build reads them instead of gating for itself. Workspace entry of chunk c, head h at
-// (c * H + h) * GW bytes: qg bf16 [64][K], kg bf16 [64][K], A bf16 [64][64] (scaled, causal),
+// (c * H + h) * GW bytes: qs bf16 [64][K] (q scale 2^{g~}: the inter term's rows, i.e. qg
+// times its column factor scale 2^r), kg bf16 [64][K], A bf16 [64][64] (scaled, causal),
 // factors f32 [4][K]: scale 2^r, 2^r, 2^{gamma - r}, gamma (base 2).
 // ---------------------------------------------------------------------------
 
@@ -999,11 +1002,14 @@ __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
     const int bad = __syncthreads_or(dmax > kGateLimit2 ? 1 : 0);
     if (tid == 0) p.flags[(long)(c0 + ci) * H + hh] = bad ? 1 : 0;
   }
+  float fs[8];   // scale 2^r: qs = qg fs
+#pragma unroll
+  for (int e = 0; e < 8; ++e) fs[e] = p.scale * exp2_hw(r[e]);
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int row = rs * RPT + j;
     const uint32_t m = (colA && row < len) ? ~0u : 0u;
-    float xq[8], xk[8];
+    float xq[8], xk[8], xs[8];
     unpack8(mask16(Rq[j], m), xq);
     unpack8(mask16(Rk[j], m), xk);
 #pragma unroll
@@ -1011,12 +1017,13 @@ __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
       const float d = gt[j][e] - r[e];
       xq[e] *= exp2_hw(d);
       xk[e] *= exp2_hw(-d);
+      xs[e] = xq[e] * fs[e];
     }
     const uint4 pq = pack8(xq), pk = pack8(xk);
     *reinterpret_cast<uint4*>(sQg + LT<KP>::off(row, cg * 8)) = pq;
     *reinterpret_cast<uint4*>(sKg + LT<KP>::off(row, cg * 8)) = pk;
     if (colA) {
-      *reinterpret_cast<uint4*>(gq + row * K + cg * 8) = pq;
+      *reinterpret_cast<uint4*>(gq + row * K + cg * 8) = pack8(xs);
       *reinterpret_cast<uint4*>(gk + row * K + cg * 8) = pk;
     }
   }
@@ -1481,7 +1488,9 @@ struct HFLayout {
   static constexpr int bytes = grow + (SG ? HC * 4 : 0);
 };
 
-template <int KP, int VP, bool SG, bool PRE = false>
+// HO: p.h_out may be set (the PRE build is instantiated without the h residual's code for
+// inference calls, which store none).
+template <int KP, int VP, bool SG, bool PRE = false, bool HO = true>
 __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   using M = HMap<KP>;
   using MV = HMap<VP>;
@@ -1520,7 +1529,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   const bf16* __restrict__ v = (const bf16*)p.v;
   const bf16* __restrict__ g = (const bf16*)p.g;
   bf16* __restrict__ o = (bf16*)p.o;
-  bf16* __restrict__ hout = (bf16*)p.h_out;
+  bf16* __restrict__ hout = HO ? (bf16*)p.h_out : nullptr;
   const int H = p.H, K = p.K, V = p.V;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, scalar
@@ -1650,8 +1659,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     const int t0 = sg.bos + ci * HC;
     const int len = min(HC, sg.eos - t0);
     // h_n to HBM first: the vector memory path is idle here (the next chunk's loads are
-    // issued at the end of the gating, and stores queued behind them wait for them)
-    if (hout) {
+    // issued at the end of the gating, and stores queued behind them wait for them). PRE
+    // copies it from h' in LDS as whole rows instead, after the output products
+    if (hout && !PRE) {
       bf16* hb = hout + ((long)(sg.c0 + ci) * H + hh) * KV + cv;
       if constexpr (ROWS) {
 #pragma unroll
@@ -1810,11 +1820,12 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
         sA[LT<HC>::off(ii, jj)] = from_f32<bf16>(jj <= ii ? a : 0.f);
       }
     }
+    // (PRE: h' = h, the workspace's qs carrying the column factor scale 2^r)
     const int oacc = LT<VP>::acc_pos(ln);
 #pragma unroll
     for (int j = 0; j < NTK; ++j) {
       const int kk = (kt0 + j) * 16 + (lane & 15);
-      const float f = sRs[kk];
+      const float f = PRE ? 1.f : sRs[kk];
 #pragma unroll
       for (int i = 0; i < NTV; ++i) {
         *reinterpret_cast<uint2*>(sHk + LT<VP>::at((kt0 + j) * 16, (vt0 + i) * 16) + oacc) =
@@ -1824,7 +1835,12 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     }
     __syncthreads();
     if constexpr (SPLIT) issue_v(step + 1, Rn);
-    if constexpr (PRE && PF == 1) issue_pk(step + 1, R);
+    if constexpr (PRE && PF == 1) {
+      issue_pk(step + 1, R);
+      // kept ahead of the output products: scheduled among them, the loads stall the later
+      // waves' MFMA issue and arrive later
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
     // ---- (3) o^T = v^T A^T + h'^T qg^T (wave: v tiles of half w&1, row tile w>>1) ----
     {
@@ -1893,6 +1909,20 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       if constexpr (ROWS)
         rows_out(sStg, o + (long)(t0 + it * 16) * rsV + (long)hh * V + cv + vt0 * 16,
                  (uint32_t)rsV, len - it * 16, Vw - vt0 * 16, ntv, ln);
+    }
+    if constexpr (PRE) {
+      // the h residual (the state entering the chunk, bf16) as whole rows of h' in LDS: the
+      // accumulators' 8-byte pieces (32 bytes of a row a store) cost ~40 % of the chunk at C5
+      if (hout) {
+        bf16* hb = hout + ((long)(sg.c0 + ci) * H + hh) * KV + cv;
+        constexpr int PR = VP / 8;   // 16-byte pieces of a row
+#pragma unroll
+        for (int j = 0; j < KP * PR / HNT; ++j) {
+          const int pc = tid + HNT * j, r = pc / PR, c8 = (pc % PR) * 8;
+          const uint4 x = *reinterpret_cast<const uint4*>(sHk + LT<VP>::off(r, c8));
+          if (r < K && c8 < Vw) st16_sel(hb, ((uint32_t)r * (uint32_t)V + c8) * 2u, x, ntv);
+        }
+      }
     }
     if constexpr (SG)
       state_update<NTV, NTK, VP, KP>(acc, sV2, sKg, sGam, vt0, kt0, ln);
@@ -2797,15 +2827,20 @@ static hipError_t launch_head_fwd(const HeadFwdArgs& p, hipStream_t st) {
   if constexpr (KP == 256) {
     if (p.g && p.gate_ws) {   // the V tiles' blocks stream the per-chunk gating
       using Lay = HFLayout<KP, VP, false>;
-      hipError_t e;
-      e = hipFuncSetAttribute((const void*)head_fwd_kernel<KP, VP, false, true>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, Lay::bytes);
+      const void* fn = p.h_out ? (const void*)head_fwd_kernel<KP, VP, false, true, true>
+                               : (const void*)head_fwd_kernel<KP, VP, false, true, false>;
+      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         Lay::bytes);
       if (e != hipSuccess) return e;
       HeadFwdArgs q = p;
       q.flags = nullptr;   // the gating kernel wrote the per-chunk flags
       ktimer_mark(KT_HEAD_FWD, false, st);
-      hipLaunchKernelGGL((head_fwd_kernel<KP, VP, false, true>), dim3((unsigned)blocks),
-                         dim3(HNT), Lay::bytes, st, q);
+      if (p.h_out)
+        hipLaunchKernelGGL((head_fwd_kernel<KP, VP, false, true, true>), dim3((unsigned)blocks),
+                           dim3(HNT), Lay::bytes, st, q);
+      else
+        hipLaunchKernelGGL((head_fwd_kernel<KP, VP, false, true, false>),
+                           dim3((unsigned)blocks), dim3(HNT), Lay::bytes, st, q);
       ktimer_mark(KT_HEAD_FWD, true, st);
       return hipGetLastError();
     }
