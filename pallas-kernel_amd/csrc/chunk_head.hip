@@ -1147,7 +1147,7 @@ __device__ __forceinline__ void acc_cumsum(float (&x)[4][4], float (&R)[4], floa
 }
 
 template <int KB, int NW>
-__global__ __launch_bounds__(NW * 64) void head_dqkg_kernel(BwdArgs p) {
+__global__ __launch_bounds__(NW * 64, 2) void head_dqkg_kernel(BwdArgs p) {
   using Lay = HDLayout<KB>;
   constexpr int NT = NW * 64;
   constexpr int KTW = KB / 16 / NW;   // key tiles per wave
@@ -1195,8 +1195,7 @@ __global__ __launch_bounds__(NW * 64) void head_dqkg_kernel(BwdArgs p) {
   // ---- staging: whole 128-byte row pieces (8 lanes a row), rows / columns past the chunk
   // or the head as zeros ----
   // V tile vt of do, v (rows: chunk rows) and of h, dh (rows: the slice's key rows)
-  auto ld_v = [&](int vt, uint4 (&rd)[P64], uint4 (&rv)[P64], uint4 (&rh)[PH],
-                  uint4 (&rdh)[PH]) {
+  auto ld_dv = [&](int vt, uint4 (&rd)[P64], uint4 (&rv)[P64]) {
 #pragma unroll
     for (int e = 0; e < P64; ++e) {
       const int pc = tid + NT * e, row = pc >> 3, col = vt * 64 + 8 * (pc & 7);
@@ -1205,6 +1204,8 @@ __global__ __launch_bounds__(NW * 64) void head_dqkg_kernel(BwdArgs p) {
       rv[e] = ld16(v, off);
       if (row >= len || col >= V) rd[e] = rv[e] = make_uint4(0, 0, 0, 0);
     }
+  };
+  auto ld_h = [&](int vt, uint4 (&rh)[PH], uint4 (&rdh)[PH]) {
 #pragma unroll
     for (int e = 0; e < PH; ++e) {
       const int pc = tid + NT * e, row = kb + (pc >> 3), col = vt * 64 + 8 * (pc & 7);
@@ -1214,6 +1215,11 @@ __global__ __launch_bounds__(NW * 64) void head_dqkg_kernel(BwdArgs p) {
       rdh[e] = ld16(dhc, off);
       if (row >= K || col >= V) rh[e] = rdh[e] = make_uint4(0, 0, 0, 0);
     }
+  };
+  auto ld_v = [&](int vt, uint4 (&rd)[P64], uint4 (&rv)[P64], uint4 (&rh)[PH],
+                  uint4 (&rdh)[PH]) {
+    ld_dv(vt, rd, rv);
+    ld_h(vt, rh, rdh);
   };
   auto st_v = [&](const uint4 (&rd)[P64], const uint4 (&rv)[P64], const uint4 (&rh)[PH],
                   const uint4 (&rdh)[PH]) {
@@ -1292,9 +1298,16 @@ __global__ __launch_bounds__(NW * 64) void head_dqkg_kernel(BwdArgs p) {
   for (int vt = 0; vt < VT; ++vt) {
     st_v(rd, rv, rh, rdh);
     __syncthreads();   // this V tile in LDS
-    if (vt + 1 < VT) ld_v(vt + 1, rd, rv, rh, rdh);
+    // the next V tile's loads in two parts, h / dh here and do / v between the products:
+    // all twelve at once stall the issuing waves behind each other
+    if (vt + 1 < VT) ld_h(vt + 1, rh, rdh);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < KTW; ++t) {
+      if (t == KTW / 2) {
+        if (vt + 1 < VT) ld_dv(vt + 1, rd, rv);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       Frag<bf16> fh[2], fdh[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
