@@ -108,10 +108,116 @@ __global__ __launch_bounds__(NG_NT) void norm_gate_fwd_kernel(NormGateArgs p) {
   }
 }
 
+// Rows held in registers (D <= R x 512: one wave a row, lane l holding features 8 l + 512 j,
+// j < R), the next row's loads in flight; the lane's dw partials stay in registers and meet
+// in LDS once. R = 1 for rows of up to 512 features (half the registers of R = 2).
+template <typename T, int R>
+__device__ __forceinline__ void norm_gate_bwd_rows(const NormGateArgs& p, float (*sDw)[1024]) {
+  const T* __restrict__ x = (const T*)p.x;
+  const T* __restrict__ g = (const T*)p.g;
+  const T* __restrict__ dy = (const T*)p.dy;
+  T* __restrict__ dx = (T*)p.dx;
+  T* __restrict__ dg = (T*)p.dg;
+  const int D = p.D, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const bool want_dw = p.w && p.dw_part;
+  float wv[R][8], dwa[R][8];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int c = lane * 8 + 512 * j;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      wv[j][e] = 1.f;
+      dwa[j][e] = 0.f;
+    }
+    if (p.w && c < D) Vec8<float>::load(p.w + c, wv[j]);
+  }
+  const long stride = (long)gridDim.x * (NG_NT / 64);
+  float v[R][8], d[R][8], gv[R][8], rstd = 0.f;
+  auto load_row = [&](long row, float (&xa)[R][8], float (&da)[R][8], float (&ga)[R][8],
+                      float& rs) {
+    rs = p.rstd[row];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int c = lane * 8 + 512 * j;
+      if (c < D) {
+        Vec8<T>::load(x + row * D + c, xa[j]);
+        Vec8<T>::load(dy + row * D + c, da[j]);
+        if (g) Vec8<T>::load(g + row * D + c, ga[j]);
+      }
+    }
+  };
+  long row = (long)blockIdx.x * (NG_NT / 64) + w;
+  if (row < p.rows) load_row(row, v, d, gv, rstd);
+  for (; row < p.rows; row += stride) {
+    float nv[R][8], nd[R][8], ng[R][8], nrs = 0.f;
+    if (row + stride < p.rows) load_row(row + stride, nv, nd, ng, nrs);
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      if (lane * 8 + 512 * j < D) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float dn = d[j][e] * wv[j][e];
+          if (g) dn *= gv[j][e] * sigmoidf(gv[j][e]);
+          dot += dn * v[j][e] * rstd;
+        }
+      }
+    }
+    const float mdot = wave_sum(dot) / (float)D;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int c = lane * 8 + 512 * j;
+      if (c < D) {
+        float ox[8], og[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float n = v[j][e] * rstd;
+          float s = 1.f;
+          if (g) {
+            const float sg = sigmoidf(gv[j][e]);
+            s = gv[j][e] * sg;
+            og[e] = d[j][e] * n * wv[j][e] * sg * (1.f + gv[j][e] * (1.f - sg));
+          }
+          ox[e] = rstd * (d[j][e] * s * wv[j][e] - n * mdot);
+          dwa[j][e] += d[j][e] * s * n;
+        }
+        Vec8<T>::store(dx + row * D + c, ox);
+        if (g) Vec8<T>::store(dg + row * D + c, og);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[j][e] = nv[j][e];
+        d[j][e] = nd[j][e];
+        gv[j][e] = ng[j][e];
+      }
+    rstd = nrs;
+  }
+  if (want_dw) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int c = lane * 8 + 512 * j;
+      if (c < D)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sDw[w][c + e] = dwa[j][e];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < D; i += NG_NT) {
+      float t = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < NG_NT / 64; ++ww) t += sDw[ww][i];
+      p.dw_part[(long)blockIdx.x * D + i] = t;
+    }
+  }
+}
+
 // n = x rstd, a = n w, s = silu(g), y = a s:
 //   dg = dy a silu'(g), silu'(g) = sig(g) (1 + g (1 - sig(g)))
 //   dn = dy s w, dx = rstd (dn - n mean(dn n)), dw_part[block] = sum_rows dy s n
-template <typename T>
+// R > 0: rows of at most R x 512 features in registers; R = 0: 1024-feature slabs.
+template <typename T, int R>
 __global__ __launch_bounds__(NG_NT) void norm_gate_bwd_kernel(NormGateArgs p) {
   __shared__ float sDw[NG_NT / 64][1024];   // per-wave dw partials of a 1024-feature slab
   const T* __restrict__ x = (const T*)p.x;
@@ -121,93 +227,9 @@ __global__ __launch_bounds__(NG_NT) void norm_gate_bwd_kernel(NormGateArgs p) {
   T* __restrict__ dg = (T*)p.dg;
   const int D = p.D, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const bool want_dw = p.w && p.dw_part;
-  if (D <= NG_REG * 512) {   // rows in registers (one slab), the next row's loads in flight
-    static_assert(NG_REG * 512 <= 1024, "one dw slab");
-    if (want_dw) {
-      for (int i = threadIdx.x; i < (NG_NT / 64) * 1024; i += NG_NT) (&sDw[0][0])[i] = 0.f;
-      __syncthreads();
-    }
-    float wv[NG_REG][8];
-#pragma unroll
-    for (int j = 0; j < NG_REG; ++j) {
-      const int c = lane * 8 + 512 * j;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) wv[j][e] = 1.f;
-      if (p.w && c < D) Vec8<float>::load(p.w + c, wv[j]);
-    }
-    const long stride = (long)gridDim.x * (NG_NT / 64);
-    float v[NG_REG][8], d[NG_REG][8], gv[NG_REG][8], rstd = 0.f;
-    auto load_row = [&](long row, float (&xa)[NG_REG][8], float (&da)[NG_REG][8],
-                        float (&ga)[NG_REG][8], float& rs) {
-      rs = p.rstd[row];
-#pragma unroll
-      for (int j = 0; j < NG_REG; ++j) {
-        const int c = lane * 8 + 512 * j;
-        if (c < D) {
-          Vec8<T>::load(x + row * D + c, xa[j]);
-          Vec8<T>::load(dy + row * D + c, da[j]);
-          if (g) Vec8<T>::load(g + row * D + c, ga[j]);
-        }
-      }
-    };
-    long row = (long)blockIdx.x * (NG_NT / 64) + w;
-    if (row < p.rows) load_row(row, v, d, gv, rstd);
-    for (; row < p.rows; row += stride) {
-      float nv[NG_REG][8], nd[NG_REG][8], ng[NG_REG][8], nrs = 0.f;
-      if (row + stride < p.rows) load_row(row + stride, nv, nd, ng, nrs);
-      float dot = 0.f;
-#pragma unroll
-      for (int j = 0; j < NG_REG; ++j) {
-        if (lane * 8 + 512 * j < D) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            float dn = d[j][e] * wv[j][e];
-            if (g) dn *= gv[j][e] * sigmoidf(gv[j][e]);
-            dot += dn * v[j][e] * rstd;
-          }
-        }
-      }
-      const float mdot = wave_sum(dot) / (float)D;
-#pragma unroll
-      for (int j = 0; j < NG_REG; ++j) {
-        const int c = lane * 8 + 512 * j;
-        if (c < D) {
-          float ox[8], og[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float n = v[j][e] * rstd;
-            float s = 1.f;
-            if (g) {
-              const float sg = sigmoidf(gv[j][e]);
-              s = gv[j][e] * sg;
-              og[e] = d[j][e] * n * wv[j][e] * sg * (1.f + gv[j][e] * (1.f - sg));
-            }
-            ox[e] = rstd * (d[j][e] * s * wv[j][e] - n * mdot);
-            if (want_dw) sDw[w][c + e] += d[j][e] * s * n;
-          }
-          Vec8<T>::store(dx + row * D + c, ox);
-          if (g) Vec8<T>::store(dg + row * D + c, og);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < NG_REG; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          v[j][e] = nv[j][e];
-          d[j][e] = nd[j][e];
-          gv[j][e] = ng[j][e];
-        }
-      rstd = nrs;
-    }
-    if (want_dw) {
-      __syncthreads();
-      for (int i = threadIdx.x; i < D; i += NG_NT) {
-        float t = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < NG_NT / 64; ++ww) t += sDw[ww][i];
-        p.dw_part[(long)blockIdx.x * D + i] = t;
-      }
-    }
+  static_assert(NG_REG * 512 <= 1024 && R <= NG_REG, "one dw slab");
+  if constexpr (R > 0) {
+    norm_gate_bwd_rows<T, R>(p, sDw);
     return;
   }
   for (int c0 = 0; c0 < D; c0 += 1024) {   // dw slabs: the row loop runs once per slab
@@ -373,12 +395,16 @@ hipError_t run_norm_gate_fwd(const NormGateArgs& p, int dtype, hipStream_t st) {
 hipError_t run_norm_gate_bwd(const NormGateArgs& p, float* dw, int dtype, hipStream_t st) {
   const long blocks = norm_gate_bwd_blocks(p.rows);
   if (blocks == 0) return hipSuccess;
+  const int r = p.D <= 512 ? 1 : p.D <= NG_REG * 512 ? NG_REG : 0;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NG_NT), 0, st, p);
+  };
   if (dtype == DT_BF16)
-    hipLaunchKernelGGL((norm_gate_bwd_kernel<bf16>), dim3((unsigned)blocks), dim3(NG_NT), 0, st,
-                       p);
+    r == 1 ? go(norm_gate_bwd_kernel<bf16, 1>)
+           : r == NG_REG ? go(norm_gate_bwd_kernel<bf16, NG_REG>) : go(norm_gate_bwd_kernel<bf16, 0>);
   else
-    hipLaunchKernelGGL((norm_gate_bwd_kernel<float>), dim3((unsigned)blocks), dim3(NG_NT), 0,
-                       st, p);
+    r == 1 ? go(norm_gate_bwd_kernel<float, 1>)
+           : r == NG_REG ? go(norm_gate_bwd_kernel<float, NG_REG>) : go(norm_gate_bwd_kernel<float, 0>);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !dw || !p.w || !p.dw_part) return e;
   return run_rows_sum(p.dw_part, (int)blocks, p.D, dw, st);

@@ -29,14 +29,16 @@ def _close(name, got, ref, tol):
     check(name, got, ref, "f32", atol=tol * max(1.0, float(np.abs(ref).max())))
 
 
+# D: rows of one 512-feature piece in registers, of two, and in 1024-feature slabs (the
+# backward's three builds)
+@pytest.mark.parametrize("D", [64, 768, 1536])
 @pytest.mark.parametrize("affine", [True, False])
 @pytest.mark.parametrize("gated", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_rmsnorm_gated(affine, gated, dtype):
+def test_rmsnorm_gated(affine, gated, dtype, D):
     from oracle import layer as L
     from tops.modules import FusedRMSNormGated, RMSNorm
 
-    D = 64
     gen = torch.Generator().manual_seed(5)
     x = torch.randn(3, 37, D, generator=gen)
     g = torch.randn(3, 37, D, generator=gen)
