@@ -12,8 +12,8 @@ Other legs (``--op``; not the headline, same JSON fields):
                     H4 K256 V512 bf16, h0 fp32, o fp32 (the reference's convention);
   chunk_fwd_c3    : configs[2] "C3", chunk_gla forward, B8 T4096 H4 K256 V512 bf16, h0;
   layer_c5        : configs[4] "C5", GatedLinearAttention forward + backward, bf16, B2
-                    T16384 hidden 2048, 4 heads (K 256, V 512), weights ~ N(0, 0.02), loss =
-                    sum(out * probe) (flops / bytes: the GLA core's);
+                    T16384 hidden 2048, 4 heads (K 256, V 512), weights ~ N(0, 0.02), the
+                    output's gradient a fixed random probe (flops / bytes: the GLA core's);
   simple_gla      : the C4 shape with a per-head constant log-decay (chunk_gla(g_gamma=...));
   decode_t1 / _t64: fused_recurrent_gla forward at a decode shape, B64 H16 K=V=128, T = 1 / 64:
                     the recurrent kernel where HBM, not VALU, bounds it.
@@ -285,7 +285,9 @@ def leg_layer_c5(dev):
 
     def step():
         out, _, _ = m(x)
-        return torch.autograd.grad((out * probe).sum(), [x] + params)
+        # the output gradient handed to the backward (as the C4 leg does): the layer's forward
+        # and backward only, no loss reduction of the output
+        return torch.autograd.grad(out, [x] + params, probe)
 
     tok = B * T * H
     fwd_b = tok * (3 * K + 2 * V) * BF
