@@ -83,7 +83,12 @@ class _FanOutLinear(torch.autograd.Function):
             dy2 = dy.reshape(-1, dy.shape[-1])
             if ctx.needs_input_grad[0]:
                 dx2 = dy2 @ w if dx2 is None else dx2.addmm_(dy2, w)
-            dws.append(dy2.t() @ x2 if ctx.needs_input_grad[1 + len(dws)] else None)
+            if ctx.needs_input_grad[1 + len(dws)]:
+                # narrow outputs: x^T dy, transposed, runs on a faster GEMM build than
+                # dy^T x (hipBLASLt, [32768, 2048] x [32768, 1024]: 235 against 304 us)
+                dws.append((x2.t() @ dy2).t() if dy2.shape[1] < x2.shape[1] else dy2.t() @ x2)
+            else:
+                dws.append(None)
         dx = None
         if ctx.needs_input_grad[0]:
             dx = dx2.view(x.shape) if dx2 is not None else torch.zeros_like(x)
