@@ -1480,6 +1480,8 @@ __global__ __launch_bounds__(NW * 64, 2) void head_dqkg_kernel(BwdArgs p) {
 // KD: kd is staged in LDS (K <= 128). Wider heads (K = 256) do not have the room; their
 // update runs on kg with the column factors split around the product:
 // h <- 2^{gamma-r} (.) (2^r h + kg^T v)  (= 2^gamma h + kd^T v).
+// PRE (wide heads streaming the per-chunk gating workspace): the qg tile holds qs = qg
+// (scale 2^r), so h' = h and o = A v + qs h.
 // SG (scalar gates): v2 = v 2^{gamma - G_j} for the state update and G (one float per row).
 template <int KP, int VP, bool SG = false>
 struct HFLayout {

@@ -76,8 +76,9 @@ struct BwdArgs {
   int vec;              // every base pointer 16-byte aligned and K, V multiples of 16 bytes
   SeqInfo si;
 };
-// Bytes of one (chunk, head) entry of the per-chunk gating workspace (chunk 64): qg, kg
-// [64][K] bf16, A [64][64] bf16 (masked, scaled), the column factors scale 2^r, 2^r,
+// Bytes of one (chunk, head) entry of the per-chunk gating workspace (chunk 64): qs = scale
+// q 2^{g~} and kg = k 2^{r-g~}, [64][K] bf16 each, A [64][64] bf16 (masked, scaled), the
+// column factors scale 2^r, 2^r,
 // 2^{gamma-r} and the chunk's summed gates gamma (base 2) [4][K] f32.
 __host__ __device__ constexpr long gate_ws_entry(int K) {
   return 2L * 64 * K * 2 + 64L * 64 * 2 + 4L * K * 4;
@@ -255,7 +256,7 @@ struct HeadScanArgs {
   float* seg_gam;
   int NS, SL;
   int pass, s_begin, ns_launch;   // set by the launcher
-  // per-chunk gating workspace of wide heads (nullable): the scans then stream qg (reverse)
+  // per-chunk gating workspace of wide heads (nullable): the scans then stream qs (reverse)
   // or kg (forward) and the column factors instead of gating in every V tile's block
   const void* gate_ws;
   float scale;            // reverse only
