@@ -67,6 +67,7 @@ class _FanOutLinear(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, *weights):
+        ctx.set_materialize_grads(False)   # unused outputs: no gradient products
         ctx.save_for_backward(x, *weights)
         return tuple(F.linear(x, w) for w in weights)
 

@@ -1,0 +1,38 @@
+"""Host-side pieces of the GLA layer that need no GPU: the fan-out projection node against
+separate ``F.linear`` calls (forward values and every gradient, float64 on the CPU)."""
+
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(ROOT, "pallas-kernel_amd"))
+
+
+@pytest.mark.parametrize("unused", [None, 1])
+def test_fanout_linear_matches_separate_linears(unused):
+    import torch
+    import torch.nn.functional as F
+
+    from tops.layers.gla import _FanOutLinear
+
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 7, 32, generator=gen, dtype=torch.float64, requires_grad=True)
+    # output widths below, at and above the input's (the narrow ones take the transposed
+    # weight-gradient product)
+    ws = [torch.randn(o, 32, generator=gen, dtype=torch.float64, requires_grad=True)
+          for o in (16, 32, 40, 4)]
+    ys = _FanOutLinear.apply(x, *ws)
+    ref = [F.linear(x, w) for w in ws]
+    for y, r in zip(ys, ref):
+        assert torch.equal(y, r)
+    keep = [i for i in range(len(ws)) if i != unused]   # an output left out of the loss
+    dys = [torch.randn(ys[i].shape, generator=gen, dtype=torch.float64) for i in keep]
+    got = torch.autograd.grad([ys[i] for i in keep], [x] + ws, dys, allow_unused=True)
+    exp = torch.autograd.grad([ref[i] for i in keep], [x] + ws, dys, allow_unused=True)
+    for i, (g, e) in enumerate(zip(got, exp)):
+        if e is None:
+            assert g is None or not g.abs().max() > 0, i
+            continue
+        assert torch.allclose(g, e, rtol=1e-12, atol=1e-12), i
