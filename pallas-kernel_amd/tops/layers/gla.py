@@ -57,6 +57,58 @@ class Linear(torch.nn.Module):
         return F.linear(x.to(dt), self.weight.to(dt), b)
 
 
+def _skinny_at_b(a, b, ones=False):
+    """``a^T b`` for a tall ``a`` [N, r] with few columns and a tall ``b`` [N, c], in float32:
+    a split over the rows (``bmm`` of S row blocks, then the S partial products summed).
+    With ``ones`` a row of column sums of ``b`` is appended (the bias gradient of a layer
+    whose output gradient is ``b``). A single GEMM of this shape has no parallelism to spare
+    in its output (r x c) and walks the N rows in one pass: hipBLASLt took 104 us for
+    [32768, 1024]^T [32768, 16] and 71 us for [32768, 16]^T [32768, 2048], the split form
+    47 and 41 us. Summed in float32 (or the inputs' wider type). Returns None when N does
+    not split (the caller then uses a GEMM)."""
+    N = a.shape[0]
+    S = 32
+    if N % S != 0 or N < S * 512:
+        return None
+    if ones:
+        a = torch.cat([a, torch.ones(N, 1, dtype=a.dtype, device=a.device)], 1)
+    n = N // S
+    # both bmm operands row-major and contiguous (the left one is [S, r, n], a small copy)
+    lhs = a.reshape(S, n, a.shape[1]).transpose(1, 2).contiguous()
+    p = torch.bmm(lhs, b.reshape(S, n, b.shape[1]))
+    return p.to(torch.promote_types(p.dtype, torch.float32)).sum(0)
+
+
+class _NarrowLinear(torch.autograd.Function):
+    """``x W^T + bias`` for an input with few features (the low-rank gate's second matrix:
+    16 -> key dim). The weight and bias gradients come from one split product over the rows
+    (``_skinny_at_b`` with the column sums appended) instead of a GEMM over all rows plus a
+    separate reduction for the bias."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        ctx.save_for_backward(x, weight)
+        ctx.has_bias = bias is not None
+        return F.linear(x, weight, bias)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight = ctx.saved_tensors
+        x2 = x.reshape(-1, x.shape[-1])
+        dy2 = dy.reshape(-1, dy.shape[-1])
+        dx = (dy2 @ weight).view(x.shape) if ctx.needs_input_grad[0] else None
+        dw = db = None
+        if ctx.needs_input_grad[1] or (ctx.has_bias and ctx.needs_input_grad[2]):
+            p = _skinny_at_b(x2, dy2, ones=ctx.has_bias)   # [r (+1), out]
+            if p is None:
+                dw = dy2.t() @ x2
+                db = dy2.sum(0) if ctx.has_bias else None
+            else:
+                dw = p[:x2.shape[1]].t().to(weight.dtype)
+                db = p[x2.shape[1]].to(weight.dtype) if ctx.has_bias else None
+        return dx, dw, db
+
+
 class _FanOutLinear(torch.autograd.Function):
     """``[x W_i^T for W_i in weights]``: bias-free projections of one input, forward as
     separate GEMMs, backward with the input gradient accumulated inside the GEMMs
@@ -85,9 +137,16 @@ class _FanOutLinear(torch.autograd.Function):
             if ctx.needs_input_grad[0]:
                 dx2 = dy2 @ w if dx2 is None else dx2.addmm_(dy2, w)
             if ctx.needs_input_grad[1 + len(dws)]:
-                # narrow outputs: x^T dy, transposed, runs on a faster GEMM build than
-                # dy^T x (hipBLASLt, [32768, 2048] x [32768, 1024]: 235 against 304 us)
-                dws.append((x2.t() @ dy2).t() if dy2.shape[1] < x2.shape[1] else dy2.t() @ x2)
+                # very narrow outputs (the low-rank gate): the split product over the rows;
+                # narrow ones: x^T dy, transposed, a faster GEMM build than dy^T x (hipBLASLt,
+                # [32768, 2048] x [32768, 1024]: 235 against 304 us)
+                p = _skinny_at_b(dy2, x2) if dy2.shape[1] <= 64 else None
+                if p is not None:
+                    dws.append(p.to(w.dtype))
+                elif dy2.shape[1] < x2.shape[1]:
+                    dws.append((x2.t() @ dy2).t())
+                else:
+                    dws.append(dy2.t() @ x2)
             else:
                 dws.append(None)
         dx = None
@@ -231,7 +290,12 @@ class GatedLinearAttention(torch.nn.Module):
         if (torch.is_grad_enabled()
                 and all(m.bias is None and m.weight.dtype == hidden_states.dtype for m in lins)):
             ys = _FanOutLinear.apply(hidden_states, *[m.weight for m in lins])
-            q, k, v, gk = ys[0], ys[1], ys[2], self.gk_proj[1](ys[3])
+            up = self.gk_proj[1]
+            q, k, v = ys[0], ys[1], ys[2]
+            gk = (_NarrowLinear.apply(ys[3], up.weight, up.bias)
+                  if up.weight.dtype == hidden_states.dtype and (
+                      up.bias is None or up.bias.dtype == up.weight.dtype)
+                  else up(ys[3]))
             if self.use_output_gate:
                 g = ys[4]
         else:
