@@ -10,8 +10,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, os.path.join(ROOT, "pallas-kernel_amd"))
 
 
+@pytest.mark.parametrize("widths", [(16, 32, 40, 4), (96, 16, 80, 128)])
 @pytest.mark.parametrize("unused", [None, 1])
-def test_fanout_linear_matches_separate_linears(unused):
+def test_fanout_linear_matches_separate_linears(unused, widths):
     import torch
     import torch.nn.functional as F
 
@@ -20,9 +21,9 @@ def test_fanout_linear_matches_separate_linears(unused):
     gen = torch.Generator().manual_seed(0)
     x = torch.randn(3, 7, 32, generator=gen, dtype=torch.float64, requires_grad=True)
     # output widths below, at and above the input's (the narrow ones take the transposed
-    # weight-gradient product)
+    # weight-gradient product; widths above 64 form the concatenated group)
     ws = [torch.randn(o, 32, generator=gen, dtype=torch.float64, requires_grad=True)
-          for o in (16, 32, 40, 4)]
+          for o in widths]
     ys = _FanOutLinear.apply(x, *ws)
     ref = [F.linear(x, w) for w in ws]
     for y, r in zip(ys, ref):
