@@ -353,6 +353,17 @@ int tops_gla_gate_logsigmoid_bwd(const void* x, const void* dy, void* dx, int64_
                                  void* stream);
 
 /*
+ * Row-wise concatenation: dst [rows, sum w_j] = [src_0 | ... | src_{nsrc-1}], each source
+ * [rows, w_j] row-major (1 <= nsrc <= 8; every w_j a positive multiple of 16 bytes; 16-byte
+ * aligned buffers).
+ * No counterpart in the reference: the layer's backward joins the output gradients of its
+ * wide projections so that one GEMM pair forms their input and weight gradients
+ * (tops/layers/gla.py:259-262, 333: separate dense layers there).
+ */
+int tops_gla_concat_cols(const void* const* srcs, const int64_t* widths, int nsrc,
+                         int64_t rows, void* dst, int dtype, void* stream);
+
+/*
  * Causal depthwise convolution of a [B, T, D] sequence (varlen: B = 1 and cu_seqlens [N+1];
  * max_len = the longest sequence), kernel width W <= 8, weight w [D][W] float32, optional
  * bias [D] float32, optional SiLU; rows before a sequence's first token read as zero.

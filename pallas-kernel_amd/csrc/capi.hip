@@ -1437,6 +1437,27 @@ int tops_gla_gate_logsigmoid_fwd(const void* x, void* y, int64_t count, float no
                     "gate_logsigmoid_fwd");
 }
 
+int tops_gla_concat_cols(const void* const* srcs, const int64_t* widths, int nsrc,
+                         int64_t rows, void* dst, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(TOPS_GLA_EINVAL, "bad dtype");
+  if (nsrc < 1 || nsrc > tops::kConcatMax || rows < 0 || srcs == nullptr || widths == nullptr)
+    return fail(TOPS_GLA_EINVAL, "nsrc must be in [1, 8], rows >= 0, srcs and widths set");
+  const int es = dtype == TOPS_GLA_BF16 ? 2 : 4;
+  long w[tops::kConcatMax];
+  for (int j = 0; j < nsrc; ++j) {
+    if (widths[j] <= 0 || (widths[j] * es) % 16 != 0)
+      return fail(TOPS_GLA_EUNSUPPORTED, "every width must be a positive multiple of 16 bytes");
+    if (rows > 0 && (srcs[j] == nullptr || !aligned16(srcs[j])))
+      return fail(TOPS_GLA_EINVAL, "sources must be non-NULL and 16-byte aligned");
+    w[j] = (long)widths[j];
+  }
+  if (rows > 0 && (dst == nullptr || !aligned16(dst)))
+    return fail(TOPS_GLA_EINVAL, "dst must be non-NULL and 16-byte aligned");
+  return hip_status(tops::run_concat_cols(srcs, w, nsrc, (long)rows, dst, es,
+                                          (hipStream_t)stream),
+                    "concat_cols");
+}
+
 int tops_gla_gate_logsigmoid_bwd(const void* x, const void* dy, void* dx, int64_t count,
                                  float normalizer, int has_clamp, float clamp_min, int dtype,
                                  void* stream) {

@@ -212,6 +212,11 @@ hipError_t run_gate(const void* x, const void* dy, void* out, long count, float 
 
 // out[c] = sum_b part[b][c] for c < M (deterministic column sums of per-block partials).
 hipError_t run_rows_sum(const float* part, int nblk, int M, float* out, hipStream_t st);
+// dst [rows, sum w_i] = [src_0 | src_1 | ...] row by row (norm_gate.hip); widths in elements
+// of esize bytes, each a multiple of 16 bytes, at most kConcatMax sources.
+constexpr int kConcatMax = 8;
+hipError_t run_concat_cols(const void* const* src, const long* widths, int nsrc, long rows,
+                           void* dst, int esize, hipStream_t st);
 
 // Causal depthwise convolution with optional bias and SiLU (short_conv.hip).
 struct ShortConvArgs {

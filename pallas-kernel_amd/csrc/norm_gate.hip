@@ -445,6 +445,47 @@ hipError_t run_rows_sum(const float* part, int nblk, int M, float* out, hipStrea
   return hipGetLastError();
 }
 
+// Row-wise concatenation of up to kConcatMax [rows, w_i] sources into dst [rows, sum w_i]
+// (widths multiples of 8 elements, 16-byte aligned buffers): one 16-byte piece a thread, the
+// pieces of a destination row in order, so both the source reads and the destination writes
+// are contiguous runs (torch.cat into a row slice of a wider tensor ran at ~2.8 TB/s here).
+struct ConcatArgs {
+  const void* src[kConcatMax];
+  long w8[kConcatMax + 1];   // prefix sums of the widths in 16-byte pieces
+  int nsrc;
+  long rows;
+};
+__global__ __launch_bounds__(256) void concat_cols_kernel(ConcatArgs a, uint4* __restrict__ dst) {
+  const long pw = a.w8[a.nsrc];   // pieces of a destination row
+  const long total = a.rows * pw;
+  for (long p = (long)blockIdx.x * 256 + threadIdx.x; p < total; p += (long)gridDim.x * 256) {
+    const long row = p / pw, c = p - row * pw;
+    int j = 0;
+#pragma unroll
+    for (int t = 1; t < kConcatMax; ++t) j += (t < a.nsrc && c >= a.w8[t]) ? 1 : 0;
+    const long w = a.w8[j + 1] - a.w8[j];
+    dst[p] = reinterpret_cast<const uint4*>(a.src[j])[row * w + (c - a.w8[j])];
+  }
+}
+
+hipError_t run_concat_cols(const void* const* src, const long* widths, int nsrc, long rows,
+                           void* dst, int esize, hipStream_t st) {
+  ConcatArgs a = {};
+  a.nsrc = nsrc;
+  a.rows = rows;
+  a.w8[0] = 0;
+  for (int j = 0; j < nsrc; ++j) {
+    a.src[j] = src[j];
+    a.w8[j + 1] = a.w8[j] + widths[j] * esize / 16;
+  }
+  const long total = rows * a.w8[nsrc];
+  if (total == 0) return hipSuccess;
+  const long blocks = std::min<long>((total + 255) / 256, 256L * 32);
+  hipLaunchKernelGGL(concat_cols_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a,
+                     (uint4*)dst);
+  return hipGetLastError();
+}
+
 hipError_t run_gate(const void* x, const void* dy, void* out, long count, float inv_n,
                     int has_clamp, float clamp, int dtype, hipStream_t st) {
   const long blocks = (count + 2047) / 2048;

@@ -61,6 +61,7 @@ _SIGS = {
     "tops_gla_rmsnorm_ws_bytes": [_I64, _I64],
     "tops_gla_gate_logsigmoid_fwd": [_P, _P, _I64, _F, _I, _F, _I, _P],
     "tops_gla_gate_logsigmoid_bwd": [_P, _P, _P, _I64, _F, _I, _F, _I, _P],
+    "tops_gla_concat_cols": [_P, _P, _I, _I64, _P, _I, _P],
     "tops_gla_short_conv_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _I64, _I64, _I,
                                 _P],
     "tops_gla_short_conv_bwd": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P,

@@ -32,7 +32,7 @@ def _declared():
 
 def test_header_lists_entry_points():
     decl = _declared()
-    assert len(decl) == 31, decl
+    assert len(decl) == 32, decl
     assert set(decl) == set(_lib.EXPORTED)
 
 
@@ -302,3 +302,20 @@ def test_noalloc_forward_validates_on_the_host():
     rc, msg = _rc("tops_gla_chunk_fwd_noalloc", NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL,
                   1.0, 1, 64, 1, 64, 64, 64, NULL, NULL, 1, 1, 1, NULL)
     assert rc == 1 and "NULL" in msg
+
+
+def test_concat_cols_rejects_bad_arguments():
+    srcs = (ctypes.c_void_p * 2)(16, 32)
+    rc, msg = _rc("tops_gla_concat_cols", srcs, (ctypes.c_int64 * 2)(1024, 3), 2, 0,
+                  ctypes.c_void_p(64), 1, NULL)
+    assert rc == 2 and "multiple of 16 bytes" in msg
+    rc, msg = _rc("tops_gla_concat_cols", srcs, (ctypes.c_int64 * 2)(1024, 8), 9, 0,
+                  ctypes.c_void_p(64), 1, NULL)
+    assert rc == 1 and "nsrc" in msg
+    rc, msg = _rc("tops_gla_concat_cols", srcs, (ctypes.c_int64 * 2)(1024, 8), 2, 0,
+                  ctypes.c_void_p(64), 7, NULL)
+    assert rc == 1 and "dtype" in msg
+    # nothing to copy: accepted without a launch
+    rc, _ = _rc("tops_gla_concat_cols", srcs, (ctypes.c_int64 * 2)(1024, 8), 2, 0,
+                ctypes.c_void_p(64), 1, NULL)
+    assert rc == 0

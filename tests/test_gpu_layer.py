@@ -226,3 +226,21 @@ def test_gla_layer_cache_decode():
             y, _, cache = m(x[:, t:t + 1], past_key_values=cache, use_cache=True)
             steps.append(y)
     _close("o", torch.cat(steps, 1), full, 1e-4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_concat_cols_matches_torch_cat(dtype):
+    """The library's row-wise concatenation (the layer's grouped projection backward) against
+    torch.cat: widths of 8 / 16-byte multiples, one to eight sources, a partial last block."""
+    from tops.layers.gla import _concat_cols
+
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    w8 = 8 if dtype == torch.bfloat16 else 4    # 16 bytes
+    for widths in ([1024, 1024, 2048, 2048], [w8], [w8 * k for k in range(1, 9)]):
+        ts = [torch.randn(1237, w, generator=gen, device="cuda").to(dtype) for w in widths]
+        got = _concat_cols(ts)
+        assert torch.equal(got, torch.cat(ts, 1))
+    # a width that is no 16-byte multiple takes torch.cat
+    ts = [torch.randn(5, 3, device="cuda").to(dtype), torch.randn(5, w8, device="cuda").to(dtype)]
+    assert torch.equal(_concat_cols(ts), torch.cat(ts, 1))
