@@ -644,14 +644,15 @@ __host__ __device__ constexpr int head_vp(int KP, int V) {
 // ---------------------------------------------------------------------------
 // LDS of head_scan_kernel: the gated a tile and the b tile of CR rows, the wave totals of
 // the cumsum, the step's decays.
-template <int KP, int VP, int NT, int CR>
+template <int KP, int VP, int NT, int CR, bool STG = false>
 struct HSLayout {
   static constexpr int a = 0;
   static constexpr int b = a + LT<KP>::bytes(CR);
   static constexpr int tot = b + LT<VP>::bytes(CR);
   static constexpr int gam = tot + (NT / 64) * KP * 4;
   static constexpr int post = gam + KP * 4;   // PRE: the per-column factor after the update
-  static constexpr int bytes = post + KP * 4;
+  static constexpr int stg = post + KP * 4;   // STG: the step's state, bf16 [k][v]
+  static constexpr int bytes = stg + (STG ? LT<VP>::bytes(KP) : 0);
 };
 
 // CR = HC: one step per chunk (every pass). CR = 2 HC (pass 1 only, which needs the
@@ -670,7 +671,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   using MA = HMap<KP, NT, CR>;
   using MB = HMap<VP, NT, CR>;
   using TL = HTilesN<KP, VP, NT / 64>;
-  using Lay = HSLayout<KP, VP, NT, CR>;
+  using Lay = HSLayout<KP, VP, NT, CR, PRE>;
   static_assert(CR == HC || CR == 2 * HC, "chunk rows");
   constexpr int RPT = MA::RPT, VRPT = MB::RPT;
   constexpr int NTV = TL::NTV, NTK = TL::NTK;
@@ -680,6 +681,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
   float* sTot = reinterpret_cast<float*>(smem + Lay::tot);
   float* sGam = reinterpret_cast<float*>(smem + Lay::gam);
   float* sPost = reinterpret_cast<float*>(smem + Lay::post);
+  bf16* sStg = reinterpret_cast<bf16*>(smem + Lay::stg);   // PRE
 
   const bf16* __restrict__ a = (const bf16*)p.a;
   const bf16* __restrict__ b = (const bf16*)p.b;
@@ -809,6 +811,20 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) gsum[e] = 0.f;
 
+  // PRE with per-chunk states: the staged state of chunk stg_ci (sStg) to s_all as whole
+  // 128-byte rows, 16 bytes a thread (nontemporal when the rows are whole lines)
+  int stg_ci = -1;
+  auto copy_staged = [&](int c) {
+    bf16* dst = s_all + ((long)(sg.c0 + c) * H + hh) * KV + cv;
+    constexpr int PR = VP / 8;
+#pragma unroll
+    for (int j = 0; j < KP * PR / NT; ++j) {
+      const int pc = tid + NT * j, r = pc / PR, c8 = (pc % PR) * 8;
+      const uint4 x = *reinterpret_cast<const uint4*>(sStg + LT<VP>::off(r, c8));
+      if (r < K && c8 < Vw) st16_sel(dst, ((uint32_t)r * (uint32_t)V + c8) * 2u, x, V % 64 == 0);
+    }
+  };
+
   // R: this step's registers; Rn: the next step's (SPLIT: its a and b rows issued here)
   auto body = [&](int step, Regs& R, Regs& Rn) {
     int t0, len, ci;
@@ -825,6 +841,7 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
     float gt[RPT][8], gam[8];
     if constexpr (PRE) {
       __syncthreads();   // the previous step's reads of the tiles are done
+      if (s_all && stg_ci >= 0) copy_staged(stg_ci);
 #pragma unroll
       for (int j = 0; j < RPT; ++j) {
         const int row = rs * RPT + j;
@@ -896,9 +913,26 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
       issue(step + 2, R);
     __syncthreads();
     if constexpr (CR == HC) {
-      if (s_all)   // state entering the chunk (forward) / leaving it (reverse)
+      // state entering the chunk (forward) / leaving it (reverse). PRE: staged in LDS and
+      // stored as whole rows after the next step's first barrier (the accumulators' 8-byte
+      // pieces, 32 bytes of a 128-byte row per store, took the dh pass at C5 70 -> 235 us)
+      if constexpr (PRE) {
+        if (s_all) {
+          const int oa = LT<VP>::acc_pos(lane);
+#pragma unroll
+          for (int j = 0; j < NTK; ++j)
+#pragma unroll
+            for (int i = 0; i < NTV; ++i)
+              *reinterpret_cast<uint2*>(sStg + LT<VP>::at((kt0 + j) * 16, (vt0 + i) * 16) +
+                                        oa) =
+                  make_uint2(pack2_bf16(acc[i][j][0], acc[i][j][1]),
+                             pack2_bf16(acc[i][j][2], acc[i][j][3]));
+          stg_ci = ci;
+        }
+      } else if (s_all) {
         store_state_bf16<NTV, NTK>(acc, s_all + ((long)(sg.c0 + ci) * H + hh) * KV + cv, K,
                                    Vw, vt0, kt0, lane, V);
+      }
     }
     state_update<NTV, NTK, VP, KP, CR>(acc, sB, sA, sGam, vt0, kt0, lane,
                                        PRE && !REV ? sPost : nullptr);
@@ -922,6 +956,12 @@ __global__ __launch_bounds__(NT) void head_scan_kernel(HeadScanArgs p) {
       body(step + 1, R1, R0);
     }
     if (step < nsteps) body(step, R0, R1);
+    if constexpr (PRE) {
+      if (s_all && stg_ci >= 0) {
+        __syncthreads();
+        copy_staged(stg_ci);
+      }
+    }
   }
 
   if (p.pass == 1) {
@@ -2718,7 +2758,7 @@ long head_seg_ws_bytes(int N, int NS, int H, int K, int V) {
 template <int KP, int VP, bool REV, bool SG, int CR, bool PRE = false>
 static hipError_t launch_head_scan_cr(const HeadScanArgs& p, hipStream_t st, long blocks) {
   constexpr int NT = HNT;
-  using Lay = HSLayout<KP, VP, NT, CR>;
+  using Lay = HSLayout<KP, VP, NT, CR, PRE>;
   static_assert(Lay::bytes <= 163840, "LDS budget exceeded");
   const void* fn = (const void*)head_scan_kernel<KP, VP, REV, NT, SG, CR, PRE>;
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
