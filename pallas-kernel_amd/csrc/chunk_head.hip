@@ -1464,11 +1464,8 @@ __global__ __launch_bounds__(NW * 64, 2) void head_dqkg_kernel(BwdArgs p) {
       fe[r] = exp2_hw(Gm[t][r] - R[t][r]);
       dkc[r] = 0.f;
     }
-    const int k4 = kb + kc + 4 * (lane >> 4);
-    const bool kin = k4 < K;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-      const int i = 16 * mi + ri;
       float qv[4], kv[4], vq[4], vk[4];
       piece(sQg, mi, kc, qv);
       piece(sKg, mi, kc, kv);
@@ -1483,11 +1480,10 @@ __global__ __launch_bounds__(NW * 64, 2) void head_dqkg_kernel(BwdArgs p) {
         y[mi][r] = qv[r] * xq - kv[r] * xk;
         dkc[r] += kv[r] * xm;
       }
-      if (i < len && kin) {
-        const uint32_t off = ((uint32_t)i * rsK + (uint32_t)k4) * 2u;
-        st8(dq, off, pack4(vq));
-        st8(dk, off, pack4(vk));
-      }
+      // dq, dk over the tile's qg, kg pieces (this lane's own, read above)
+      const int o = LT<KB>::at(16 * mi, kc) + LT<KB>::acc_pos(lane);
+      *reinterpret_cast<uint2*>(sQg + o) = pack4(vq);
+      *reinterpret_cast<uint2*>(sKg + o) = pack4(vk);
     }
     // dg = suffix over the rows of y + 2^Gamma sum_v h dh + sum_rows kg Xm
     float add[4];
@@ -1499,7 +1495,6 @@ __global__ __launch_bounds__(NW * 64, 2) void head_dqkg_kernel(BwdArgs p) {
     float run[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mi = 3; mi >= 0; --mi) {
-      const int i = 16 * mi + ri;
       float x[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -1507,7 +1502,23 @@ __global__ __launch_bounds__(NW * 64, 2) void head_dqkg_kernel(BwdArgs p) {
         x[r] = suf + run[r] + add[r];
         run[r] += __shfl(suf, lane & 0x30);   // the row group's total (its row 0)
       }
-      if (i < len && kin) st8(dg, ((uint32_t)i * rsK + (uint32_t)k4) * 2u, pack4(x));
+      // dg over the tile's g pieces (read into G before the tiles)
+      *reinterpret_cast<uint2*>(sG + LT<KB>::at(16 * mi, kc) + LT<KB>::acc_pos(lane)) =
+          pack4(x);
+    }
+  }
+  __syncthreads();   // dq, dk, dg of every key tile in LDS
+  // whole row pieces of the slice (partial-line stores of the pieces above are slow)
+  const bool ntk = K % 64 == 0;
+#pragma unroll
+  for (int e = 0; e < PK; ++e) {
+    const int pc = tid + NT * e, row = pc / (KB / 8), c8 = 8 * (pc % (KB / 8));
+    const int o = LT<KB>::off(row, c8);
+    if (row < len && kb + c8 < K) {
+      const uint32_t off = ((uint32_t)row * rsK + (uint32_t)(kb + c8)) * 2u;
+      st16_sel(dq, off, *reinterpret_cast<const uint4*>(sQg + o), ntk);
+      st16_sel(dk, off, *reinterpret_cast<const uint4*>(sKg + o), ntk);
+      st16_sel(dg, off, *reinterpret_cast<const uint4*>(sG + o), ntk);
     }
   }
 }
