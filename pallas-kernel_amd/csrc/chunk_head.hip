@@ -1544,6 +1544,8 @@ struct HFLayout {
   static constexpr int hk = v + LT<VP>::bytes(HC);      // h' [k][v]
   static constexpr int a = hk + LT<VP>::bytes(KP);      // A  [i][j]
   static constexpr int tot = a + LT<HC>::bytes(HC);   // cumsum wave totals (!SG)
+  // PRE (no cumsum): the chunk's output tile staged over the totals and the first rows
+  static constexpr int ost = tot;
   static constexpr int first = tot + (SG ? 0 : HNW * KP * 4);
   static constexpr int gam = first + KP * 4;
   static constexpr int rsc = gam + KP * 4;
@@ -1574,6 +1576,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   // next chunk's gating, which comes after the cumsum's barrier. Scalar gates stage in the kd
   // tile, which they do not use.
   constexpr bool ROWS = !PRE && Lay::KD && NTV == 4 && HNW * kStgBytes <= LT<KP>::bytes(HC);
+  // PRE: o staged in LDS (64 rows, pitch kStgPitch) and stored as whole rows after the next
+  // chunk's first barrier; the wave pairs of a row tile each hold half its row
+  static_assert(!PRE || HC * kStgPitch * 2 <= Lay::gam - Lay::ost, "PRE output staging");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   bf16* sQg = reinterpret_cast<bf16*>(smem + Lay::qg);
   bf16* sKg = reinterpret_cast<bf16*>(smem + Lay::kg);
@@ -1589,6 +1594,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   float* sPost = reinterpret_cast<float*>(smem + Lay::post);
   bf16* sV2 = reinterpret_cast<bf16*>(smem + Lay::v2);
   float* sG = reinterpret_cast<float*>(smem + Lay::grow);
+  bf16* sOst = reinterpret_cast<bf16*>(smem + Lay::ost);
 
   const bf16* __restrict__ q = (const bf16*)p.q;
   const bf16* __restrict__ k = (const bf16*)p.k;
@@ -1716,6 +1722,16 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     hload<RPT>(R.k, pre_entry(step) + HC * K, (uint32_t)K, rs * RPT, HC, cg * 8, K);
     issue_v(step, R);
   };
+  // PRE: the staged output tile of chunk `step` to HBM, one 16-byte row piece a thread
+  auto o_out = [&](int step) {
+    static_assert(!PRE || HC * VP / 8 == HNT, "one piece a thread");
+    const int t0s = sg.bos + (sg.cb + step) * HC, lens = min(HC, sg.eos - t0s);
+    const int r = tid / (VP / 8), c8 = 8 * (tid % (VP / 8));
+    const uint4 x = *reinterpret_cast<const uint4*>(sOst + r * kStgPitch + c8);
+    if (r < lens && c8 < Vw)
+      st16_sel(o + (long)t0s * rsV + (long)hh * V + cv, ((uint32_t)r * (uint32_t)rsV + c8) * 2u,
+               x, ntv);
+  };
   // R: this chunk's registers; Rn: the next chunk's (SPLIT: its q, k and v issued here)
   auto body = [&](int step, Regs& R, Regs& Rn) {
     // lane taken through opaque() every chunk: the per-lane LDS offsets are recomputed in
@@ -1767,6 +1783,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
         const int off = which == 0 ? Lay::rsc : which == 1 ? Lay::pre : Lay::post;
         *reinterpret_cast<uint4*>(smem + off + col * 4) = R.f;
       }
+      // the previous chunk's output (after this chunk's tile stores: their wait for the
+      // loads would otherwise also wait for these stores)
+      if (step > 0) o_out(step - 1);
     } else if constexpr (SG) {
       // scalar gates: A's decay 2^{G_i - G_j} is applied after q k^T, the inter term's 2^{G_i}
       // after q h', and the update runs on v 2^{gamma - G_j}; every factor is <= 1 for
@@ -1964,6 +1983,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
             make_uint2(pack2_bf16(ot[i][0], ot[i][1]), pack2_bf16(ot[i][2], ot[i][3]));
         if constexpr (ROWS) {
           stage_tile(sStg, i, ox, ln);
+        } else if constexpr (PRE) {
+          *reinterpret_cast<uint2*>(sOst + (it * 16 + (lane & 15)) * kStgPitch + vt * 16 +
+                                    4 * (lane >> 4)) = ox;
         } else {
           const int row = it * 16 + (lane & 15);
           const int vv = vt * 16 + 4 * (lane >> 4);
@@ -2018,6 +2040,10 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     Regs R0;
     issue(0, R0);
     for (int step = 0; step < nsteps; ++step) body(step, R0, R0);
+    if constexpr (PRE) {
+      __syncthreads();   // the last chunk's output tile in LDS
+      o_out(nsteps - 1);
+    }
   }
 
   if (s == p.NS - 1 && p.ht)
