@@ -421,8 +421,26 @@ struct DvLayout {
   static constexpr int R = PRE ? 0 : (3 * TILE > AT + TILE) ? 3 * TILE : AT + TILE;
   static constexpr int qg = R, kg = PRE ? 0 : R + TILE, dh = PRE ? TILE : R + 2 * TILE;
   static constexpr int loop_end = dh + SQ, after_end = do_ + TILE;
-  static constexpr int bytes = loop_end > after_end ? loop_end : after_end;
+  static constexpr int base = loop_end > after_end ? loop_end : after_end;
+  // bf16 64-row chunks: dv staged as rows (pitch P64) for whole-line stores
+  static constexpr bool STG = ES == 2 && C == 64;
+  static constexpr int stg = base;
+  static constexpr int bytes = base + (STG ? SQ : 0);
 };
+
+// 16 bytes to global memory, nontemporal when `nt` (whole 128-byte lines only: partial lines
+// written this way are slow). The empty asm statements keep the two stores apart.
+typedef uint32_t dv_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void row_st16(void* dst, const uint4& x, bool nt) {
+  if (nt) {
+    const dv_u32x4 v = {x.x, x.y, x.z, x.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<dv_u32x4*>(dst));
+  } else {
+    asm volatile("");
+    *reinterpret_cast<uint4*>(dst) = x;
+    asm volatile("");
+  }
+}
 
 template <typename T, int C, bool VEC, bool PRE = false>
 __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
@@ -444,6 +462,9 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
   T* sQg = reinterpret_cast<T*>(dyn + Lay::qg);
   T* sKg = reinterpret_cast<T*>(dyn + Lay::kg);
   T* sDh = reinterpret_cast<T*>(dyn + Lay::dh);
+  // dv rows staged for whole-line stores (bf16, 64-row chunks, 16-byte aligned rows)
+  constexpr bool STG = Lay::STG && VEC;
+  T* sStg = reinterpret_cast<T*>(dyn + Lay::stg);
 
   const T* __restrict__ q = (const T*)p.q;
   const T* __restrict__ k = (const T*)p.k;
@@ -600,7 +621,10 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
     mma_tile2<T, true, true>(Dacc[j], sDo + mv * 16, P64, sA + nj * 16, PCP, CP, lane);
     const int jj = nj * 16 + (lane & 15);
     const int vv = vb + mv * 16 + 4 * (lane >> 4);
-    if (jj < len) {
+    if constexpr (STG) {
+      *reinterpret_cast<uint2*>(sStg + jj * P64 + mv * 16 + 4 * (lane >> 4)) =
+          make_uint2(pack2_bf16(Dacc[j][0], Dacc[j][1]), pack2_bf16(Dacc[j][2], Dacc[j][3]));
+    } else if (jj < len) {
       T* dst = dv + baseV + (long)jj * rsV + vv;
       if (VEC && vv + 3 < V) {
         if constexpr (sizeof(T) == 2) {
@@ -615,6 +639,17 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
         for (int rr = 0; rr < 4; ++rr)
           if (vv + rr < V) dst[rr] = from_f32<T>(Dacc[j][rr]);
       }
+    }
+  }
+  if constexpr (STG) {
+    __syncthreads();   // the tile's rows in LDS
+    const bool nt = V % 64 == 0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int pc = tid + 256 * e, r = pc >> 3, c8 = 8 * (pc & 7);
+      if (r < len && vb + c8 < V)
+        row_st16(dv + baseV + (long)r * rsV + vb + c8,
+                 *reinterpret_cast<const uint4*>(sStg + r * P64 + c8), nt);
     }
   }
 }
