@@ -1110,12 +1110,14 @@ __global__ __launch_bounds__(HNT) void head_gate_kernel(HeadFwdArgs p) {
 // Wave w owns key tiles KTW w .. KTW w + KTW - 1 of the slice over all 64 rows, so the chunk
 // cumsum of the gates and dg's reverse cumsum over the rows run inside the wave (DPP row
 // shifts over the 16 lanes of a row group, a running total over the four row tiles): no
-// block-wide exchange. do and v tiles are staged in LDS; h and dh fragments are read straight
-// from HBM (16 bytes a lane), each by the one wave that uses it, one V tile ahead; dA is formed
-// once per slice. Two blocks share a CU (61.5 KB of LDS, two waves per SIMD), so one block's
-// gating and epilogue run under the other's V loop; the two slices of a K = 256 head are
-// adjacent blocks (one XCD), whose do / v reads meet in its L2. Replaces a grid of (chunk,
-// head, 64-column key tile) blocks, each of which read all of do and v and formed dA again.
+// block-wide exchange. do, v, h and dh tiles are staged in LDS with whole-line loads, one V
+// tile ahead; dA is formed once per slice; dq, dk and dg are written over the wave's own q, k
+// and g pieces in LDS and stored as whole row pieces of the slice (8-byte pieces straight to
+// HBM are partial-line stores). Two blocks share a CU (61.5 KB of LDS, two waves per SIMD),
+// so one block's gating and epilogue run under the other's V loop; the two slices of a
+// K = 256 head are adjacent blocks (one XCD), whose do / v reads meet in its L2. Replaces a
+// grid of (chunk, head, 64-column key tile) blocks, each of which read all of do and v and
+// formed dA again.
 // ---------------------------------------------------------------------------
 constexpr int DKB = 128;   // key columns per block
 constexpr int DNW = 4;     // waves per block
