@@ -428,20 +428,6 @@ struct DvLayout {
   static constexpr int bytes = base + (STG ? SQ : 0);
 };
 
-// 16 bytes to global memory, nontemporal when `nt` (whole 128-byte lines only: partial lines
-// written this way are slow). The empty asm statements keep the two stores apart.
-typedef uint32_t dv_u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void row_st16(void* dst, const uint4& x, bool nt) {
-  if (nt) {
-    const dv_u32x4 v = {x.x, x.y, x.z, x.w};
-    __builtin_nontemporal_store(v, reinterpret_cast<dv_u32x4*>(dst));
-  } else {
-    asm volatile("");
-    *reinterpret_cast<uint4*>(dst) = x;
-    asm volatile("");
-  }
-}
-
 template <typename T, int C, bool VEC, bool PRE = false>
 __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
   static_assert(!PRE || C == 64, "the gating workspace holds chunks of 64");
@@ -648,7 +634,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
     for (int e = 0; e < 2; ++e) {
       const int pc = tid + 256 * e, r = pc >> 3, c8 = 8 * (pc & 7);
       if (r < len && vb + c8 < V)
-        row_st16(dv + baseV + (long)r * rsV + vb + c8,
+        st16_sel(dv + baseV, ((uint32_t)r * (uint32_t)rsV + (uint32_t)(vb + c8)) * 2u,
                  *reinterpret_cast<const uint4*>(sStg + r * P64 + c8), nt);
     }
   }

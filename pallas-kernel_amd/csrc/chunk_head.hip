@@ -211,40 +211,6 @@ __device__ __forceinline__ void ld_f8(const float* p, float (&x)[8]) {
   x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
 
-// Global accesses are a uniform base pointer (scalar registers) plus a 32-bit per-lane
-// byte offset, which the compiler emits as the scalar-base form of the global loads and
-// stores: one VGPR per address instead of a 64-bit pair.
-__device__ __forceinline__ uint4 ld16(const void* base, uint32_t off) {
-  return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + off);
-}
-__device__ __forceinline__ void st16(void* base, uint32_t off, const uint4& x) {
-  *reinterpret_cast<uint4*>(reinterpret_cast<char*>(base) + off) = x;
-}
-__device__ __forceinline__ void st8(void* base, uint32_t off, const uint2& x) {
-  *reinterpret_cast<uint2*>(reinterpret_cast<char*>(base) + off) = x;
-}
-
-// 16 bytes, nontemporal. The kernels' outputs are written once and not read again in the
-// launch: streamed past the L2 they leave no dirty lines for the writeback at the end of
-// the launch, which otherwise holds up the next launch (on MI355X 15-20 us after the fused
-// kernels). Only for whole 128-byte row pieces: partial lines written this way are slow.
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void st16_nt(void* base, uint32_t off, const uint4& x) {
-  const u32x4_t v = {x.x, x.y, x.z, x.w};
-  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(base) + off));
-}
-// st16_nt when `nt`, else st16. The empty asm statements keep the two stores from being
-// merged into one (which would drop the nontemporal hint).
-__device__ __forceinline__ void st16_sel(void* base, uint32_t off, const uint4& x, bool nt) {
-  if (nt) {
-    st16_nt(base, off, x);
-  } else {
-    asm volatile("");
-    st16(base, off, x);
-    asm volatile("");
-  }
-}
-
 // A wave's 16 x 64 bf16 block written to HBM as whole rows: staged tile by tile
 // (stage_tile: a 16 x 16 tile whose lane holds 4 consecutive columns, 4 (lane >> 4) + 0..3,
 // of row lane & 15) in the wave's own 16 x 72 LDS area `stg` (no other wave touches it; a
@@ -2137,7 +2103,6 @@ __global__ __launch_bounds__(NT) void head_bwd_kernel(HeadBwdArgs p) {
   using MV = HMap<VP, NT>;
   using Lay = HBLayout<KP, VP, NW, SG>;
   constexpr int RPT = M::RPT, VRPT = MV::RPT;
-  constexpr int PX = Lay::PX;
   constexpr int NKT = KP / 16, NVT = VP / 16;
   // dh tiles per wave: v by halves (w & 1), k split over the NW / 2 wave pairs
   constexpr int NTV = VP / 32, NTK = NKT / (NW / 2);

@@ -41,6 +41,40 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float f) {
   return r;
 }
 
+// Global accesses are a uniform base pointer (scalar registers) plus a 32-bit per-lane
+// byte offset, which the compiler emits as the scalar-base form of the global loads and
+// stores: one VGPR per address instead of a 64-bit pair.
+__device__ __forceinline__ uint4 ld16(const void* base, uint32_t off) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + off);
+}
+__device__ __forceinline__ void st16(void* base, uint32_t off, const uint4& x) {
+  *reinterpret_cast<uint4*>(reinterpret_cast<char*>(base) + off) = x;
+}
+__device__ __forceinline__ void st8(void* base, uint32_t off, const uint2& x) {
+  *reinterpret_cast<uint2*>(reinterpret_cast<char*>(base) + off) = x;
+}
+
+// 16 bytes, nontemporal. The kernels' outputs are written once and not read again in the
+// launch: streamed past the L2 they leave no dirty lines for the writeback at the end of
+// the launch, which otherwise holds up the next launch (on MI355X 15-20 us after the fused
+// kernels). Only for whole 128-byte row pieces: partial lines written this way are slow.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st16_nt(void* base, uint32_t off, const uint4& x) {
+  const u32x4_t v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(base) + off));
+}
+// st16_nt when `nt`, else st16. The empty asm statements keep the two stores from being
+// merged into one (which would drop the nontemporal hint).
+__device__ __forceinline__ void st16_sel(void* base, uint32_t off, const uint4& x, bool nt) {
+  if (nt) {
+    st16_nt(base, off, x);
+  } else {
+    asm volatile("");
+    st16(base, off, x);
+    asm volatile("");
+  }
+}
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // Two floats -> two bf16 in one 32-bit word (element a in the low half), one instruction.
