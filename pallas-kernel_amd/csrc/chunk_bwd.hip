@@ -14,9 +14,11 @@
 //   above except dv is local to a K tile (its contractions run over V and over the chunk).
 // chunk_bwd_dv_kernel:   one block per (chunk, head, 64-wide V tile), accumulating the
 //   K contractions of A and of k_d.dh over K tiles; it produces dv^T tiles so that each lane
-//   stores four consecutive values of a row. With the per-chunk gating workspace (PRE: wide
-//   bf16 heads, chunk 64) it reads kg, e^{gamma-r} and A from there instead: the gating and
-//   A would otherwise be recomputed by every V tile's block of a (chunk, head).
+//   holds four consecutive values of a row (bf16 with 64-row chunks: staged in LDS and
+//   stored as whole 16-byte row pieces; otherwise stored directly). With the per-chunk
+//   gating workspace (PRE: wide bf16 heads, chunk 64) it reads kg, e^{gamma-r} and A from
+//   there instead: the gating and A would otherwise be recomputed by every V tile's block of
+//   a (chunk, head).
 // Tiles are staged in LDS row-major exactly as loaded (16-byte global loads); operands that
 // are needed transposed (kg^T, qg^T, dA^T, dh^T, do^T, A^T) are read with transposed MFMA
 // fragments. Element-wise work maps a thread to two adjacent columns x C/8 rows.
