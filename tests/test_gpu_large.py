@@ -105,3 +105,38 @@ def test_past_2_31_elements(c):
         xs, ys = pick(x), first(y)
         assert torch.isfinite(xs.float()).all(), name
         assert torch.equal(xs, ys), (name, (xs.float() - ys.float()).abs().max().item())
+
+
+def test_past_2_31_elements_fixed_length():
+    """The fixed-length call (segmented: every (sequence, head) cut into segments whose entry
+    states come from a segment pass) on one sequence of 2^21 + 300 tokens, H 8, K = V = 128
+    (q, k, v, g of 2^31 + 307200 elements each), against the same sequence as a varlen call
+    (one segment, walked in order): the segments' entry states are summed in another order,
+    so the two agree to the bf16 bar (max-abs error / max |ref| <= 2e-2) and, for the float32
+    final state and dh0, to 1e-4 relative."""
+    H, K, V = 8, 128, 128
+    free, _ = torch.cuda.mem_get_info(0)
+    if free < 96 * 2**30:
+        pytest.skip(f"needs 96 GiB of free device memory, {free / 2**30:.0f} free")
+    T = 2**31 // (H * K) + 300
+    gen = torch.Generator(device="cuda:0").manual_seed(2025)
+    q, k, v, g, h0, do, dht = _inputs(T, H, K, V, 1, gen, torch.bfloat16)
+    import tops.ops.gla as G
+
+    def run(cu):
+        xs = [t.detach().requires_grad_(True) for t in (q, k, v, g, h0)]
+        o, ht = G.chunk_gla(*xs[:4], initial_state=xs[4], output_final_state=True,
+                            cu_seqlens=None if cu is None else torch.tensor(cu), chunk_size=64)
+        grads = torch.autograd.grad((o, ht), xs, (do, dht))
+        torch.cuda.synchronize()
+        return [o.detach(), ht.detach()] + list(grads)
+
+    fixed = run(None)
+    ref = run([0, T])
+    names = ["o", "ht", "dq", "dk", "dv", "dg", "dh0"]
+    for name, x, y in zip(names, fixed, ref):
+        assert torch.isfinite(x.float()).all(), name
+        err = (x.float() - y.float()).abs().max().item() / y.float().abs().max().item()
+        bar = 1e-4 if x.dtype == torch.float32 else 2e-2
+        print(f"{name}: error / max |ref| {err:.2e} (bar {bar})", flush=True)
+        assert err <= bar, (name, err)
