@@ -22,6 +22,8 @@
  *    For fixed-length calls NC must equal B * ceil(T / chunk_size).
  *  - Per-chunk state buffers ([NC, H, K, V], element type `dtype`) are caller-provided
  *    workspaces; the library allocates nothing.
+ *  - Sizes: B * T and NC * H below 2^31; a tensor may hold more than 2^31 elements (the
+ *    kernels form global offsets from 64-bit bases).
  *  - Work is enqueued on `stream` (a hipStream_t); nothing synchronizes the device.
  *  - Return value: TOPS_GLA_OK, or an error code with a message from
  *    tops_gla_last_error() (thread-local). Invalid arguments never launch a kernel.
