@@ -61,7 +61,12 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
+// 1 / (1 + e^{-x}) with the hardware reciprocal (v_rcp_f32, 1 ulp): an IEEE division is a
+// ten-instruction scale / fix-up sequence, a large share of these VALU-bound kernels' work.
+// Saturates to 0 / 1 (e^{-x} overflowing to inf gives rcp(inf) = 0).
+__device__ __forceinline__ float sigmoidf(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __expf(-x));
+}
 
 }  // namespace
 
@@ -151,14 +156,15 @@ __device__ __forceinline__ void norm_gate_bwd_rows(const NormGateArgs& p, float 
   for (; row < p.rows; row += stride) {
     float nv[R][8], nd[R][8], ng[R][8], nrs = 0.f;
     if (row + stride < p.rows) load_row(row + stride, nv, nd, ng, nrs);
-    float dot = 0.f;
+    float dot = 0.f, sgv[R][8];   // sigmoid(g), formed once per element
 #pragma unroll
     for (int j = 0; j < R; ++j) {
       if (lane * 8 + 512 * j < D) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float dn = d[j][e] * wv[j][e];
-          if (g) dn *= gv[j][e] * sigmoidf(gv[j][e]);
+          sgv[j][e] = g ? sigmoidf(gv[j][e]) : 1.f;
+          if (g) dn *= gv[j][e] * sgv[j][e];
           dot += dn * v[j][e] * rstd;
         }
       }
@@ -174,7 +180,7 @@ __device__ __forceinline__ void norm_gate_bwd_rows(const NormGateArgs& p, float 
           const float n = v[j][e] * rstd;
           float s = 1.f;
           if (g) {
-            const float sg = sigmoidf(gv[j][e]);
+            const float sg = sgv[j][e];
             s = gv[j][e] * sg;
             og[e] = d[j][e] * n * wv[j][e] * sg * (1.f + gv[j][e] * (1.f - sg));
           }
