@@ -45,7 +45,9 @@ __device__ __forceinline__ void st8<bf16>(bf16* p, const float (&x)[8]) {
                                             pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
 }
 
-__device__ __forceinline__ float sig(float x) { return 1.f / (1.f + __expf(-x)); }
+// 1 / (1 + e^{-x}) with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE
+// division's scale / fix-up sequence; saturates to 0 / 1.
+__device__ __forceinline__ float sig(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 struct ScPos {
   int bos, eos, t, c0;
