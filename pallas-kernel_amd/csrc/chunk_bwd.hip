@@ -219,7 +219,8 @@ __global__ __launch_bounds__(256) void chunk_bwd_dqkg_kernel(BwdArgs p) {
     Pair<T>::ld(sKr + row * P64 + c_0, k0[rr], k1[rr]);
     const float e0 = gexp<T>(d0[rr]), e1 = gexp<T>(d1[rr]);
     Pair<T>::st(sQg + row * P64 + c_0, q0[rr] * e0, q1[rr] * e1);
-    Pair<T>::st(sKg + row * P64 + c_0, k0[rr] / e0, k1[rr] / e1);
+    Pair<T>::st(sKg + row * P64 + c_0, gdiv<T>(k0[rr], d0[rr], e0),
+                gdiv<T>(k1[rr], d1[rr], e1));
   }
   if (seg == 0) {
     sR[c_0] = p.scale * gexp<T>(r0);
@@ -350,9 +351,9 @@ __global__ __launch_bounds__(256) void chunk_bwd_dqkg_kernel(BwdArgs p) {
     const float2 xk = *reinterpret_cast<const float2*>(XK + row * PX + c_0);
     const float2 xm = *reinterpret_cast<const float2*>(XM + row * PX + c_0);
     const float vq0 = ep0 * xq.x, vq1 = ep1 * xq.y;
-    const float vk0 = xk.x / ep0, vk1 = xk.y / ep1;
-    dki0 += k0[rr] * (xm.x / ep0);
-    dki1 += k1[rr] * (xm.y / ep1);
+    const float vk0 = gdiv<T>(xk.x, d0[rr], ep0), vk1 = gdiv<T>(xk.y, d1[rr], ep1);
+    dki0 += k0[rr] * gdiv<T>(xm.x, d0[rr], ep0);
+    dki1 += k1[rr] * gdiv<T>(xm.y, d1[rr], ep1);
     s0 += q0[rr] * vq0 - k0[rr] * vk0;
     s1 += q1[rr] * vq1 - k1[rr] * vk1;
     dgr0[rr] = s0;
@@ -527,7 +528,8 @@ __global__ __launch_bounds__(256) void chunk_bwd_dv_kernel(BwdArgs p) {
         Pair<T>::ld(sKr + row * P64 + c_0, ka, kb2);
         const float e0 = gexp<T>(d0[rr]), e1 = gexp<T>(d1[rr]);
         Pair<T>::st(sQg + row * P64 + c_0, qa * e0, qb * e1);
-        Pair<T>::st(sKg + row * P64 + c_0, ka / e0, kb2 / e1);
+        Pair<T>::st(sKg + row * P64 + c_0, gdiv<T>(ka, d0[rr], e0),
+                    gdiv<T>(kb2, d1[rr], e1));
       }
       if (seg == 0) {
         sEg[c_0] = gexp<T>(gam0 - r0);

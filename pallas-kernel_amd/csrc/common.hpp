@@ -103,6 +103,20 @@ __device__ __forceinline__ float gexp<bf16>(float x) {
   return __expf(x);
 }
 
+// x / e given e = gexp<T>(d): float inputs divide (the float32 path keeps the IEEE
+// division); bf16 inputs multiply by e^{-d} instead (a hardware exp in place of the
+// division's scale / fix-up sequence)
+template <typename T>
+__device__ __forceinline__ float gdiv(float x, float d, float e);
+template <>
+__device__ __forceinline__ float gdiv<float>(float x, float, float e) {
+  return x / e;
+}
+template <>
+__device__ __forceinline__ float gdiv<bf16>(float x, float d, float) {
+  return x * __expf(-d);
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). Remap the
 // hardware block id so that consecutive logical blocks land on the same XCD.
 __device__ __forceinline__ int xcd_remap(int L, int total) {
