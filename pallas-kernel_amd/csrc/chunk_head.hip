@@ -1968,7 +1968,9 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
     }
     if constexpr (PRE) {
       // the h residual (the state entering the chunk, bf16) as whole rows of h' in LDS: the
-      // accumulators' 8-byte pieces (32 bytes of a row a store) cost ~40 % of the chunk at C5
+      // accumulators' 8-byte pieces (32 bytes of a row a store) cost ~40 % of the chunk at C5.
+      // Plain stores: nontemporal ones measured 7 % slower for this kernel at C5 (303 against
+      // 282 us), though the o rows and the scans' states gain from them.
       if (hout) {
         bf16* hb = hout + ((long)(sg.c0 + ci) * H + hh) * KV + cv;
         constexpr int PR = VP / 8;   // 16-byte pieces of a row
@@ -1976,7 +1978,7 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
         for (int j = 0; j < KP * PR / HNT; ++j) {
           const int pc = tid + HNT * j, r = pc / PR, c8 = (pc % PR) * 8;
           const uint4 x = *reinterpret_cast<const uint4*>(sHk + LT<VP>::off(r, c8));
-          if (r < K && c8 < Vw) st16_sel(hb, ((uint32_t)r * (uint32_t)V + c8) * 2u, x, ntv);
+          if (r < K && c8 < Vw) st16(hb, ((uint32_t)r * (uint32_t)V + c8) * 2u, x);
         }
       }
     }
