@@ -1694,11 +1694,13 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   auto o_out = [&](int step) {
     static_assert(!PRE || HC * VP / 8 == HNT, "one piece a thread");
     const int t0s = sg.bos + (sg.cb + step) * HC, lens = min(HC, sg.eos - t0s);
-    const int r = tid / (VP / 8), c8 = 8 * (tid % (VP / 8));
+    // lanes past the chunk or the tile store the last row / piece again (the same bytes to the
+    // same address), so that no per-lane branch surrounds the stores (with it and the h
+    // residual's: 282 against 271 us for the kernel at C5). Vw and K are multiples of 8 here.
+    const int r = min(tid / (VP / 8), lens - 1), c8 = min(8 * (tid % (VP / 8)), Vw - 8);
     const uint4 x = *reinterpret_cast<const uint4*>(sOst + r * kStgPitch + c8);
-    if (r < lens && c8 < Vw)
-      st16_sel(o + (long)t0s * rsV + (long)hh * V + cv, ((uint32_t)r * (uint32_t)rsV + c8) * 2u,
-               x, ntv);
+    st16_sel(o + (long)t0s * rsV + (long)hh * V + cv, ((uint32_t)r * (uint32_t)rsV + c8) * 2u, x,
+             ntv);
   };
   // R: this chunk's registers; Rn: the next chunk's (SPLIT: its q, k and v issued here)
   auto body = [&](int step, Regs& R, Regs& Rn) {
@@ -1970,15 +1972,16 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
       // the h residual (the state entering the chunk, bf16) as whole rows of h' in LDS: the
       // accumulators' 8-byte pieces (32 bytes of a row a store) cost ~40 % of the chunk at C5.
       // Plain stores: nontemporal ones measured 7 % slower for this kernel at C5 (303 against
-      // 282 us), though the o rows and the scans' states gain from them.
-      if (hout) {
+      // 282 us), though the o rows and the scans' states gain from them. Lanes past the head or
+      // the tile store the last row / piece again, as in o_out: no branch around the stores.
+      if constexpr (HO) {
         bf16* hb = hout + ((long)(sg.c0 + ci) * H + hh) * KV + cv;
         constexpr int PR = VP / 8;   // 16-byte pieces of a row
 #pragma unroll
         for (int j = 0; j < KP * PR / HNT; ++j) {
-          const int pc = tid + HNT * j, r = pc / PR, c8 = (pc % PR) * 8;
+          const int pc = tid + HNT * j, r = min(pc / PR, K - 1), c8 = min((pc % PR) * 8, Vw - 8);
           const uint4 x = *reinterpret_cast<const uint4*>(sHk + LT<VP>::off(r, c8));
-          if (r < K && c8 < Vw) st16(hb, ((uint32_t)r * (uint32_t)V + c8) * 2u, x);
+          st16(hb, ((uint32_t)r * (uint32_t)V + c8) * 2u, x);
         }
       }
     }
