@@ -2012,14 +2012,11 @@ __global__ __launch_bounds__(HNT) void head_fwd_kernel(HeadFwdArgs p) {
   } else if (nsteps > 0) {
     Regs R0;
     issue(0, R0);
-    if constexpr (PRE) {
-      // the first chunk peeled: the loop is then entered, like each of its trips, right
-      // after a chunk's stores, so the wait for a chunk's loads need not cover them
-      body(0, R0, R0);
-      for (int step = 1; step < nsteps; ++step) body(step, R0, R0);
-    } else {
-      for (int step = 0; step < nsteps; ++step) body(step, R0, R0);
-    }
+    // the first chunk's loads waited for here (as in the backward): the loop's wait for a
+    // chunk's loads, sized for this entry, would otherwise also wait on every later trip for
+    // the previous chunk's h residual stores
+    if constexpr (PRE) vm_wait_all();
+    for (int step = 0; step < nsteps; ++step) body(step, R0, R0);
     if constexpr (PRE) {
       __syncthreads();   // the last chunk's output tile in LDS
       o_out(nsteps - 1);
